@@ -1,0 +1,183 @@
+/*
+ * ttsplat.h -- C ABI of the MI355X (gfx950) poly-splat / WSR 3DGS hot path.
+ *
+ * Every entry point takes device pointers allocated by the caller, plain sizes and a
+ * hipStream_t; it only enqueues work on that stream (no allocation, no synchronisation),
+ * so every call can be captured into a hipGraph.  Return value: 0 on success, a negative
+ * TTS_E* domain code for bad arguments (nothing is launched), or a positive hipError_t from
+ * the launch.  tts_strerror() names a code.
+ *
+ * The reference (tt-splat) is pure Python; each entry point below replaces the Python/ttnn
+ * function cited beside it (paths relative to the reference checkout).
+ *
+ * Shared layouts
+ *   params [G,14] fp32 row-major, columns mx,my,mz, qw,qx,qy,qz, lx,ly,lz, cr,cg,cb, op
+ *                 (tools/resident_traced.py:91, the fused-Adam [G,14] block :233-235)
+ *   camera [16]   fp32: R_v row-major (9), t_v (3), fx, fy, cx, cy  (world->camera, OpenCV)
+ *   proj   [G,12] fp32 per-gaussian record written by tts_geom_fwd:
+ *                 0 mu_x, 1 mu_y, 2 a, 3 b, 4 c (conic = Sigma2d^-1), 5 depth,
+ *                 6..8 color_o = keep*sigmoid(op)*color, 9 o_col = keep*sigmoid(op),
+ *                 10 sigmoid(op), 11 zero
+ *   keep   [G]    uint8, depth > near
+ *   bins   idx[T,K] int32 (0 in empty slots), valid[T,K] uint8; tiles row-major, T = (H/S)*(W/S)
+ *   image  [H,W,3] fp32 row-major; den [H,W] fp32 (WSR denominator sum(w*oc) + w_b)
+ *   bg     [4]    fp32: w_b (already softplus'ed), c_b r, g, b
+ *   grad9  [G,9]  fp32 per-gaussian gradient of (a, b, c, mu_x, mu_y, col_o r,g,b, o_col)
+ *                 (the scatter layout of tools/resident_traced.py:383-395)
+ *   theta  [T,6,K] fp32 monomial-major theta_u, col [T,K,3], oc [T,K] (tools/m4_train_binned.py:130-143)
+ */
+#ifndef TTSPLAT_H
+#define TTSPLAT_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTS_OK 0
+#define TTS_EINVAL (-1)     /* null pointer or non-positive size */
+#define TTS_ETILE (-2)      /* S not in {16,32}, or H/W not a multiple of S */
+#define TTS_EK (-3)         /* K outside [1, 512] */
+#define TTS_EWORKSPACE (-4) /* workspace missing or too small */
+#define TTS_ESPAN (-5)      /* quantised-distance span outside [1, 8192] */
+#define TTS_EG (-6)         /* G above 2^30 */
+#define TTS_ERADIUS (-7)    /* stencil radius other than 1 */
+
+/* Library version, (major << 16) | minor. */
+int tts_version(void);
+
+/* Static description of a return code. */
+const char* tts_strerror(int code);
+
+/* ---------------------------------------------------------------- geometry ---------- */
+
+/* Geometry forward + activations for one camera.
+ * Replaces spike/geometry.py:28-57 (project_ewa, with quat_to_rotmat :10-19 and cov3d
+ * :22-25 on exp(log_scales)), spike/forward.py:69-71 (color_from_dc) and the activations of
+ * tools/m4_train_binned.py:194-202; device form tools/geom_device.py:44-94.
+ * Writes proj[G,12] and keep[G].  near = 0.2, blur = 0.3 in the reference. */
+int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, float blur,
+                 float* proj, uint8_t* keep, hipStream_t stream);
+
+/* Geometry + activation backward: grad9[G,9] -> gparams[G,14] (overwritten).
+ * Replaces tools/geom_bwd.py:67-152 (bwd) and the activation part of
+ * tools/operands_manual.py:432-460 (bwd_manual); device form tools/geom_device.py:106-198,
+ * tools/resident_traced.py:397-427. */
+int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, float blur,
+                 const float* grad9, float* gparams, hipStream_t stream);
+
+/* ------------------------------------------------------------------ binning --------- */
+
+/* Bytes of zero-initialised scratch tts_assign_bins needs for G gaussians on an H x W image
+ * with S x S tiles.  The caller zeroes it once; every successful call leaves it zeroed. */
+size_t tts_bin_workspace_bytes(int G, int H, int W, int S);
+
+/* Fixed-budget spatial-hash binning, R = 1: each gaussian is hashed to one S x S cell, offered
+ * to the 3x3 tiles around it, and each tile keeps the K candidates nearest its centre.
+ * Replaces tools/m4_train_binned.py:75-127 (assign_bins) and the dense device binning of
+ * tools/bin_device.py:140-187.  mu2d[g*mu_stride + {0,1}], keep[g*keep_stride].
+ * Order inside a tile is by (clamp(int64(dist2), 0, span-1), stencil index j, gaussian id),
+ * i.e. the reference's sort key with ties in its concatenation order; span = 2048 at S = 16.
+ * Writes idx[T,K], valid[T,K]; count[T] (kept per tile) and ncand[T] (candidates per tile)
+ * are optional (may be NULL). */
+int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
+                    int G, int H, int W, int S, int R, int K, int span,
+                    int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand,
+                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------- splat ---------- */
+
+/* Per-tile gather + theta_u build: proj + bins -> theta[T,6,K], col[T,K,3], oc[T,K]
+ * (zero in invalid slots).  Replaces tools/m4_train_binned.py:130-143 (theta_u_gathered) with
+ * the gathers of :207-211 (_operands); device form tools/traced_fwd.py:63-82.  k = poly cutoff. */
+int tts_theta_u_gathered(const float* proj, const int32_t* idx, const uint8_t* valid,
+                         int H, int W, int S, int K, float k,
+                         float* theta, float* col, float* oc, hipStream_t stream);
+
+/* Fused binned splat forward from the per-gaussian records: gather, tile-local theta_u,
+ * u = Phi.theta_u, w = relu(u)^2, C = (sum w col + w_b c_b) / (sum w oc + w_b), written
+ * straight into the image.  Replaces tools/bh_views.py:65-71 on _operands
+ * (tools/m4_train_binned.py:189-212) and the device chain tools/resident_traced.py:358-370.
+ * den may be NULL (it is needed by tts_splat_bwd). */
+int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
+                  int H, int W, int S, int K, float k, const float* bg,
+                  float* image, float* den, hipStream_t stream);
+
+/* Splat forward from pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K].
+ * Replaces _DevRenderBinned.forward, tools/m4_train_binned.py:154-166 (ops :146-151). */
+int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc,
+                        int H, int W, int S, int K, const float* bg,
+                        float* image, float* den, hipStream_t stream);
+
+/* Fused binned splat backward: given dL/dimage, recompute w per (pixel, slot), contract over
+ * the tile's pixels per slot, apply the theta backward and add each slot's gradient into
+ * grad9[G,9] (atomics; grad9 must be zeroed by the caller).  gwb (dL/dw_b, accumulated) may
+ * be NULL.  Replaces WSRPolySplatHot.backward (spike/backward.py:42-58), render_bwd +
+ * theta_bwd (tools/resident_traced.py:60-88) and the slot->gaussian scatter
+ * (:383-395 device, :718-727 host). */
+int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
+                  int H, int W, int S, int K, float k, const float* bg,
+                  const float* image, const float* den, const float* gimage,
+                  float* grad9, float* gwb, hipStream_t stream);
+
+/* Splat backward on pre-gathered operands: writes per-slot gtheta[T,6,K], gcol[T,K,3],
+ * goc[T,K] (overwritten) and accumulates gwb.  Replaces _DevRenderBinned.backward,
+ * tools/m4_train_binned.py:168-186. */
+int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc,
+                        int H, int W, int S, int K, const float* bg,
+                        const float* image, const float* den, const float* gimage,
+                        float* gtheta, float* gcol, float* goc, float* gwb,
+                        hipStream_t stream);
+
+/* -------------------------------------------------------------------- loss ---------- */
+
+/* Bytes of scratch tts_loss_grad needs for an H x W image (no initialisation needed). */
+size_t tts_loss_workspace_bytes(int H, int W);
+
+/* Number of fp32 partial sums tts_loss_grad writes.  The first *n_ssim are sums of the SSIM
+ * map, the rest are sums of |x-y|:
+ *   loss = (1-l) * sum|x-y| / (3HW) + l * (1 - sumS / (3 (H-10)(W-10))). */
+int tts_loss_partials_count(int H, int W, int* n_ssim);
+
+/* dL/dimage of L = (1-lambda)*mean|x-y| + lambda*(1 - mean SSIM(clamp(x,0,1), clamp(y,0,1))),
+ * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4.
+ * Replaces spike/metrics.py:26-28 (loss_fn, differentiated by autograd), the manual gradient
+ * tools/loss_manual.py:76-103 and the device loss tools/resident_traced.py:431-464.
+ * image, target, gimage: [H,W,3]; H, W >= 11.  partials may be NULL. */
+int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
+                  float* gimage, float* partials, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
+/* -------------------------------------------------------------------- adam ---------- */
+
+/* Advance the device step counter (int32, step[0] += 1) and derive the bias corrections the
+ * following tts_adam / tts_geom_bwd_adam read.  step must point at 4 int32 words (the last
+ * three hold the derived fp32 factors).  Replaces the host bias-correction of
+ * tools/resident_traced.py:478-481. */
+int tts_adam_advance(int32_t* step, float beta1, float beta2, hipStream_t stream);
+
+/* Adam over n = G*14 fp32 values with a per-column learning rate lr[14]; reads the factors
+ * tts_adam_advance stored.  Replaces adam_fused, tools/resident_traced.py:478-490
+ * (and torch.optim.Adam in spike/train.py:19). */
+int tts_adam(float* params, float* m, float* v, const float* grad, const float* lr, int G,
+             const int32_t* step, float beta1, float beta2, float eps, hipStream_t stream);
+
+/* Fused geometry backward + Adam for one step: grad9 -> 14 gradients -> Adam update of
+ * params/m/v; grad9 is zeroed afterwards for the next step's atomics.  gparams (the 14
+ * gradients) may be NULL.  Replaces tools/resident_traced.py:397-427 + :739-740. */
+int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, float blur,
+                      float* grad9, float* gparams, float* m, float* v, const float* lr,
+                      const int32_t* step, float beta1, float beta2, float eps,
+                      hipStream_t stream);
+
+/* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */
+int tts_zero(float* buf, int64_t n, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TTSPLAT_H */

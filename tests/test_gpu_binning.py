@@ -1,0 +1,128 @@
+"""GPU binning vs the oracle: bit-exact.
+
+Contract (tools/m4_train_binned.py:75-127):
+  1. GPU == the stable-order oracle, bit for bit, on every configuration.
+  2. GPU == the reference order (torch default argsort) bit for bit once the pair count is
+     >= 32768 (the reference sort is the stable radix sort there): c3, c4.
+  3. Below that (c1, ~17k pairs), equal in every tile without a quantised-distance tie; tie
+     tiles are counted.
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import bins_equal_report, config_inputs
+from oracle import binning as obin
+from ttsplat import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_bins(cfg, P, cam, K=None):
+    K = cfg.K if K is None else K
+    proj, keep = kernels.geom_fwd(P.cuda(), cam.device_block("cuda"))
+    idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, K,
+                                                   cfg.span)
+    torch.cuda.synchronize()
+    return proj[:, 0:2].cpu(), keep.cpu().bool(), idx.cpu(), valid.cpu(), count.cpu(), ncand.cpu()
+
+
+@pytest.mark.parametrize("name", ["c1_ref", "c1", "c3", "c4"])
+def test_bins_bitexact_stable(name):
+    cfg, P, cam = config_inputs(name)
+    print(f"[bins] {name} G={cfg.G} {cfg.H}x{cfg.W} S={cfg.S} K={cfg.K}", flush=True)
+    mu, keep, idx, valid, count, ncand = gpu_bins(cfg, P, cam)
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ridx, rvalid, rncand = obin.assign_bins(mu, keep, tmap, 1, cfg.K, cfg.span, stable=True,
+                                            return_stats=True)
+    ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+    assert ndiff == 0, f"{ndiff} tiles differ, first {tiles[:8].tolist()}"
+    assert torch.equal(ncand.long(), rncand)
+    assert torch.equal(count.long(), rncand.clamp(max=cfg.K))
+    print(f"[bins] {name}: pairs={int(rncand.sum())} overflow tiles={int((rncand > cfg.K).sum())}")
+
+
+@pytest.mark.parametrize("name", ["c3", "c4"])
+def test_bins_match_reference_order(name):
+    cfg, P, cam = config_inputs(name)
+    mu, keep, idx, valid, _, ncand = gpu_bins(cfg, P, cam)
+    assert int(ncand.sum()) >= obin.RADIX_STABLE_MIN_PAIRS
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ridx, rvalid = obin.assign_bins(mu, keep, tmap, 1, cfg.K, cfg.span, stable=False)
+    ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+    assert ndiff == 0, f"{ndiff} tiles differ from the reference order, first {tiles[:8].tolist()}"
+
+
+def test_bins_c1_reference_order_outside_tie_tiles():
+    cfg, P, cam = config_inputs("c1_ref")
+    mu, keep, idx, valid, _, ncand = gpu_bins(cfg, P, cam)
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ridx, rvalid = obin.assign_bins(mu, keep, tmap, 1, cfg.K, cfg.span, stable=False)
+    ties = set(obin.tie_tiles(mu, keep, tmap, 1, cfg.span).tolist())
+    _, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+    outside = [t for t in tiles.tolist() if t not in ties]
+    assert not outside, f"tiles without a key tie differ: {outside[:8]}"
+    # every tile keeps the same gaussian SET unless a tie straddles slot K
+    print(f"[bins] c1_ref pairs={int(ncand.sum())} tie tiles={len(ties)} "
+          f"order-differing tiles={len(tiles)}")
+
+
+def _edge_mu(G, H, W, seed):
+    g = torch.Generator().manual_seed(seed)
+    mu = torch.empty(G, 2)
+    mu[:, 0] = torch.rand(G, generator=g) * (W + 200) - 100
+    mu[:, 1] = torch.rand(G, generator=g) * (H + 200) - 100
+    n = G // 8
+    mu[:n] = torch.tensor([37.25, 61.5])                  # a pile of exact duplicates
+    mu[n:2 * n, 0] = torch.randint(0, W // 16 + 1, (n,), generator=g).float() * 16  # on tile edges
+    mu[n:2 * n, 1] = torch.randint(0, H // 16 + 1, (n,), generator=g).float() * 16
+    mu[2 * n] = torch.tensor([math.nan, 5.0])
+    mu[2 * n + 1] = torch.tensor([math.inf, -math.inf])
+    mu[2 * n + 2] = torch.tensor([1e30, -1e30])
+    mu[2 * n + 3] = torch.tensor([-0.0, 1e-40])
+    keep = torch.rand(G, generator=g) > 0.1
+    return mu, keep
+
+
+@pytest.mark.parametrize("S,K,G", [(16, 128, 4000), (16, 1, 300), (32, 64, 5000), (16, 512, 20000)])
+def test_bins_edge_cases(S, K, G):
+    H, W = 96, 160
+    mu, keep = _edge_mu(G, H, W, seed=S + K)
+    span = 2048 if S == 16 else 8192
+    idx, valid, count, ncand = kernels.assign_bins(mu.cuda().contiguous(),
+                                                   keep.to(torch.uint8).cuda(), H, W, S, K, span)
+    tmap = obin.TileMap(H, W, S)
+    ridx, rvalid, rncand = obin.assign_bins(mu, keep, tmap, 1, K, span, stable=True,
+                                            return_stats=True)
+    ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+    assert ndiff == 0, f"{ndiff} tiles differ, first {tiles[:8].tolist()}"
+    assert torch.equal(ncand.cpu().long(), rncand)
+
+
+def test_bins_empty_and_all_culled():
+    H, W, S, K = 64, 64, 16, 32
+    mu = torch.rand(100, 2, device="cuda") * 64
+    keep = torch.zeros(100, dtype=torch.uint8, device="cuda")
+    idx, valid, count, ncand = kernels.assign_bins(mu, keep, H, W, S, K, 2048)
+    assert int(valid.sum()) == 0 and int(idx.abs().sum()) == 0 and int(ncand.sum()) == 0
+    mu0 = torch.empty(0, 2, device="cuda")
+    keep0 = torch.empty(0, dtype=torch.uint8, device="cuda")
+    idx, valid, count, ncand = kernels.assign_bins(mu0, keep0, H, W, S, K, 2048)
+    assert int(valid.sum()) == 0
+
+
+def test_bins_repeatable():
+    cfg, P, cam = config_inputs("c4")
+    a = gpu_bins(cfg, P, cam)
+    b = gpu_bins(cfg, P, cam)
+    assert torch.equal(a[2], b[2]) and torch.equal(a[3], b[3])
+
+
+def test_bins_bad_arguments_raise():
+    mu = torch.rand(10, 2, device="cuda")
+    keep = torch.ones(10, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ValueError):
+        kernels.assign_bins(mu, keep, 100, 64, 16, 32, 2048)     # H not a multiple of S
+    with pytest.raises(Exception):
+        kernels.assign_bins(mu, keep, 64, 64, 16, 4096, 2048)    # K too large

@@ -1,0 +1,127 @@
+"""GPU splat forward/backward vs the oracle.
+
+Forward: image within 1e-4 max-abs (fp32).  Backward: parameter gradients within 1e-3 relative
+L2 of torch autograd through the oracle's binned render (tools/bh_views.py:65-71 on _operands,
+spike/backward.py).  The oracle runs on the GPU's own bins so both sides see the same lists.
+"""
+import pytest
+import torch
+
+from helpers import cam_dict, config_inputs, max_abs, rel_l2
+from oracle import binning as obin
+from oracle import splat as osplat
+from ttsplat import binned, kernels
+
+pytestmark = pytest.mark.gpu
+
+GROUPS = {"means": slice(0, 3), "quats": slice(3, 7), "scales": slice(7, 10),
+          "color": slice(10, 13), "opacity": slice(13, 14)}
+
+
+def setup(name, G=None, k=None):
+    cfg, P, cam = config_inputs(name, G=G)
+    k = cfg.k if k is None else k
+    camera = cam.device_block("cuda")
+    proj, keep = kernels.geom_fwd(P.cuda(), camera)
+    idx, valid, _, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, cfg.K,
+                                           cfg.span)
+    bg = torch.tensor([float(torch.nn.functional.softplus(torch.tensor(-3.0))), 1.0, 1.0, 1.0],
+                      device="cuda")
+    bins = (idx.cpu().long(), valid.cpu().bool())
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    return cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k
+
+
+@pytest.mark.parametrize("name,k", [("c1_ref", 4.0), ("c1", 9.0), ("c1_ref", 9.0), ("c3", 4.0)])
+def test_splat_fwd_parity(name, k):
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup(name, k=k)
+    print(f"[fwd] {name} k={k}", flush=True)
+    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
+    ref, ex = osplat.render_binned(P, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins,
+                                   return_all=True)
+    err = max_abs(img, ref)
+    print(f"[fwd] {name} k={k} max|err|={err:.3e}")
+    assert err <= 1e-4
+    assert max_abs(den, ex["den"]) <= 1e-4 * float(ex["den"].abs().max())
+
+
+def test_theta_gather_matches_operands():
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c1_ref")
+    th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, k)
+    rth, rcol, roc, _, _ = osplat.operands(P, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
+    assert max_abs(col, rcol) <= 1e-6
+    assert max_abs(oc, roc[..., 0]) <= 1e-6
+    # theta entries scale with the tile-local offset; compare relative to their magnitude
+    assert rel_l2(th, rth) <= 1e-5
+
+
+@pytest.mark.parametrize("name,k", [("c1_ref", 4.0), ("c1", 9.0), ("c3", 4.0)])
+def test_splat_bwd_param_grads(name, k):
+    """d(sum R*img)/dparams, GPU fused backward + geometry backward vs oracle autograd."""
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup(name, k=k)
+    print(f"[bwd] {name} k={k}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    R = torch.randn(cfg.H, cfg.W, 3, generator=g)
+    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
+    grad9 = torch.zeros(cfg.G, 9, device="cuda")
+    gwb = torch.zeros(1, device="cuda")
+    kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R.cuda(), grad9,
+                      gwb)
+    gP = kernels.geom_bwd(P.cuda(), camera, grad9).cpu()
+    Pr = P.clone().requires_grad_(True)
+    ref = osplat.render_binned(Pr, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
+    (ref * R).sum().backward()
+    for gname, sl in GROUPS.items():
+        e = rel_l2(gP[:, sl], Pr.grad[:, sl])
+        print(f"[bwd] {name} d{gname}: rel L2 {e:.2e}")
+        assert e <= 1e-3, gname
+    # dL/dw_b: autograd through the oracle with w_b as a leaf
+    wb = torch.tensor(float(bg[0]), dtype=torch.float64, requires_grad=True)
+    th, col, oc, _, _ = osplat.operands(P.double(), cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
+    C, _ = osplat.splat_tiles(th, col, oc, tmap.Phi.double(), wb, torch.ones(3, dtype=torch.float64))
+    (osplat.tiles_to_image(C, tmap) * R.double()).sum().backward()
+    assert abs(float(gwb) - float(wb.grad)) <= 1e-3 * abs(float(wb.grad)) + 1e-4
+
+
+def test_dev_render_binned_theta_api():
+    """DevRenderBinned (pre-gathered operands, the _DevRenderBinned drop-in) vs oracle autograd."""
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c1_ref")
+    th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, k)
+    th = th.clone().requires_grad_(True)
+    col = col.clone().requires_grad_(True)
+    oc1 = oc[..., None].clone().requires_grad_(True)
+    wb = bg[0].clone().requires_grad_(True)
+    img = binned.DevRenderBinned.apply(th, col, oc1, wb, tmap.Phi, tmap.gidx, bg[1:], cfg.H, cfg.W)
+    R = torch.randn(cfg.H, cfg.W, 3, generator=torch.Generator().manual_seed(3))
+    (img * R.cuda()).sum().backward()
+    # oracle
+    tr = th.detach().cpu().double().requires_grad_(True)
+    cr = col.detach().cpu().double().requires_grad_(True)
+    orr = oc1.detach().cpu().double().requires_grad_(True)
+    wr = torch.tensor(float(bg[0]), dtype=torch.float64, requires_grad=True)
+    C, _ = osplat.splat_tiles(tr, cr, orr, tmap.Phi.double(), wr, torch.ones(3, dtype=torch.float64))
+    ref = osplat.tiles_to_image(C, tmap)
+    assert max_abs(img, ref) <= 1e-4
+    (ref * R.double()).sum().backward()
+    assert rel_l2(th.grad, tr.grad) <= 1e-3
+    assert rel_l2(col.grad, cr.grad) <= 1e-3
+    assert rel_l2(oc1.grad, orr.grad) <= 1e-3
+    assert abs(float(wb.grad) - float(wr.grad)) <= 1e-3 * abs(float(wr.grad)) + 1e-4
+
+
+def test_render_binned_device_autograd():
+    """render_binned_device (whole chain as one autograd op) vs oracle autograd."""
+    from ttsplat.model import GaussianModel
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap_o, k = setup("c1_ref")
+    m = GaussianModel(P.cuda())
+    m.params.requires_grad_(True)
+    tmap = binned.TileMap(cfg.H, cfg.W, cfg.S)
+    img, gbins = binned.render_binned_device(m, cam, tmap, K=cfg.K, return_bins=True)
+    R = torch.randn(cfg.H, cfg.W, 3, generator=torch.Generator().manual_seed(5))
+    (img * R.cuda()).sum().backward()
+    Pr = P.clone().requires_grad_(True)
+    ref = osplat.render_binned(Pr, cam_dict(cam), tmap_o, K=cfg.K, k=k,
+                               bins=(gbins[0].cpu(), gbins[1].cpu()))
+    assert max_abs(img, ref) <= 1e-4
+    (ref * R).sum().backward()
+    assert rel_l2(m.params.grad, Pr.grad) <= 1e-3

@@ -1,0 +1,381 @@
+// Per-gaussian kernels: EWA projection + activations, their backward, and Adam.
+// One thread per gaussian; all fp32.  The math follows spike/geometry.py:10-57,
+// spike/forward.py:69-71 and tools/m4_train_binned.py:194-202; the backward is the chain rule
+// of that forward (derived below, checked against torch autograd of the CPU oracle).
+
+#include <math.h>
+
+#include "tts_common.h"
+
+namespace tts {
+
+// Forward intermediates kept for the backward (all recomputed from params, never stored).
+struct GeoState {
+  float qn[4];       // normalised quaternion w,x,y,z
+  float qnorm;       // |q| before the 1e-12 clamp
+  float qdiv;        // max(|q|, 1e-12)
+  float M[3][3];     // R_v * R(q)
+  float s2[3];       // exp(log_scale)^2
+  float SC[3][3];    // camera-space covariance M diag(s2) M^T
+  float mc[3];       // camera-space mean
+  float z;           // max(depth, near)
+  bool zmask;        // depth >= near (gradient passes the clamp)
+  bool keep;         // depth > near
+  float J00, J02, J11, J12;
+  float s00, s01, s11;
+  float det_inv;     // 1 / max(det, 1e-12)
+  bool dmask;        // det >= 1e-12
+  float mux, muy, a, b, c;
+  float color[3];    // max(0.5 + C0*dc, 0)
+  float o;           // sigmoid(op)
+};
+
+__device__ __forceinline__ void geo_forward(const float* __restrict__ p, const Camera& cam,
+                                            float near_z, float blur, GeoState& s) {
+  const float qw = p[3], qx = p[4], qy = p[5], qz = p[6];
+  s.qnorm = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
+  s.qdiv = fmaxf(s.qnorm, 1e-12f);
+  const float w = qw / s.qdiv, x = qx / s.qdiv, y = qy / s.qdiv, z = qz / s.qdiv;
+  s.qn[0] = w; s.qn[1] = x; s.qn[2] = y; s.qn[3] = z;
+  float R[3][3];
+  R[0][0] = 1.f - 2.f * (y * y + z * z); R[0][1] = 2.f * (x * y - w * z); R[0][2] = 2.f * (x * z + w * y);
+  R[1][0] = 2.f * (x * y + w * z); R[1][1] = 1.f - 2.f * (x * x + z * z); R[1][2] = 2.f * (y * z - w * x);
+  R[2][0] = 2.f * (x * z - w * y); R[2][1] = 2.f * (y * z + w * x); R[2][2] = 1.f - 2.f * (x * x + y * y);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const float sc = expf(p[7 + i]);
+    s.s2[i] = sc * sc;
+  }
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      s.M[i][k] = cam.R[3 * i + 0] * R[0][k] + cam.R[3 * i + 1] * R[1][k] + cam.R[3 * i + 2] * R[2][k];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int l = 0; l < 3; ++l)
+      s.SC[i][l] = s.M[i][0] * s.M[l][0] * s.s2[0] + s.M[i][1] * s.M[l][1] * s.s2[1] +
+                   s.M[i][2] * s.M[l][2] * s.s2[2];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    s.mc[i] = cam.R[3 * i + 0] * p[0] + cam.R[3 * i + 1] * p[1] + cam.R[3 * i + 2] * p[2] + cam.t[i];
+  const float depth = s.mc[2];
+  s.keep = depth > near_z;
+  s.zmask = depth >= near_z;
+  s.z = fmaxf(depth, near_z);
+  const float zi = 1.0f / s.z;
+  s.mux = cam.fx * s.mc[0] / s.z + cam.cx;
+  s.muy = cam.fy * s.mc[1] / s.z + cam.cy;
+  s.J00 = cam.fx * zi;
+  s.J11 = cam.fy * zi;
+  s.J02 = -cam.fx * s.mc[0] / (s.z * s.z);
+  s.J12 = -cam.fy * s.mc[1] / (s.z * s.z);
+  s.s00 = s.J00 * s.J00 * s.SC[0][0] + 2.f * s.J00 * s.J02 * s.SC[0][2] + s.J02 * s.J02 * s.SC[2][2] + blur;
+  s.s11 = s.J11 * s.J11 * s.SC[1][1] + 2.f * s.J11 * s.J12 * s.SC[1][2] + s.J12 * s.J12 * s.SC[2][2] + blur;
+  s.s01 = s.J00 * s.J11 * s.SC[0][1] + s.J00 * s.J12 * s.SC[0][2] + s.J02 * s.J11 * s.SC[1][2] +
+          s.J02 * s.J12 * s.SC[2][2];
+  const float det = s.s00 * s.s11 - s.s01 * s.s01;
+  s.dmask = det >= 1e-12f;
+  s.det_inv = 1.0f / fmaxf(det, 1e-12f);
+  s.a = s.s11 * s.det_inv;
+  s.b = -s.s01 * s.det_inv;
+  s.c = s.s00 * s.det_inv;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) s.color[i] = fmaxf(0.5f + kC0 * p[10 + i], 0.0f);
+  s.o = sigmoidf_(p[13]);
+}
+
+// Chain rule of geo_forward.  gin = (ga, gb, gc, gmux, gmuy, gcol_o r,g,b, go_col);
+// gout = the 14 parameter gradients in [G,14] column order.
+__device__ __forceinline__ void geo_backward(const float* __restrict__ p, const Camera& cam,
+                                             const GeoState& s, const float* gin, float* gout) {
+  // conic = (s11, -s01, s00) / det
+  const float di = s.det_inv;
+  float gs11 = gin[0] * di, gs01 = -gin[1] * di, gs00 = gin[2] * di;
+  const float gdi = gin[0] * s.s11 - gin[1] * s.s01 + gin[2] * s.s00;
+  const float gdet = s.dmask ? -gdi * di * di : 0.0f;
+  gs00 += gdet * s.s11;
+  gs11 += gdet * s.s00;
+  gs01 += -2.0f * gdet * s.s01;
+  const float h = 0.5f * gs01;
+  // Sigma2d = J SC J^T with J rows J0 = (J00, 0, J02), J1 = (0, J11, J12):
+  //   dL/dJ = 2 Gs J SC, Gs = [[gs00, h], [h, gs11]];  dL/dSC (symmetrised) = 2 E, E = J^T Gs J.
+  float JSC0[3], JSC1[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    JSC0[k] = s.J00 * s.SC[0][k] + s.J02 * s.SC[2][k];
+    JSC1[k] = s.J11 * s.SC[1][k] + s.J12 * s.SC[2][k];
+  }
+  const float gJ00 = 2.f * (gs00 * JSC0[0] + h * JSC1[0]);
+  const float gJ02 = 2.f * (gs00 * JSC0[2] + h * JSC1[2]);
+  const float gJ11 = 2.f * (h * JSC0[1] + gs11 * JSC1[1]);
+  const float gJ12 = 2.f * (h * JSC0[2] + gs11 * JSC1[2]);
+  float E[3][3];
+  E[0][0] = gs00 * s.J00 * s.J00;
+  E[0][1] = h * s.J00 * s.J11;
+  E[0][2] = gs00 * s.J00 * s.J02 + h * s.J00 * s.J12;
+  E[1][1] = gs11 * s.J11 * s.J11;
+  E[1][2] = gs11 * s.J11 * s.J12 + h * s.J11 * s.J02;
+  E[2][2] = gs00 * s.J02 * s.J02 + gs11 * s.J12 * s.J12 + 2.f * h * s.J02 * s.J12;
+  E[1][0] = E[0][1]; E[2][0] = E[0][2]; E[2][1] = E[1][2];
+  // SC = M diag(s2) M^T:  dL/dM = 2 E M diag(s2);  dL/ds2_m = (M^T E M)_mm
+  float EM[3][3];
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int m = 0; m < 3; ++m) EM[a][m] = E[a][0] * s.M[0][m] + E[a][1] * s.M[1][m] + E[a][2] * s.M[2][m];
+  float gM[3][3], gs2[3];
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    gs2[m] = s.M[0][m] * EM[0][m] + s.M[1][m] * EM[1][m] + s.M[2][m] * EM[2][m];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) gM[a][m] = 2.f * EM[a][m] * s.s2[m];
+  }
+  // M = R_v R  ->  dL/dR = R_v^T gM
+  float gR[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+      gR[i][k] = cam.R[0 * 3 + i] * gM[0][k] + cam.R[1 * 3 + i] * gM[1][k] + cam.R[2 * 3 + i] * gM[2][k];
+  // mean path: mu2d = f * mc_xy / z + c ;  J entries depend on z and mc_xy.
+  const float fx = cam.fx, fy = cam.fy, z = s.z;
+  const float zi = 1.0f / z, zi2 = zi * zi, zi3 = zi2 * zi;
+  const float gmx2 = gin[3], gmy2 = gin[4];
+  const float gmcx = gmx2 * fx * zi - gJ02 * fx * zi2;
+  const float gmcy = gmy2 * fy * zi - gJ12 * fy * zi2;
+  float gz = -gJ00 * fx * zi2 - gJ11 * fy * zi2 + 2.f * gJ02 * fx * s.mc[0] * zi3 +
+             2.f * gJ12 * fy * s.mc[1] * zi3 - gmx2 * fx * s.mc[0] * zi2 - gmy2 * fy * s.mc[1] * zi2;
+  const float gmcz = s.zmask ? gz : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 3; ++j) gout[j] = cam.R[0 * 3 + j] * gmcx + cam.R[1 * 3 + j] * gmcy + cam.R[2 * 3 + j] * gmcz;
+  // rotation from the normalised quaternion
+  const float w = s.qn[0], x = s.qn[1], y = s.qn[2], zq = s.qn[3];
+  const float gw = 2.f * (-zq * gR[0][1] + y * gR[0][2] + zq * gR[1][0] - x * gR[1][2] - y * gR[2][0] + x * gR[2][1]);
+  const float gx = 2.f * (y * gR[0][1] + zq * gR[0][2] + y * gR[1][0] - 2.f * x * gR[1][1] - w * gR[1][2] +
+                          zq * gR[2][0] + w * gR[2][1] - 2.f * x * gR[2][2]);
+  const float gy = 2.f * (-2.f * y * gR[0][0] + x * gR[0][1] + w * gR[0][2] + x * gR[1][0] + zq * gR[1][2] -
+                          w * gR[2][0] + zq * gR[2][1] - 2.f * y * gR[2][2]);
+  const float gzq = 2.f * (-2.f * zq * gR[0][0] - w * gR[0][1] + x * gR[0][2] + w * gR[1][0] -
+                           2.f * zq * gR[1][1] + y * gR[1][2] + x * gR[2][0] + y * gR[2][1]);
+  // q_n = q / max(|q|, 1e-12)
+  const float inv = 1.0f / s.qdiv;
+  const float dot = (s.qnorm >= 1e-12f) ? (w * gw + x * gx + y * gy + zq * gzq) : 0.0f;
+  gout[3] = (gw - w * dot) * inv;
+  gout[4] = (gx - x * dot) * inv;
+  gout[5] = (gy - y * dot) * inv;
+  gout[6] = (gzq - zq * dot) * inv;
+  // s2 = exp(2 log_scale)
+#pragma unroll
+  for (int m = 0; m < 3; ++m) gout[7 + m] = gs2[m] * 2.f * s.s2[m];
+  // activations: color_o = keo * color, o_col = keo, keo = keep * sigmoid(op)
+  const float keo = s.keep ? s.o : 0.0f;
+  const float gkeo = gin[5] * s.color[0] + gin[6] * s.color[1] + gin[7] * s.color[2] + gin[8];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const bool pass = (0.5f + kC0 * p[10 + c]) >= 0.0f;
+    gout[10 + c] = pass ? gin[5 + c] * keo * kC0 : 0.0f;
+  }
+  gout[13] = s.keep ? gkeo * s.o * (1.0f - s.o) : 0.0f;
+}
+
+__device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
+  Camera c;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) c.R[i] = cam[i];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) c.t[i] = cam[9 + i];
+  c.fx = cam[12]; c.fy = cam[13]; c.cx = cam[14]; c.cy = cam[15];
+  return c;
+}
+
+__global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
+                                                  const float* __restrict__ camera, float near_z,
+                                                  float blur, float* __restrict__ proj,
+                                                  uint8_t* __restrict__ keep) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const Camera cam = load_camera(camera);
+  GeoState s;
+  geo_forward(params + (int64_t)g * 14, cam, near_z, blur, s);
+  const float keo = s.keep ? s.o : 0.0f;
+  float4* out = reinterpret_cast<float4*>(proj + (int64_t)g * 12);
+  out[0] = make_float4(s.mux, s.muy, s.a, s.b);
+  out[1] = make_float4(s.c, s.mc[2], keo * s.color[0], keo * s.color[1]);
+  out[2] = make_float4(keo * s.color[2], keo, s.o, 0.0f);
+  keep[g] = s.keep ? 1 : 0;
+}
+
+__global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ params, int G,
+                                                  const float* __restrict__ camera, float near_z,
+                                                  float blur, const float* __restrict__ grad9,
+                                                  float* __restrict__ gparams) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const Camera cam = load_camera(camera);
+  const float* p = params + (int64_t)g * 14;
+  GeoState s;
+  geo_forward(p, cam, near_z, blur, s);
+  float gin[9], gout[14];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) gin[i] = grad9[(int64_t)g * 9 + i];
+  geo_backward(p, cam, s, gin, gout);
+#pragma unroll
+  for (int i = 0; i < 14; ++i) gparams[(int64_t)g * 14 + i] = gout[i];
+}
+
+// step[0]: int32 step number; step[1..2]: fp32 1/bc1 and 1/sqrt(bc2) for that step.
+__global__ void k_adam_advance(int32_t* step, float b1, float b2) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const int t = step[0] + 1;
+  step[0] = t;
+  const double bc1 = 1.0 - pow((double)b1, (double)t);
+  const double bc2 = 1.0 - pow((double)b2, (double)t);
+  float* f = reinterpret_cast<float*>(step);
+  f[1] = (float)(1.0 / bc1);
+  f[2] = (float)(1.0 / sqrt(bc2));
+}
+
+__device__ __forceinline__ void adam_update(float& p, float& m, float& v, float g, float lr,
+                                            float inv_bc1, float inv_sqrt_bc2, float b1, float b2,
+                                            float eps) {
+  m = b1 * m + (1.0f - b1) * g;
+  v = b2 * v + (1.0f - b2) * g * g;
+  p -= (lr * inv_bc1) * m / (sqrtf(v) * inv_sqrt_bc2 + eps);
+}
+
+__global__ __launch_bounds__(256) void k_adam(float* __restrict__ params, float* __restrict__ m,
+                                              float* __restrict__ v, const float* __restrict__ grad,
+                                              const float* __restrict__ lr, int64_t n,
+                                              const int32_t* __restrict__ step, float b1, float b2,
+                                              float eps) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float* f = reinterpret_cast<const float*>(step);
+  const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
+  float pp = params[i], mm = m[i], vv = v[i];
+  adam_update(pp, mm, vv, grad[i], lr[i % 14], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
+  params[i] = pp;
+  m[i] = mm;
+  v[i] = vv;
+}
+
+__global__ __launch_bounds__(256) void k_geom_bwd_adam(
+    float* __restrict__ params, int G, const float* __restrict__ camera, float near_z, float blur,
+    float* __restrict__ grad9, float* __restrict__ gparams, float* __restrict__ m,
+    float* __restrict__ v, const float* __restrict__ lr, const int32_t* __restrict__ step,
+    float b1, float b2, float eps) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const Camera cam = load_camera(camera);
+  float* p = params + (int64_t)g * 14;
+  float pl[14];
+#pragma unroll
+  for (int i = 0; i < 14; ++i) pl[i] = p[i];
+  GeoState s;
+  geo_forward(pl, cam, near_z, blur, s);
+  float gin[9], gout[14];
+#pragma unroll
+  for (int i = 0; i < 9; ++i) {
+    gin[i] = grad9[(int64_t)g * 9 + i];
+    grad9[(int64_t)g * 9 + i] = 0.0f;
+  }
+  geo_backward(pl, cam, s, gin, gout);
+  const float* f = reinterpret_cast<const float*>(step);
+  const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
+  float* mg = m + (int64_t)g * 14;
+  float* vg = v + (int64_t)g * 14;
+#pragma unroll
+  for (int i = 0; i < 14; ++i) {
+    float mm = mg[i], vv = vg[i];
+    adam_update(pl[i], mm, vv, gout[i], lr[i], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
+    p[i] = pl[i];
+    mg[i] = mm;
+    vg[i] = vv;
+    if (gparams) gparams[(int64_t)g * 14 + i] = gout[i];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) buf[i] = 0.0f;
+}
+
+}  // namespace tts
+
+using namespace tts;
+
+extern "C" {
+
+int tts_version(void) { return (0 << 16) | 1; }
+
+const char* tts_strerror(int code) {
+  switch (code) {
+    case TTS_OK: return "ok";
+    case TTS_EINVAL: return "invalid argument (null pointer or non-positive size)";
+    case TTS_ETILE: return "tile side must be 16 or 32 and divide H and W";
+    case TTS_EK: return "K must be in [1, 512]";
+    case TTS_EWORKSPACE: return "workspace missing or too small";
+    case TTS_ESPAN: return "span must be in [1, 8192]";
+    case TTS_EG: return "G must be below 2^30";
+    case TTS_ERADIUS: return "only stencil radius R = 1 is supported";
+    default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
+  }
+}
+
+int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, float blur,
+                 float* proj, uint8_t* keep, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_fwd<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, proj, keep);
+  return launch_status();
+}
+
+int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, float blur,
+                 const float* grad9, float* gparams, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams))) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, grad9, gparams);
+  return launch_status();
+}
+
+int tts_adam_advance(int32_t* step, float beta1, float beta2, hipStream_t stream) {
+  if (!step) return TTS_EINVAL;
+  k_adam_advance<<<1, 64, 0, stream>>>(step, beta1, beta2);
+  return launch_status();
+}
+
+int tts_adam(float* params, float* m, float* v, const float* grad, const float* lr, int G,
+             const int32_t* step, float beta1, float beta2, float eps, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !m || !v || !grad || !lr || !step))) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  const int64_t n = (int64_t)G * 14;
+  k_adam<<<grid1d(n, 256), 256, 0, stream>>>(params, m, v, grad, lr, n, step, beta1, beta2, eps);
+  return launch_status();
+}
+
+int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, float blur,
+                      float* grad9, float* gparams, float* m, float* v, const float* lr,
+                      const int32_t* step, float beta1, float beta2, float eps,
+                      hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !m || !v || !lr || !step)))
+    return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd_adam<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, grad9,
+                                                      gparams, m, v, lr, step, beta1, beta2, eps);
+  return launch_status();
+}
+
+int tts_zero(float* buf, int64_t n, hipStream_t stream) {
+  if (n < 0 || (n > 0 && !buf)) return TTS_EINVAL;
+  if (n == 0) return TTS_OK;
+  k_zero<<<grid1d(n, 256), 256, 0, stream>>>(buf, n);
+  return launch_status();
+}
+
+}  // extern "C"

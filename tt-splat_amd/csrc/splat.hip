@@ -1,0 +1,442 @@
+// Binned poly-splat + WSR render, forward and backward.  One 256-thread workgroup per S x S
+// tile (S = 16 or 32).  Math: tools/bh_views.py:65-71 (forward), spike/backward.py:42-58 and
+// tools/resident_traced.py:60-88 (backward + theta backward), tools/m4_train_binned.py:130-143
+// (tile-local theta_u).
+//
+// Forward: the tile's valid slots are compacted into LDS as theta_u (6) and (col_o, o_col) (4);
+// each thread owns S*S/256 pixels and walks the slots:
+//     u = theta . [lx^2, ly^2, lx*ly, lx, ly, 1],  w = max(u,0)^2,  num += w*col, den += w*oc
+// and writes C = (num + w_b c_b) / (den + w_b) straight into the [H,W,3] image.
+//
+// Backward: per-pixel gnum = gC/den, gden = -(gC.C)/den are staged in LDS; the slots are then
+// contracted over the tile's pixels slot-parallel (TPS threads share one slot and split its
+// rows).  Along a pixel row, u = (th0*lx + c1)*lx + c0 with c0, c1 fixed per row, and the
+// theta gradient is gathered as three row moments sum(gu*lx^2), sum(gu*lx), sum(gu), so the
+// inner loop costs 16 VALU ops per (pixel, slot) pair.  Each slot's 10 partial sums are
+// combined in LDS, pushed through the theta backward, and added into grad9[g] with one
+// hardware float atomic per value (a gaussian lives in at most 9 tiles at R = 1).
+
+#include "tts_common.h"
+
+namespace tts {
+
+constexpr int kSplatMaxK = 512;
+
+struct SlotLDS {
+  float4* ta;  // theta_u 0..3
+  float4* tb;  // theta_u 4..5, -, -
+  float4* cl;  // col_o r,g,b, o_col
+  int* gid;    // gaussian id (proj mode) or original slot (theta mode)
+};
+
+__device__ __forceinline__ SlotLDS carve_slots(unsigned char* base, int K) {
+  SlotLDS s;
+  s.ta = reinterpret_cast<float4*>(base);
+  s.tb = s.ta + K;
+  s.cl = s.tb + K;
+  s.gid = reinterpret_cast<int*>(s.cl + K);
+  return s;
+}
+
+__device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (3 * 16 + 4); }
+
+// Tile-local theta_u for one gaussian record (tools/m4_train_binned.py:130-143).
+__device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
+                                           float oy, float inv_k, float4& ta, float4& tb,
+                                           float4& cl) {
+  const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+  const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+  const float a = r0.z, b = r0.w, c = r1.x;
+  const float mx = r0.x - ox, my = r0.y - oy;
+  const float Q0 = a * mx * mx + 2.0f * b * mx * my + c * my * my;
+  ta = make_float4(-a * inv_k, -c * inv_k, -2.0f * b * inv_k, 2.0f * (a * mx + b * my) * inv_k);
+  tb = make_float4(2.0f * (b * mx + c * my) * inv_k, 1.0f - Q0 * inv_k, 0.0f, 0.0f);
+  cl = make_float4(r1.z, r1.w, r2.x, r2.y);
+}
+
+// Compact the tile's valid slots into LDS in slot order.  Returns the valid count.
+__device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
+                                               const int32_t* __restrict__ idx,
+                                               const uint8_t* __restrict__ valid, int t, int K,
+                                               float ox, float oy, float inv_k, SlotLDS sl,
+                                               int* s_tmp) {
+  int base = 0;
+  for (int s0 = 0; s0 < K; s0 += 256) {
+    const int s = s0 + threadIdx.x;
+    const int v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
+    int total;
+    const int pos = base + block_excl_scan256(v, s_tmp, &total);
+    if (v) {
+      const int g = idx[(int64_t)t * K + s];
+      float4 ta, tb, cl;
+      build_slot(proj, g, ox, oy, inv_k, ta, tb, cl);
+      sl.ta[pos] = ta;
+      sl.tb[pos] = tb;
+      sl.cl[pos] = cl;
+      sl.gid[pos] = g;
+    }
+    base += total;
+  }
+  return base;
+}
+
+// Load pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K] (all K slots).
+__device__ __forceinline__ void load_slots_theta(const float* __restrict__ theta,
+                                                 const float* __restrict__ col,
+                                                 const float* __restrict__ oc, int t, int K,
+                                                 SlotLDS sl) {
+  const float* th = theta + (int64_t)t * 6 * K;
+  for (int s = threadIdx.x; s < K; s += blockDim.x) {
+    sl.ta[s] = make_float4(th[s], th[K + s], th[2 * K + s], th[3 * K + s]);
+    sl.tb[s] = make_float4(th[4 * K + s], th[5 * K + s], 0.0f, 0.0f);
+    const float* c = col + ((int64_t)t * K + s) * 3;
+    sl.cl[s] = make_float4(c[0], c[1], c[2], oc[(int64_t)t * K + s]);
+    sl.gid[s] = s;
+  }
+}
+
+template <int S, bool FROM_PROJ>
+__global__ __launch_bounds__(256) void k_splat_fwd(
+    const float* __restrict__ proj, const int32_t* __restrict__ idx,
+    const uint8_t* __restrict__ valid, const float* __restrict__ theta,
+    const float* __restrict__ col, const float* __restrict__ oc, int ntx, int W, int K,
+    float inv_k, const float* __restrict__ bg, float* __restrict__ image,
+    float* __restrict__ den_out) {
+  constexpr int PPT = S * S / 256;  // pixels per thread
+  extern __shared__ unsigned char s_dyn[];
+  __shared__ int s_tmp[4];
+  const SlotLDS sl = carve_slots(s_dyn, K);
+  const int t = blockIdx.x;
+  const int tx = t % ntx, ty = t / ntx;
+  const int ox = tx * S, oy = ty * S;
+  int n;
+  if constexpr (FROM_PROJ) {
+    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
+  } else {
+    load_slots_theta(theta, col, oc, t, K, sl);
+    n = K;
+  }
+  __syncthreads();
+
+  float lx[PPT], ly[PPT], xx[PPT], yy[PPT], xy[PPT];
+  float ar[PPT], ag[PPT], ab[PPT], ad[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int p = threadIdx.x + 256 * i;
+    lx[i] = (float)(p % S) + 0.5f;
+    ly[i] = (float)(p / S) + 0.5f;
+    xx[i] = lx[i] * lx[i];
+    yy[i] = ly[i] * ly[i];
+    xy[i] = lx[i] * ly[i];
+    ar[i] = ag[i] = ab[i] = ad[i] = 0.0f;
+  }
+  for (int s = 0; s < n; ++s) {
+    const float4 A = sl.ta[s], B = sl.tb[s], C = sl.cl[s];
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const float u = A.x * xx[i] + A.y * yy[i] + A.z * xy[i] + A.w * lx[i] + B.x * ly[i] + B.y;
+      const float r = fmaxf(u, 0.0f);
+      const float w = r * r;
+      ar[i] += w * C.x;
+      ag[i] += w * C.y;
+      ab[i] += w * C.z;
+      ad[i] += w * C.w;
+    }
+  }
+  const float wb = bg[0];
+  const float cbr = wb * bg[1], cbg = wb * bg[2], cbb = wb * bg[3];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int p = threadIdx.x + 256 * i;
+    const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
+    const float d = ad[i] + wb;
+    image[pix * 3 + 0] = (ar[i] + cbr) / d;
+    image[pix * 3 + 1] = (ag[i] + cbg) / d;
+    image[pix * 3 + 2] = (ab[i] + cbb) / d;
+    if (den_out) den_out[pix] = d;
+  }
+}
+
+template <int S, bool FROM_PROJ>
+__global__ __launch_bounds__(256) void k_splat_bwd(
+    const float* __restrict__ proj, const int32_t* __restrict__ idx,
+    const uint8_t* __restrict__ valid, const float* __restrict__ theta,
+    const float* __restrict__ col, const float* __restrict__ oc, int ntx, int W, int K,
+    float inv_k, const float* __restrict__ bg, const float* __restrict__ image,
+    const float* __restrict__ den, const float* __restrict__ gimage, float* __restrict__ grad9,
+    float* __restrict__ gtheta, float* __restrict__ gcol, float* __restrict__ goc,
+    float* __restrict__ gwb) {
+  constexpr int P = S * S;
+  extern __shared__ unsigned char s_dyn[];
+  __shared__ int s_tmp[4];
+  __shared__ float s_ftmp[4];
+  const SlotLDS sl = carve_slots(s_dyn, K);
+  float4* s_px = reinterpret_cast<float4*>(s_dyn + slot_lds_bytes(K) + (16 - slot_lds_bytes(K) % 16) % 16);
+  float* s_red = reinterpret_cast<float*>(s_px + P);  // [10][256]
+
+  const int t = blockIdx.x;
+  const int tx = t % ntx, ty = t / ntx;
+  const int ox = tx * S, oy = ty * S;
+  int n;
+  if constexpr (FROM_PROJ) {
+    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
+  } else {
+    load_slots_theta(theta, col, oc, t, K, sl);
+    n = K;
+  }
+  // Per-pixel WSR backward: gnum = gC/den, gden = -(gC . C)/den.
+  const float wb = bg[0];
+  float wpart = 0.0f;
+  for (int p = threadIdx.x; p < P; p += 256) {
+    const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
+    const float inv = 1.0f / den[pix];
+    const float g0 = gimage[pix * 3 + 0], g1 = gimage[pix * 3 + 1], g2 = gimage[pix * 3 + 2];
+    const float c0 = image[pix * 3 + 0], c1 = image[pix * 3 + 1], c2 = image[pix * 3 + 2];
+    const float4 q = make_float4(g0 * inv, g1 * inv, g2 * inv, -(g0 * c0 + g1 * c1 + g2 * c2) * inv);
+    s_px[p] = q;
+    wpart += q.x * bg[1] + q.y * bg[2] + q.z * bg[3] + q.w;
+  }
+  if (gwb) {
+    const float tot = block_sum256(wpart, s_ftmp);
+    if (threadIdx.x == 0) unsafeAtomicAdd(gwb, tot);
+  }
+  __syncthreads();
+
+  // threads per slot: split rows while slots are few
+  int tps = 1;
+  while (tps < 16 && tps * 2 * n <= 256) tps <<= 1;
+  const int sg = 256 / tps;
+  const int h = threadIdx.x / sg, sl_local = threadIdx.x % sg;
+  const float ox_f = (float)ox, oy_f = (float)oy;
+  for (int c0s = 0; c0s < n; c0s += sg) {
+    const int s = c0s + sl_local;
+    const bool active = s < n;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f), B = A, C = A;
+    if (active) {
+      A = sl.ta[s];
+      B = sl.tb[s];
+      C = sl.cl[s];
+    }
+    float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f;
+    float gr = 0.f, gg = 0.f, gb = 0.f, go = 0.f;
+    if (active) {
+      for (int y = h; y < S; y += tps) {
+        const float ly = (float)y + 0.5f;
+        const float yy = ly * ly;
+        const float cc0 = A.y * yy + B.x * ly + B.y;  // u = (A.x*lx + cc1)*lx + cc0
+        const float cc1 = A.z * ly + A.w;
+        float m0 = 0.f, m1 = 0.f, m2 = 0.f;
+        const float4* row = s_px + y * S;
+#pragma unroll
+        for (int x = 0; x < S; ++x) {
+          const float lx = (float)x + 0.5f;
+          const float u = (A.x * lx + cc1) * lx + cc0;
+          const float r = fmaxf(u, 0.0f);
+          const float w = r * r;
+          const float4 q = row[x];
+          const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
+          const float gu = r * gw;  // half of dL/du
+          gr += w * q.x;
+          gg += w * q.y;
+          gb += w * q.z;
+          go += w * q.w;
+          m0 += gu * (lx * lx);
+          m1 += gu * lx;
+          m2 += gu;
+        }
+        g0 += m0;
+        g2 += ly * m1;
+        g3 += m1;
+        g1 += yy * m2;
+        g4 += ly * m2;
+        g5 += m2;
+      }
+    }
+    // combine the tps row-partials of each slot
+    if (tps > 1) {
+      float* red = s_red + threadIdx.x;
+      red[0 * 256] = g0; red[1 * 256] = g1; red[2 * 256] = g2; red[3 * 256] = g3;
+      red[4 * 256] = g4; red[5 * 256] = g5; red[6 * 256] = gr; red[7 * 256] = gg;
+      red[8 * 256] = gb; red[9 * 256] = go;
+      __syncthreads();
+      if (h == 0) {
+        for (int k2 = 1; k2 < tps; ++k2) {
+          const float* o = s_red + k2 * sg + sl_local;
+          g0 += o[0 * 256]; g1 += o[1 * 256]; g2 += o[2 * 256]; g3 += o[3 * 256];
+          g4 += o[4 * 256]; g5 += o[5 * 256]; gr += o[6 * 256]; gg += o[7 * 256];
+          gb += o[8 * 256]; go += o[9 * 256];
+        }
+      }
+      __syncthreads();
+    }
+    if (h == 0 && active) {
+      // dL/du = 2 r gw: the factor 2 was left out of the inner loop
+      g0 *= 2.f; g1 *= 2.f; g2 *= 2.f; g3 *= 2.f; g4 *= 2.f; g5 *= 2.f;
+      if constexpr (FROM_PROJ) {
+        // theta backward (tools/resident_traced.py:72-88), gtQ = gtheta * (-1/k)
+        const int g = sl.gid[s];
+        const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+        const float4 r0 = r[0], r1 = r[1];
+        const float a = r0.z, b = r0.w, c = r1.x;
+        const float mx = r0.x - ox_f, my = r0.y - oy_f;
+        const float nk = -inv_k;
+        const float q0 = g0 * nk, q1 = g1 * nk, q2 = g2 * nk, q3 = g3 * nk, q4 = g4 * nk, q5 = g5 * nk;
+        const float ga = q0 - 2.f * mx * q3 + mx * mx * q5;
+        const float gbv = 2.f * q2 - 2.f * my * q3 - 2.f * mx * q4 + 2.f * mx * my * q5;
+        const float gc = q1 - 2.f * my * q4 + my * my * q5;
+        const float gmx = -2.f * a * q3 - 2.f * b * q4 + (2.f * a * mx + 2.f * b * my) * q5;
+        const float gmy = -2.f * b * q3 - 2.f * c * q4 + (2.f * b * mx + 2.f * c * my) * q5;
+        float* dst = grad9 + (int64_t)g * 9;
+        unsafeAtomicAdd(dst + 0, ga);
+        unsafeAtomicAdd(dst + 1, gbv);
+        unsafeAtomicAdd(dst + 2, gc);
+        unsafeAtomicAdd(dst + 3, gmx);
+        unsafeAtomicAdd(dst + 4, gmy);
+        unsafeAtomicAdd(dst + 5, gr);
+        unsafeAtomicAdd(dst + 6, gg);
+        unsafeAtomicAdd(dst + 7, gb);
+        unsafeAtomicAdd(dst + 8, go);
+      } else {
+        float* th = gtheta + (int64_t)t * 6 * K;
+        th[s] = g0; th[K + s] = g1; th[2 * K + s] = g2;
+        th[3 * K + s] = g3; th[4 * K + s] = g4; th[5 * K + s] = g5;
+        float* gcp = gcol + ((int64_t)t * K + s) * 3;
+        gcp[0] = gr; gcp[1] = gg; gcp[2] = gb;
+        goc[(int64_t)t * K + s] = go;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_theta_gather(const float* __restrict__ proj,
+                                                      const int32_t* __restrict__ idx,
+                                                      const uint8_t* __restrict__ valid, int ntx,
+                                                      int S, int K, float inv_k,
+                                                      float* __restrict__ theta,
+                                                      float* __restrict__ col,
+                                                      float* __restrict__ oc) {
+  const int t = blockIdx.x;
+  const int tx = t % ntx, ty = t / ntx;
+  const float ox = (float)(tx * S), oy = (float)(ty * S);
+  for (int s = threadIdx.x; s < K; s += blockDim.x) {
+    const int64_t ts = (int64_t)t * K + s;
+    float4 ta = make_float4(0.f, 0.f, 0.f, 0.f), tb = ta, cl = ta;
+    if (valid[ts]) build_slot(proj, idx[ts], ox, oy, inv_k, ta, tb, cl);
+    float* th = theta + (int64_t)t * 6 * K;
+    th[s] = ta.x; th[K + s] = ta.y; th[2 * K + s] = ta.z; th[3 * K + s] = ta.w;
+    th[4 * K + s] = tb.x; th[5 * K + s] = tb.y;
+    col[ts * 3 + 0] = cl.x; col[ts * 3 + 1] = cl.y; col[ts * 3 + 2] = cl.z;
+    oc[ts] = cl.w;
+  }
+}
+
+inline int check_tile(int H, int W, int S, int K) {
+  if (H <= 0 || W <= 0) return TTS_EINVAL;
+  if (S != 16 && S != 32) return TTS_ETILE;
+  if (H % S || W % S) return TTS_ETILE;
+  if (K < 1 || K > kSplatMaxK) return TTS_EK;
+  return TTS_OK;
+}
+
+inline size_t fwd_lds(int K) { return (size_t)K * (3 * 16 + 4); }
+inline size_t bwd_lds(int K, int S) {
+  size_t a = (size_t)K * (3 * 16 + 4);
+  a += (16 - a % 16) % 16;
+  return a + (size_t)S * S * 16 + 10 * 256 * sizeof(float);
+}
+
+template <bool FROM_PROJ>
+int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
+               const float* col, const float* oc, int H, int W, int S, int K, float k,
+               const float* bg, float* image, float* den, hipStream_t stream) {
+  const int ntx = W / S, T = (H / S) * ntx;
+  const float inv_k = (float)(1.0 / (double)k);
+  if (S == 16)
+    k_splat_fwd<16, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(proj, idx, valid, theta, col, oc,
+                                                               ntx, W, K, inv_k, bg, image, den);
+  else
+    k_splat_fwd<32, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(proj, idx, valid, theta, col, oc,
+                                                               ntx, W, K, inv_k, bg, image, den);
+  return launch_status();
+}
+
+template <bool FROM_PROJ>
+int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
+               const float* col, const float* oc, int H, int W, int S, int K, float k,
+               const float* bg, const float* image, const float* den, const float* gimage,
+               float* grad9, float* gtheta, float* gcol, float* goc, float* gwb,
+               hipStream_t stream) {
+  const int ntx = W / S, T = (H / S) * ntx;
+  const float inv_k = (float)(1.0 / (double)k);
+  if (S == 16)
+    k_splat_bwd<16, FROM_PROJ><<<T, 256, bwd_lds(K, 16), stream>>>(
+        proj, idx, valid, theta, col, oc, ntx, W, K, inv_k, bg, image, den, gimage, grad9, gtheta,
+        gcol, goc, gwb);
+  else
+    k_splat_bwd<32, FROM_PROJ><<<T, 256, bwd_lds(K, 32), stream>>>(
+        proj, idx, valid, theta, col, oc, ntx, W, K, inv_k, bg, image, den, gimage, grad9, gtheta,
+        gcol, goc, gwb);
+  return launch_status();
+}
+
+}  // namespace tts
+
+using namespace tts;
+
+extern "C" {
+
+int tts_theta_u_gathered(const float* proj, const int32_t* idx, const uint8_t* valid, int H,
+                         int W, int S, int K, float k, float* theta, float* col, float* oc,
+                         hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!proj || !idx || !valid || !theta || !col || !oc) return TTS_EINVAL;
+  const int ntx = W / S, T = (H / S) * ntx;
+  k_theta_gather<<<T, 256, 0, stream>>>(proj, idx, valid, ntx, S, K, (float)(1.0 / (double)k),
+                                        theta, col, oc);
+  return launch_status();
+}
+
+int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, int H, int W,
+                  int S, int K, float k, const float* bg, float* image, float* den,
+                  hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!proj || !idx || !valid || !bg || !image) return TTS_EINVAL;
+  return launch_fwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, H, W, S, K, k, bg, image,
+                          den, stream);
+}
+
+int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc, int H, int W,
+                        int S, int K, const float* bg, float* image, float* den,
+                        hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!theta || !col || !oc || !bg || !image) return TTS_EINVAL;
+  return launch_fwd<false>(nullptr, nullptr, nullptr, theta, col, oc, H, W, S, K, 1.0f, bg,
+                           image, den, stream);
+}
+
+int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, int H, int W,
+                  int S, int K, float k, const float* bg, const float* image, const float* den,
+                  const float* gimage, float* grad9, float* gwb, hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!proj || !idx || !valid || !bg || !image || !den || !gimage || !grad9) return TTS_EINVAL;
+  return launch_bwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, H, W, S, K, k, bg, image,
+                          den, gimage, grad9, nullptr, nullptr, nullptr, gwb, stream);
+}
+
+int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc, int H, int W,
+                        int S, int K, const float* bg, const float* image, const float* den,
+                        const float* gimage, float* gtheta, float* gcol, float* goc, float* gwb,
+                        hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!theta || !col || !oc || !bg || !image || !den || !gimage || !gtheta || !gcol || !goc)
+    return TTS_EINVAL;
+  return launch_bwd<false>(nullptr, nullptr, nullptr, theta, col, oc, H, W, S, K, 1.0f, bg,
+                           image, den, gimage, nullptr, gtheta, gcol, goc, gwb, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,268 @@
+"""Typed wrappers over the libttsplat C ABI.
+
+Each wrapper validates device, dtype, contiguity and shape of every tensor, then enqueues the
+kernel on the current torch stream.  Nothing here allocates unless an output is not supplied
+(out=None); the graph-captured training step passes every buffer in.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr, require, stream
+
+F32, I32, U8 = torch.float32, torch.int32, torch.uint8
+
+NEAR, BLUR = 0.2, 0.3          # tools/geom_device.py:25
+BETA1, BETA2, EPS = 0.9, 0.999, 1e-8   # tools/resident_traced.py:92
+
+
+def _aligned16(t, name):
+    """The kernels read [G,12] records as float4: the base address must be 16-byte aligned."""
+    if t.data_ptr() % 16:
+        raise ValueError(f"{name} must start on a 16-byte boundary")
+    return t
+
+
+def version():
+    v = _lib.load().tts_version()
+    return (v >> 16, v & 0xFFFF)
+
+
+# ------------------------------------------------------------------------------- geometry --
+def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None):
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(camera, "camera", F32, (16,), dev)
+    proj = torch.empty(G, 12, device=dev, dtype=F32) if proj is None else proj
+    keep = torch.empty(G, device=dev, dtype=U8) if keep is None else keep
+    _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
+    require(keep, "keep", U8, (G,), dev)
+    call("tts_geom_fwd", ptr(params), G, ptr(camera), near, blur, ptr(proj), ptr(keep), stream())
+    return proj, keep
+
+
+def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None):
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(camera, "camera", F32, (16,), dev)
+    require(grad9, "grad9", F32, (G, 9), dev)
+    out = torch.empty(G, 14, device=dev, dtype=F32) if out is None else out
+    require(out, "gparams", F32, (G, 14), dev)
+    call("tts_geom_bwd", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(out), stream())
+    return out
+
+
+# -------------------------------------------------------------------------------- binning --
+def bin_workspace(G, H, W, S, device):
+    """Zero-initialised workspace for assign_bins (kept zeroed by the library)."""
+    n = _lib.load().tts_bin_workspace_bytes(G, H, W, S)
+    return torch.zeros(max(n, 1), device=device, dtype=U8)
+
+
+def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, idx=None,
+                valid=None, count=None, ncand=None):
+    """mu2d: [G,2] fp32 (or any [G,>=2] row-contiguous view, e.g. the proj record),
+    keep: [G] uint8 or bool.  Returns idx[T,K] int32, valid[T,K] uint8, count[T], ncand[T]."""
+    G = mu2d.shape[0]
+    dev = mu2d.device
+    if not mu2d.is_cuda or mu2d.dtype != F32 or mu2d.dim() != 2 or mu2d.shape[1] < 2 \
+            or mu2d.stride(1) != 1:
+        raise ValueError("mu2d must be a [G,>=2] fp32 GPU tensor with unit column stride")
+    if keep.dtype == torch.bool:
+        keep = keep.view(U8)
+    require(keep, "keep", U8, (G,), dev)
+    if S not in (16, 32) or H % S or W % S:
+        raise ValueError(f"tile side {S} must be 16 or 32 and divide {H}x{W}")
+    T = (H // S) * (W // S)
+    idx = torch.empty(T, K, device=dev, dtype=I32) if idx is None else idx
+    valid = torch.empty(T, K, device=dev, dtype=U8) if valid is None else valid
+    count = torch.empty(T, device=dev, dtype=I32) if count is None else count
+    ncand = torch.empty(T, device=dev, dtype=I32) if ncand is None else ncand
+    require(idx, "idx", I32, (T, K), dev)
+    require(valid, "valid", U8, (T, K), dev)
+    require(count, "count", I32, (T,), dev)
+    require(ncand, "ncand", I32, (T,), dev)
+    workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
+    call("tts_assign_bins", ptr(mu2d), mu2d.stride(0), ptr(keep), 1, G, H, W, S, R, K, span,
+         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(workspace), workspace.numel(),
+         stream())
+    return idx, valid, count, ncand
+
+
+# ---------------------------------------------------------------------------------- splat --
+def _bins_check(idx, valid, H, W, S, dev):
+    T = (H // S) * (W // S)
+    if idx.dim() != 2 or idx.shape[0] != T:
+        raise ValueError(f"idx must be [T={T},K], got {tuple(idx.shape)}")
+    K = idx.shape[1]
+    if valid.dtype == torch.bool:
+        valid = valid.view(U8)
+    require(idx, "idx", I32, (T, K), dev)
+    require(valid, "valid", U8, (T, K), dev)
+    return T, K, valid
+
+
+def theta_gather(proj, idx, valid, H, W, S, k, theta=None, col=None, oc=None):
+    dev = proj.device
+    _aligned16(require(proj, "proj", F32, (proj.shape[0], 12)), "proj")
+    T, K, valid = _bins_check(idx, valid, H, W, S, dev)
+    theta = torch.empty(T, 6, K, device=dev, dtype=F32) if theta is None else theta
+    col = torch.empty(T, K, 3, device=dev, dtype=F32) if col is None else col
+    oc = torch.empty(T, K, device=dev, dtype=F32) if oc is None else oc
+    require(theta, "theta", F32, (T, 6, K), dev)
+    require(col, "col", F32, (T, K, 3), dev)
+    require(oc, "oc", F32, (T, K), dev)
+    call("tts_theta_u_gathered", ptr(proj), ptr(idx), ptr(valid), H, W, S, K, float(k),
+         ptr(theta), ptr(col), ptr(oc), stream())
+    return theta, col, oc
+
+
+def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None):
+    dev = proj.device
+    _aligned16(require(proj, "proj", F32, (proj.shape[0], 12)), "proj")
+    T, K, valid = _bins_check(idx, valid, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    call("tts_splat_fwd", ptr(proj), ptr(idx), ptr(valid), H, W, S, K, float(k), ptr(bg),
+         ptr(image), ptr(den), stream())
+    return image, den
+
+
+def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, grad9, gwb=None):
+    dev = proj.device
+    G = proj.shape[0]
+    _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
+    T, K, valid = _bins_check(idx, valid, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    require(grad9, "grad9", F32, (G, 9), dev)
+    if gwb is not None:
+        require(gwb, "gwb", F32, (1,), dev)
+    call("tts_splat_bwd", ptr(proj), ptr(idx), ptr(valid), H, W, S, K, float(k), ptr(bg),
+         ptr(image), ptr(den), ptr(gimage), ptr(grad9), ptr(gwb), stream())
+    return grad9
+
+
+def splat_fwd_theta(theta, col, oc, bg, H, W, S, image=None, den=None):
+    dev = theta.device
+    T = (H // S) * (W // S)
+    K = theta.shape[-1]
+    require(theta, "theta", F32, (T, 6, K))
+    require(col, "col", F32, (T, K, 3), dev)
+    require(oc, "oc", F32, (T, K), dev)
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    call("tts_splat_fwd_theta", ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg), ptr(image),
+         ptr(den), stream())
+    return image, den
+
+
+def splat_bwd_theta(theta, col, oc, bg, H, W, S, image, den, gimage, gwb=None):
+    dev = theta.device
+    T = (H // S) * (W // S)
+    K = theta.shape[-1]
+    require(theta, "theta", F32, (T, 6, K))
+    require(col, "col", F32, (T, K, 3), dev)
+    require(oc, "oc", F32, (T, K), dev)
+    require(bg, "bg", F32, (4,), dev)
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    gtheta = torch.empty_like(theta)
+    gcol = torch.empty_like(col)
+    goc = torch.empty_like(oc)
+    call("tts_splat_bwd_theta", ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg), ptr(image),
+         ptr(den), ptr(gimage), ptr(gtheta), ptr(gcol), ptr(goc), ptr(gwb), stream())
+    return gtheta, gcol, goc
+
+
+# ----------------------------------------------------------------------------------- loss --
+def loss_workspace(H, W, device):
+    n = _lib.load().tts_loss_workspace_bytes(H, W)
+    if n == 0:
+        raise ValueError(f"image {H}x{W} is smaller than the 11x11 SSIM window")
+    return torch.empty(n // 4, device=device, dtype=F32)
+
+
+def loss_partials_count(H, W):
+    ns = ctypes.c_int(0)
+    n = _lib.load().tts_loss_partials_count(H, W, ctypes.byref(ns))
+    return n, ns.value
+
+
+def loss_grad(image, target, lam=0.2, gimage=None, partials=None, workspace=None):
+    H, W = image.shape[0], image.shape[1]
+    dev = image.device
+    require(image, "image", F32, (H, W, 3))
+    require(target, "target", F32, (H, W, 3), dev)
+    gimage = torch.empty_like(image) if gimage is None else gimage
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    if partials is not None:
+        require(partials, "partials", F32, (loss_partials_count(H, W)[0],), dev)
+    workspace = loss_workspace(H, W, dev) if workspace is None else workspace
+    call("tts_loss_grad", ptr(image), ptr(target), H, W, float(lam), ptr(gimage), ptr(partials),
+         ptr(workspace), workspace.numel() * 4, stream())
+    return gimage
+
+
+def loss_from_partials(partials, H, W, lam=0.2):
+    """Loss value from the partial sums written by loss_grad (a device scalar)."""
+    _, ns = loss_partials_count(H, W)
+    s_sum = partials[:ns].double().sum()
+    l1_sum = partials[ns:].double().sum()
+    n = 3.0 * H * W
+    n_s = 3.0 * (H - 10) * (W - 10)
+    return ((1.0 - lam) * l1_sum / n + lam * (1.0 - s_sum / n_s)).float()
+
+
+# ----------------------------------------------------------------------------------- adam --
+def adam_state(device):
+    """Step block: int32 step counter + the two fp32 bias-correction factors (4 words)."""
+    return torch.zeros(4, device=device, dtype=I32)
+
+
+def adam_advance(step, b1=BETA1, b2=BETA2):
+    require(step, "step", I32, (4,))
+    call("tts_adam_advance", ptr(step), b1, b2, stream())
+
+
+def adam(params, m, v, grad, lr, step, b1=BETA1, b2=BETA2, eps=EPS):
+    G = params.shape[0]
+    dev = params.device
+    for t, n in ((params, "params"), (m, "m"), (v, "v"), (grad, "grad")):
+        require(t, n, F32, (G, 14), dev)
+    require(lr, "lr", F32, (14,), dev)
+    require(step, "step", I32, (4,), dev)
+    call("tts_adam", ptr(params), ptr(m), ptr(v), ptr(grad), ptr(lr), G, ptr(step), b1, b2, eps,
+         stream())
+
+
+def geom_bwd_adam(params, camera, grad9, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
+                  b1=BETA1, b2=BETA2, eps=EPS):
+    G = params.shape[0]
+    dev = params.device
+    for t, n in ((params, "params"), (m, "m"), (v, "v")):
+        require(t, n, F32, (G, 14), dev)
+    require(camera, "camera", F32, (16,), dev)
+    require(grad9, "grad9", F32, (G, 9), dev)
+    require(lr, "lr", F32, (14,), dev)
+    require(step, "step", I32, (4,), dev)
+    if gparams is not None:
+        require(gparams, "gparams", F32, (G, 14), dev)
+    call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(gparams),
+         ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
+
+
+def zero_(buf):
+    require(buf, "buf", F32)
+    call("tts_zero", ptr(buf), buf.numel(), stream())
+    return buf

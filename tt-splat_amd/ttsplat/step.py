@@ -1,0 +1,134 @@
+"""Device-resident, graph-captured training step (the traced step of tools/resident_traced.py).
+
+The reference allocates every persistent buffer first (tools/resident_traced.py:222-296),
+captures the step as ttnn traces (:551-567) and replays them per iteration (:667-757), with
+host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
+host round trip:
+
+    geom_fwd -> assign_bins (4 kernels) -> splat_fwd -> loss_grad (2 kernels)
+             -> splat_bwd (theta bwd + slot->gaussian atomics) -> adam_advance
+             -> geom_bwd_adam (geometry bwd + Adam + grad9 reset)
+
+captured once per camera into a HIP graph (torch.cuda.CUDAGraph) and replayed.  The step
+counter and Adam bias corrections live in device memory, so replays need no re-capture.
+All buffers are allocated in __init__; a replay allocates nothing.
+"""
+import torch
+
+from . import kernels
+from .binned import TileMap
+from .kernels import F32, I32, U8
+
+DEFAULT_LR = 1e-3
+MEANS_LR = 1.6e-4
+
+
+def lr_vector(lr=DEFAULT_LR, means_lr=MEANS_LR, device="cuda"):
+    """Per-column learning rates for the [G,14] block: means get means_lr, the rest lr."""
+    v = torch.full((14,), float(lr), dtype=F32)
+    v[0:3] = float(means_lr)
+    return v.to(device)
+
+
+class TrainStep:
+    """Owns params [G,14], Adam moments and every work buffer for training against one or more
+    (camera, target) pairs; step(i) runs one full training step on camera i."""
+
+    def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
+                 c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda"):
+        dev = torch.device(device)
+        self.dev = dev
+        self.G = params.shape[0]
+        self.H, self.W = cameras[0].H, cameras[0].W
+        self.K, self.S, self.k, self.lam = K, S, float(k), float(lambda_ssim)
+        self.tmap = TileMap(self.H, self.W, S, device=dev)
+        self.span = span or self.tmap.span
+        T = self.tmap.T
+        G, H, W = self.G, self.H, self.W
+        # parameters and optimiser state
+        self.P = params.to(dev, F32).contiguous().clone()
+        self.m = torch.zeros(G, 14, device=dev, dtype=F32)
+        self.v = torch.zeros(G, 14, device=dev, dtype=F32)
+        self.step_block = kernels.adam_state(dev)
+        self.lr = (lr_vector(device=dev) if lr is None else torch.as_tensor(lr, dtype=F32).to(dev)).contiguous()
+        w_b = torch.nn.functional.softplus(torch.tensor(float(w_b_raw)))
+        self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
+        # per-view inputs
+        self.cams = [c.device_block(dev) for c in cameras]
+        self.targets = [t.to(dev, F32).contiguous() for t in targets]
+        if len(self.targets) != len(self.cams):
+            raise ValueError("one target image per camera is required")
+        # work buffers
+        self.proj = torch.empty(G, 12, device=dev, dtype=F32)
+        self.keep = torch.empty(G, device=dev, dtype=U8)
+        self.bin_ws = kernels.bin_workspace(G, H, W, S, dev)
+        self.idx = torch.empty(T, K, device=dev, dtype=I32)
+        self.valid = torch.empty(T, K, device=dev, dtype=U8)
+        self.count = torch.empty(T, device=dev, dtype=I32)
+        self.ncand = torch.empty(T, device=dev, dtype=I32)
+        self.image = torch.empty(H, W, 3, device=dev, dtype=F32)
+        self.den = torch.empty(H, W, device=dev, dtype=F32)
+        self.gimage = torch.empty(H, W, 3, device=dev, dtype=F32)
+        self.loss_ws = kernels.loss_workspace(H, W, dev)
+        self.partials = torch.empty(kernels.loss_partials_count(H, W)[0], device=dev, dtype=F32)
+        self.grad9 = torch.zeros(G, 9, device=dev, dtype=F32)
+        self.graphs = {}
+
+    # ---------------------------------------------------------------------------------
+    def forward(self, ci=0):
+        """Geometry + binning + fused splat for camera ci into self.image (no training)."""
+        kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep)
+        kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
+                            self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
+                            self.ncand)
+        kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
+                          self.k, self.image, self.den)
+        return self.image
+
+    def enqueue(self, ci=0):
+        """Enqueue one full training step for camera ci on the current stream."""
+        self.forward(ci)
+        kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
+                          self.loss_ws)
+        kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
+                          self.k, self.image, self.den, self.gimage, self.grad9)
+        kernels.adam_advance(self.step_block)
+        kernels.geom_bwd_adam(self.P, self.cams[ci], self.grad9, self.m, self.v, self.lr,
+                              self.step_block)
+
+    def capture(self, cams=None):
+        """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
+        kernel's code object is resident) and its effect on the state is rolled back."""
+        cams = range(len(self.cams)) if cams is None else cams
+        state = [t.clone() for t in (self.P, self.m, self.v, self.step_block)]
+        side = torch.cuda.Stream(device=self.dev)
+        side.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(side):
+            for ci in cams:
+                self.enqueue(ci)
+        torch.cuda.current_stream(self.dev).wait_stream(side)
+        for dst, src in zip((self.P, self.m, self.v, self.step_block), state):
+            dst.copy_(src)
+        torch.cuda.synchronize(self.dev)
+        for ci in cams:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.enqueue(ci)
+            self.graphs[ci] = g
+        torch.cuda.synchronize(self.dev)
+
+    def step(self, ci=0):
+        """One training step on camera ci (graph replay when captured, else eager)."""
+        g = self.graphs.get(ci)
+        if g is not None:
+            g.replay()
+        else:
+            self.enqueue(ci)
+
+    def loss(self):
+        """Loss of the last step (a device scalar; reading it synchronises)."""
+        return kernels.loss_from_partials(self.partials, self.H, self.W, self.lam)
+
+    @property
+    def steps_done(self):
+        return int(self.step_block[0].item())
