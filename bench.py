@@ -1,0 +1,244 @@
+"""Benchmark: graph-captured training step and forward render on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--no-cpu-baseline]
+
+Headline (`value`): training iterations per second at G=100k (clustered), 1264x832, K=128,
+8 orbit cameras round-robin (one camera per step), fp32: each step is geometry fwd, binning,
+fused splat fwd, L1+SSIM loss gradient, fused splat bwd (+theta bwd + slot->gaussian atomics),
+geometry bwd + Adam, replayed as one HIP graph per camera.  Inputs are resident on the GPU
+before the timed region; the timed region is exactly K steps between two synchronisations.
+
+Also reported: forward fps (geometry + binning + splat, graph replay) for the same scene, the
+G=2000 128x128 numbers, per-kernel times from HIP events on the launch stream, the roofline of
+the dominant kernel, and the CPU oracle (PyTorch-CPU restatement of the reference path) timed on
+this host's cores on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "tt-splat_amd"), ROOT]
+
+METRIC = "train it/s + render fps (G2k res128, G100k 1264×832), % of HBM/VALU roofline"
+PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector/matrix peak
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+FLOP_PER_PAIR = {"splat_fwd": 22.0, "splat_bwd": 44.0}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=30)
+    ap.add_argument("--config", default="c4")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--kernel-reps", type=int, default=100)
+    return ap.parse_args()
+
+
+def build_step(cfg, torch, TrainStep):
+    """TrainStep for the configuration; targets are the GPU render of the seed-1 set."""
+    cams = cfg.cameras()
+    P0 = cfg.params(seed=0)
+    tgt_maker = TrainStep(cfg.params(seed=1), cams, [torch.zeros(cfg.H, cfg.W, 3)] * len(cams),
+                          K=cfg.K, S=cfg.S, k=cfg.k)
+    targets = []
+    for ci in range(len(cams)):
+        targets.append(tgt_maker.forward(ci).clone())
+    del tgt_maker
+    ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k)
+    return ts
+
+
+def time_train(ts, steps, warmup, torch):
+    ncam = len(ts.cams)
+    ts.capture()
+    for i in range(warmup):
+        ts.step(i % ncam)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ts.step((warmup + i) % ncam)
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def time_forward(ts, steps, warmup, torch):
+    ncam = len(ts.cams)
+    graphs = []
+    for ci in range(ncam):
+        ts.forward(ci)
+    torch.cuda.synchronize()
+    for ci in range(ncam):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ts.forward(ci)
+        graphs.append(g)
+    for i in range(warmup):
+        graphs[i % ncam].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        graphs[i % ncam].replay()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0
+
+
+def time_kernels(ts, reps, torch, kernels):
+    """Average duration of each kernel group at the current state (camera 0), from HIP events
+    recorded on the stream the kernels are launched on."""
+    ts.enqueue(0)                       # bring every buffer to a consistent step state
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    P_save, m_save, v_save, s_save = (t.clone() for t in (ts.P, ts.m, ts.v, ts.step_block))
+    cam = ts.cams[0]
+    jobs = {
+        "geom_fwd": lambda: kernels.geom_fwd(ts.P, cam, proj=ts.proj, keep=ts.keep),
+        "binning": lambda: kernels.assign_bins(ts.proj[:, 0:2], ts.keep, ts.H, ts.W, ts.S, ts.K,
+                                               ts.span, 1, ts.bin_ws, ts.idx, ts.valid,
+                                               ts.count, ts.ncand, ts.inv),
+        "tile_order": lambda: kernels.tile_order(ts.count, ts.K, ts.order),
+        "splat_fwd": lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S,
+                                               ts.k, ts.image, ts.den, ts.order),
+        "loss_grad": lambda: kernels.loss_grad(ts.image, ts.targets[0], ts.lam, ts.gimage,
+                                               ts.partials, ts.loss_ws),
+        "splat_bwd": lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
+                                               ts.S, ts.k, ts.image, ts.den, ts.gimage,
+                                               ts.gslot, order=ts.order),
+        "geom_bwd_adam": lambda: kernels.geom_bwd_adam(ts.P, cam, ts.gslot, ts.inv, ts.m, ts.v,
+                                                       ts.lr, ts.step_block),
+    }
+    out = {}
+    for name, fn in jobs.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        e1.synchronize()
+        out[name] = e0.elapsed_time(e1) / reps * 1e3      # microseconds per launch
+    # restore the state the measurement perturbed
+    for dst, src in zip((ts.P, ts.m, ts.v, ts.step_block), (P_save, m_save, v_save, s_save)):
+        dst.copy_(src)
+    ts.forward(0)
+    torch.cuda.synchronize()
+    return out
+
+
+def cpu_baseline(cfg, seconds, torch):
+    """The oracle's training step (autograd through the PyTorch-CPU restatement of the
+    reference path, torch.optim-equivalent Adam) on this host, camera 0, bounded sample."""
+    from oracle import binning as obin
+    from oracle import pipeline as opipe
+    from oracle import splat as osplat
+    cam = cfg.cameras()[0].as_dict()
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    P = cfg.params(seed=0)
+    with torch.no_grad():
+        tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k)
+    m = torch.zeros_like(P)
+    v = torch.zeros_like(P)
+    lr = torch.full((14,), 1e-3)
+    lr[:3] = 1.6e-4
+    opipe.train_step(P, m, v, 1, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)     # warm-up
+    n, t0 = 0, time.perf_counter()
+    while n < 2 or time.perf_counter() - t0 < seconds:
+        opipe.train_step(P, m, v, n + 2, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)
+        n += 1
+    dt = time.perf_counter() - t0
+    nf, t1 = 0, time.perf_counter()
+    with torch.no_grad():
+        while nf < 2 or time.perf_counter() - t1 < seconds / 3:
+            osplat.render_binned(P, cam, tmap, K=cfg.K, k=cfg.k)
+            nf += 1
+    df = time.perf_counter() - t1
+    return dict(value=n / dt, unit="it/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"{n} oracle train steps ({dt:.1f} s) + {nf} forwards ({df:.1f} s) "
+                       f"after 1 warm-up, {cfg.name} camera 0",
+                fwd_fps=nf / df)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
+              "(the sharding design is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from ttsplat import kernels, scenes
+    from ttsplat.step import TrainStep
+
+    cfg = scenes.CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    ts = build_step(cfg, torch, TrainStep)
+    train_s = time_train(ts, args.steps, args.warmup, torch)
+    its = args.steps / train_s
+    fwd_s = time_forward(ts, args.steps, args.warmup, torch)
+    fps = args.steps / fwd_s
+    loss_last = float(ts.loss())
+    kt = time_kernels(ts, args.kernel_reps, torch, kernels)
+    pairs = int(ts.count.long().sum()) * ts.S * ts.S
+    rows = {}
+    for name in ("splat_fwd", "splat_bwd"):
+        flops = FLOP_PER_PAIR[name] * pairs
+        tfl = flops / (kt[name] * 1e-6) / 1e12
+        rows[name] = dict(us=kt[name], tflops=tfl, frac=tfl / PEAK_FP32_TFLOPS)
+    dom = max(("splat_fwd", "splat_bwd"), key=lambda n: kt[n])
+    roofline = dict(bound="valu", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
+                    unit="TFLOP/s", frac=rows[dom]["frac"], traffic=None,
+                    flops_per_launch=FLOP_PER_PAIR[dom] * pairs, pairs_per_launch=pairs,
+                    us_per_launch=kt[dom])
+    # the small configuration (G=2000, 128x128)
+    small = scenes.CONFIGS["c2"]
+    ts2 = build_step(small, torch, TrainStep)
+    its2 = 1000 / time_train(ts2, 1000, 50, torch)
+    fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(cfg, args.cpu_seconds, torch)
+    out = {
+        "metric": METRIC,
+        "value": its,
+        "unit": "it/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": train_s / args.steps * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": f"{cfg.name}: training step, G={cfg.G} "
+                               f"{'clustered' if cfg.means == 'clustered' else 'uniform'} "
+                               f"gaussians, {cfg.W}x{cfg.H}, K={cfg.K}, S={cfg.S}, k={cfg.k}, "
+                               f"{len(ts.cams)} orbit cameras round-robin, one per step",
+                   "G": cfg.G, "W": cfg.W, "H": cfg.H, "K": cfg.K, "S": cfg.S},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": {
+            f"{cfg.name}_fwd_fps": fps,
+            f"{cfg.name}_loss_after_steps": loss_last,
+            "kernel_us": kt,
+            "kernel_roofline": rows,
+            "overflow_tiles": int((ts.ncand > ts.K).sum()),
+            "pairs_kept": int(ts.count.long().sum()),
+            "candidates": int(ts.ncand.long().sum()),
+            "c2_train_its": its2,
+            "c2_fwd_fps": fps2,
+            "c2_note": "G=2000 128x128 fp32 (render operands not rounded to bf16)",
+        },
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

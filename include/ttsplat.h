@@ -14,16 +14,21 @@
  *   params [G,14] fp32 row-major, columns mx,my,mz, qw,qx,qy,qz, lx,ly,lz, cr,cg,cb, op
  *                 (tools/resident_traced.py:91, the fused-Adam [G,14] block :233-235)
  *   camera [16]   fp32: R_v row-major (9), t_v (3), fx, fy, cx, cy  (world->camera, OpenCV)
- *   proj   [G,12] fp32 per-gaussian record written by tts_geom_fwd:
+ *   proj   [G,12] fp32 per-gaussian record written by tts_geom_fwd, 16-byte aligned:
  *                 0 mu_x, 1 mu_y, 2 a, 3 b, 4 c (conic = Sigma2d^-1), 5 depth,
  *                 6..8 color_o = keep*sigmoid(op)*color, 9 o_col = keep*sigmoid(op),
  *                 10 sigmoid(op), 11 zero
  *   keep   [G]    uint8, depth > near
  *   bins   idx[T,K] int32 (0 in empty slots), valid[T,K] uint8; tiles row-major, T = (H/S)*(W/S)
+ *   inv    [G,9]  int32 inverse bin table: inv[g][j] = t*K + slot of gaussian g in the tile it
+ *                 reaches through stencil index j, or -1 (the slot table of
+ *                 tools/m9_scatter_oracle.py:20-32, indexed by stencil position)
  *   image  [H,W,3] fp32 row-major; den [H,W] fp32 (WSR denominator sum(w*oc) + w_b)
  *   bg     [4]    fp32: w_b (already softplus'ed), c_b r, g, b
- *   grad9  [G,9]  fp32 per-gaussian gradient of (a, b, c, mu_x, mu_y, col_o r,g,b, o_col)
- *                 (the scatter layout of tools/resident_traced.py:383-395)
+ *   gslot  [T,K,9] fp32 per-slot gradient of (a, b, c, mu_x, mu_y, col_o r,g,b, o_col): the
+ *                 concatenated per-slot outputs [gct|gmt|gcol|goc] of tools/resident_traced.py:387-388
+ *   grad9  [G,9]  fp32 per-gaussian sum of gslot over the gaussian's slots
+ *                 (the scatter output of tools/resident_traced.py:383-395 / :718-727)
  *   theta  [T,6,K] fp32 monomial-major theta_u, col [T,K,3], oc [T,K] (tools/m4_train_binned.py:130-143)
  */
 #ifndef TTSPLAT_H
@@ -43,7 +48,7 @@ extern "C" {
 #define TTS_EK (-3)         /* K outside [1, 512] */
 #define TTS_EWORKSPACE (-4) /* workspace missing or too small */
 #define TTS_ESPAN (-5)      /* quantised-distance span outside [1, 8192] */
-#define TTS_EG (-6)         /* G above 2^30 */
+#define TTS_EG (-6)         /* G above 2^30 (2^28 for binning) */
 #define TTS_ERADIUS (-7)    /* stencil radius other than 1 */
 
 /* Library version, (major << 16) | minor. */
@@ -78,15 +83,20 @@ size_t tts_bin_workspace_bytes(int G, int H, int W, int S);
 /* Fixed-budget spatial-hash binning, R = 1: each gaussian is hashed to one S x S cell, offered
  * to the 3x3 tiles around it, and each tile keeps the K candidates nearest its centre.
  * Replaces tools/m4_train_binned.py:75-127 (assign_bins) and the dense device binning of
- * tools/bin_device.py:140-187.  mu2d[g*mu_stride + {0,1}], keep[g*keep_stride].
- * Order inside a tile is by (clamp(int64(dist2), 0, span-1), stencil index j, gaussian id),
- * i.e. the reference's sort key with ties in its concatenation order; span = 2048 at S = 16.
- * Writes idx[T,K], valid[T,K]; count[T] (kept per tile) and ncand[T] (candidates per tile)
- * are optional (may be NULL). */
+ * tools/bin_device.py:140-187 (with its inverse table, :219-276).  mu2d[g*mu_stride + {0,1}],
+ * keep[g*keep_stride].  Order inside a tile is by (clamp(int64(dist2), 0, span-1), stencil
+ * index j, gaussian id), i.e. the reference's sort key with ties in its concatenation order;
+ * span = 2048 at S = 16.  Writes idx[T,K], valid[T,K]; count[T] (kept per tile), ncand[T]
+ * (candidates per tile) and inv[G,9] are optional (may be NULL). */
 int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                     int G, int H, int W, int S, int R, int K, int span,
-                    int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand,
+                    int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Tile ids ordered by kept count, heaviest first (counting sort of count[T], values in [0,K]).
+ * Handing it to tts_splat_fwd / tts_splat_bwd makes the expensive tiles start first.  No
+ * counterpart in the reference (whose tiles are batched matmuls of equal shape). */
+int tts_tile_order(const int32_t* count, int T, int K, int32_t* order, hipStream_t stream);
 
 /* ------------------------------------------------------------------- splat ---------- */
 
@@ -101,9 +111,9 @@ int tts_theta_u_gathered(const float* proj, const int32_t* idx, const uint8_t* v
  * u = Phi.theta_u, w = relu(u)^2, C = (sum w col + w_b c_b) / (sum w oc + w_b), written
  * straight into the image.  Replaces tools/bh_views.py:65-71 on _operands
  * (tools/m4_train_binned.py:189-212) and the device chain tools/resident_traced.py:358-370.
- * den may be NULL (it is needed by tts_splat_bwd). */
+ * den may be NULL (it is needed by tts_splat_bwd).  order (tts_tile_order) may be NULL. */
 int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
-                  int H, int W, int S, int K, float k, const float* bg,
+                  const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
                   float* image, float* den, hipStream_t stream);
 
 /* Splat forward from pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K].
@@ -113,24 +123,36 @@ int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc,
                         float* image, float* den, hipStream_t stream);
 
 /* Fused binned splat backward: given dL/dimage, recompute w per (pixel, slot), contract over
- * the tile's pixels per slot, apply the theta backward and add each slot's gradient into
- * grad9[G,9] (atomics; grad9 must be zeroed by the caller).  gwb (dL/dw_b, accumulated) may
- * be NULL.  Replaces WSRPolySplatHot.backward (spike/backward.py:42-58), render_bwd +
- * theta_bwd (tools/resident_traced.py:60-88) and the slot->gaussian scatter
- * (:383-395 device, :718-727 host). */
+ * the tile's pixels per slot and apply the theta backward; each valid slot's 9 gradients are
+ * stored to gslot[T,K,9] (entries of invalid slots are left untouched).  gwb, if not NULL,
+ * receives per-tile partials of dL/dw_b ([T], the caller sums them).  Replaces
+ * WSRPolySplatHot.backward (spike/backward.py:42-58) and render_bwd + theta_bwd
+ * (tools/resident_traced.py:60-88).  order (tts_tile_order) may be NULL. */
 int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
-                  int H, int W, int S, int K, float k, const float* bg,
+                  const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
                   const float* image, const float* den, const float* gimage,
-                  float* grad9, float* gwb, hipStream_t stream);
+                  float* gslot, float* gwb, hipStream_t stream);
 
 /* Splat backward on pre-gathered operands: writes per-slot gtheta[T,6,K], gcol[T,K,3],
- * goc[T,K] (overwritten) and accumulates gwb.  Replaces _DevRenderBinned.backward,
- * tools/m4_train_binned.py:168-186. */
+ * goc[T,K] (overwritten) and per-tile dL/dw_b partials gwb[T] (may be NULL).  Replaces
+ * _DevRenderBinned.backward, tools/m4_train_binned.py:168-186. */
 int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc,
                         int H, int W, int S, int K, const float* bg,
                         const float* image, const float* den, const float* gimage,
                         float* gtheta, float* gcol, float* goc, float* gwb,
                         hipStream_t stream);
+
+/* Slot -> gaussian reduce: grad9[g] = sum over the gaussian's slots of gslot, gathered through
+ * inv in stencil order (deterministic, no atomics).  Replaces the device gather-reduce
+ * tools/resident_traced.py:383-395 (gather_reduce, tools/m9_scatter_oracle.py:35-42). */
+int tts_slot_reduce(const float* gslot, const int32_t* inv, int G, float* grad9,
+                    hipStream_t stream);
+
+/* Slot -> gaussian reduce for bins without an inverse table: grad9 (zeroed by the caller)
+ * += gslot of every valid slot, with float atomics.  Replaces the host index_add of
+ * tools/resident_traced.py:718-727. */
+int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* valid, int T, int K,
+                     float* grad9, hipStream_t stream);
 
 /* -------------------------------------------------------------------- loss ---------- */
 
@@ -165,12 +187,12 @@ int tts_adam_advance(int32_t* step, float beta1, float beta2, hipStream_t stream
 int tts_adam(float* params, float* m, float* v, const float* grad, const float* lr, int G,
              const int32_t* step, float beta1, float beta2, float eps, hipStream_t stream);
 
-/* Fused geometry backward + Adam for one step: grad9 -> 14 gradients -> Adam update of
- * params/m/v; grad9 is zeroed afterwards for the next step's atomics.  gparams (the 14
- * gradients) may be NULL.  Replaces tools/resident_traced.py:397-427 + :739-740. */
+/* Fused slot reduce + geometry backward + Adam for one step: gslot gathered through inv ->
+ * 14 gradients -> Adam update of params/m/v.  gparams (the 14 gradients) may be NULL.
+ * Replaces tools/resident_traced.py:383-427 (scatter_dev + geom_bwd) + :739-740 (adam_fused). */
 int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, float blur,
-                      float* grad9, float* gparams, float* m, float* v, const float* lr,
-                      const int32_t* step, float beta1, float beta2, float eps,
+                      const float* gslot, const int32_t* inv, float* gparams, float* m, float* v,
+                      const float* lr, const int32_t* step, float beta1, float beta2, float eps,
                       hipStream_t stream);
 
 /* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */

@@ -83,23 +83,32 @@ def test_adam_matches_torch():
 
 
 def test_geom_bwd_adam_fused_equals_separate():
+    """slot gather-reduce + geometry bwd + Adam in one kernel == the three separate ops."""
     cfg, P, cam = config_inputs("c1_ref")
-    grad9 = torch.randn(cfg.G, 9, generator=torch.Generator().manual_seed(2)).cuda()
     camb = cam.device_block("cuda")
+    proj, keep = kernels.geom_fwd(P.cuda(), camb)
+    inv = torch.empty(cfg.G, 9, device="cuda", dtype=torch.int32)
+    idx, valid, _, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, cfg.K,
+                                           cfg.span, inv=inv)
+    T = idx.shape[0]
+    gslot = torch.randn(T, cfg.K, 9, generator=torch.Generator().manual_seed(2)).cuda()
     lr = torch.full((14,), 1e-3, device="cuda")
     # separate
     p1 = P.cuda().clone(); m1 = torch.zeros_like(p1); v1 = torch.zeros_like(p1)
     s1 = kernels.adam_state("cuda")
-    gP = kernels.geom_bwd(p1, camb, grad9)
+    gP = kernels.geom_bwd(p1, camb, kernels.slot_reduce(gslot, inv))
     kernels.adam_advance(s1)
     kernels.adam(p1, m1, v1, gP, lr, s1)
     # fused
     p2 = P.cuda().clone(); m2 = torch.zeros_like(p2); v2 = torch.zeros_like(p2)
     s2 = kernels.adam_state("cuda")
-    g9 = grad9.clone()
     gP2 = torch.empty_like(p2)
     kernels.adam_advance(s2)
-    kernels.geom_bwd_adam(p2, camb, g9, m2, v2, lr, s2, gparams=gP2)
+    kernels.geom_bwd_adam(p2, camb, gslot, inv, m2, v2, lr, s2, gparams=gP2)
     assert max_abs(gP, gP2) == 0.0
     assert max_abs(p1, p2) <= 1e-6
-    assert float(g9.abs().max()) == 0.0          # grad9 reset for the next step's atomics
+    # the reduce equals the oracle's index_add over the valid slots
+    ref = torch.zeros(cfg.G, 9, dtype=torch.float64).index_add_(
+        0, idx.cpu().long().reshape(-1)[valid.cpu().reshape(-1).bool()],
+        gslot.cpu().double().reshape(-1, 9)[valid.cpu().reshape(-1).bool()])
+    assert rel_l2(kernels.slot_reduce(gslot, inv), ref) <= 1e-6

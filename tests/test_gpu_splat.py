@@ -23,8 +23,9 @@ def setup(name, G=None, k=None):
     k = cfg.k if k is None else k
     camera = cam.device_block("cuda")
     proj, keep = kernels.geom_fwd(P.cuda(), camera)
+    setup.inv = torch.empty(cfg.G, 9, device="cuda", dtype=torch.int32)
     idx, valid, _, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, cfg.K,
-                                           cfg.span)
+                                           cfg.span, inv=setup.inv)
     bg = torch.tensor([float(torch.nn.functional.softplus(torch.tensor(-3.0))), 1.0, 1.0, 1.0],
                       device="cuda")
     bins = (idx.cpu().long(), valid.cpu().bool())
@@ -63,10 +64,14 @@ def test_splat_bwd_param_grads(name, k):
     g = torch.Generator().manual_seed(7)
     R = torch.randn(cfg.H, cfg.W, 3, generator=g)
     img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
-    grad9 = torch.zeros(cfg.G, 9, device="cuda")
-    gwb = torch.zeros(1, device="cuda")
-    kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R.cuda(), grad9,
-                      gwb)
+    gwb = torch.zeros(tmap.T, device="cuda")
+    gslot = kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R.cuda(),
+                              gwb=gwb)
+    grad9 = kernels.slot_reduce(gslot, setup.inv)
+    # the atomic scatter (bins without an inverse table) gives the same sums
+    grad9_sc = kernels.slot_scatter(gslot, idx, valid, cfg.G)
+    assert rel_l2(grad9_sc, grad9) <= 1e-6
+    gwb = gwb.sum()
     gP = kernels.geom_bwd(P.cuda(), camera, grad9).cpu()
     Pr = P.clone().requires_grad_(True)
     ref = osplat.render_binned(Pr, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
@@ -125,3 +130,36 @@ def test_render_binned_device_autograd():
     assert max_abs(img, ref) <= 1e-4
     (ref * R).sum().backward()
     assert rel_l2(m.params.grad, Pr.grad) <= 1e-3
+
+
+def test_inverse_table_matches_bins():
+    """inv[g][j] lists exactly the valid slots holding g (tools/m9_scatter_oracle.py:20-32)."""
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c4")
+    inv = setup.inv.cpu().long()
+    idx_c, val_c = bins
+    flat = torch.nonzero(val_c.reshape(-1)).flatten()
+    ent = inv[inv >= 0]
+    assert torch.equal(torch.sort(ent).values, flat)                 # every valid slot once
+    g_of = idx_c.reshape(-1)[ent]
+    rows = torch.nonzero(inv >= 0)[:, 0]
+    assert torch.equal(g_of, rows)                                   # slot holds that gaussian
+    # the stencil index: tile of the slot relative to the gaussian's cell
+    S = cfg.S
+    mu = proj[:, 0:2].cpu()
+    cx = (mu[:, 0] / S).floor().long().clamp(0, tmap.ntx - 1)
+    cy = (mu[:, 1] / S).floor().long().clamp(0, tmap.nty - 1)
+    gj = torch.nonzero(inv >= 0)
+    t = inv[gj[:, 0], gj[:, 1]] // cfg.K
+    j = ((t // tmap.ntx) - cy[gj[:, 0]] + 1) * 3 + ((t % tmap.ntx) - cx[gj[:, 0]] + 1)
+    assert torch.equal(j, gj[:, 1])
+
+
+def test_backward_is_deterministic():
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c3")
+    R = torch.randn(cfg.H, cfg.W, 3, generator=torch.Generator().manual_seed(9)).cuda()
+    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
+    outs = []
+    for _ in range(2):
+        gslot = kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R)
+        outs.append(kernels.geom_bwd(P.cuda(), camera, kernels.slot_reduce(gslot, setup.inv)))
+    assert torch.equal(outs[0], outs[1])

@@ -261,11 +261,58 @@ __global__ __launch_bounds__(256) void k_adam(float* __restrict__ params, float*
   v[i] = vv;
 }
 
+// Sum of one gaussian's slot gradients, gathered through the inverse bin table inv[g][0..9)
+// (tile*K + slot, or -1) in stencil order: the slot->gaussian reduce of
+// tools/m9_scatter_oracle.py:35-42 / tools/resident_traced.py:383-395, without atomics and in a
+// fixed order (so the result is reproducible bit for bit).
+__device__ __forceinline__ void gather_slot_grads(const float* __restrict__ gslot,
+                                                  const int32_t* __restrict__ inv, int g,
+                                                  float* gin) {
+  int e[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) e[j] = inv[(int64_t)g * 9 + j];
+#pragma unroll
+  for (int c = 0; c < 9; ++c) gin[c] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    if (e[j] >= 0) {
+      const float* src = gslot + (int64_t)e[j] * 9;
+#pragma unroll
+      for (int c = 0; c < 9; ++c) gin[c] += src[c];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_slot_reduce(const float* __restrict__ gslot,
+                                                     const int32_t* __restrict__ inv, int G,
+                                                     float* __restrict__ grad9) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  float gin[9];
+  gather_slot_grads(gslot, inv, g, gin);
+#pragma unroll
+  for (int c = 0; c < 9; ++c) grad9[(int64_t)g * 9 + c] = gin[c];
+}
+
+// Slot->gaussian reduce for bins that come without an inverse table (e.g. handed in by a
+// caller): float atomics, order-dependent rounding.  grad9 must be zeroed first.
+__global__ __launch_bounds__(256) void k_slot_scatter(const float* __restrict__ gslot,
+                                                      const int32_t* __restrict__ idx,
+                                                      const uint8_t* __restrict__ valid,
+                                                      int64_t TK, float* __restrict__ grad9) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= TK || !valid[i]) return;
+  float* dst = grad9 + (int64_t)idx[i] * 9;
+#pragma unroll
+  for (int c = 0; c < 9; ++c) unsafeAtomicAdd(dst + c, gslot[i * 9 + c]);
+}
+
 __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     float* __restrict__ params, int G, const float* __restrict__ camera, float near_z, float blur,
-    float* __restrict__ grad9, float* __restrict__ gparams, float* __restrict__ m,
-    float* __restrict__ v, const float* __restrict__ lr, const int32_t* __restrict__ step,
-    float b1, float b2, float eps) {
+    const float* __restrict__ gslot, const int32_t* __restrict__ inv,
+    float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
+    const float* __restrict__ lr, const int32_t* __restrict__ step, float b1, float b2,
+    float eps) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const Camera cam = load_camera(camera);
@@ -276,11 +323,7 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
   GeoState s;
   geo_forward(pl, cam, near_z, blur, s);
   float gin[9], gout[14];
-#pragma unroll
-  for (int i = 0; i < 9; ++i) {
-    gin[i] = grad9[(int64_t)g * 9 + i];
-    grad9[(int64_t)g * 9 + i] = 0.0f;
-  }
+  gather_slot_grads(gslot, inv, g, gin);
   geo_backward(pl, cam, s, gin, gout);
   const float* f = reinterpret_cast<const float*>(step);
   const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
@@ -318,7 +361,7 @@ const char* tts_strerror(int code) {
     case TTS_EK: return "K must be in [1, 512]";
     case TTS_EWORKSPACE: return "workspace missing or too small";
     case TTS_ESPAN: return "span must be in [1, 8192]";
-    case TTS_EG: return "G must be below 2^30";
+    case TTS_EG: return "G must be below 2^30 (at most 2^28 for binning)";
     case TTS_ERADIUS: return "only stencil radius R = 1 is supported";
     default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }
@@ -359,15 +402,34 @@ int tts_adam(float* params, float* m, float* v, const float* grad, const float* 
 }
 
 int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, float blur,
-                      float* grad9, float* gparams, float* m, float* v, const float* lr,
-                      const int32_t* step, float beta1, float beta2, float eps,
+                      const float* gslot, const int32_t* inv, float* gparams, float* m, float* v,
+                      const float* lr, const int32_t* step, float beta1, float beta2, float eps,
                       hipStream_t stream) {
-  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !m || !v || !lr || !step)))
+  if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !m || !v || !lr || !step)))
     return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_adam<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, grad9,
-                                                      gparams, m, v, lr, step, beta1, beta2, eps);
+  k_geom_bwd_adam<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, gslot,
+                                                      inv, gparams, m, v, lr, step, beta1, beta2,
+                                                      eps);
+  return launch_status();
+}
+
+int tts_slot_reduce(const float* gslot, const int32_t* inv, int G, float* grad9,
+                    hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!gslot || !inv || !grad9))) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_slot_reduce<<<grid1d(G, 256), 256, 0, stream>>>(gslot, inv, G, grad9);
+  return launch_status();
+}
+
+int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* valid, int T, int K,
+                     float* grad9, hipStream_t stream) {
+  if (T < 0 || K < 0 || (T * K > 0 && (!gslot || !idx || !valid || !grad9))) return TTS_EINVAL;
+  const int64_t TK = (int64_t)T * K;
+  if (TK == 0) return TTS_OK;
+  k_slot_scatter<<<grid1d(TK, 256), 256, 0, stream>>>(gslot, idx, valid, TK, grad9);
   return launch_status();
 }
 

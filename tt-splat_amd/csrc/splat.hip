@@ -13,8 +13,9 @@
 // rows).  Along a pixel row, u = (th0*lx + c1)*lx + c0 with c0, c1 fixed per row, and the
 // theta gradient is gathered as three row moments sum(gu*lx^2), sum(gu*lx), sum(gu), so the
 // inner loop costs 16 VALU ops per (pixel, slot) pair.  Each slot's 10 partial sums are
-// combined in LDS, pushed through the theta backward, and added into grad9[g] with one
-// hardware float atomic per value (a gaussian lives in at most 9 tiles at R = 1).
+// combined in LDS and pushed through the theta backward; the slot's 9 gradients are stored to
+// gslot[T,K,9] (no atomics: the per-gaussian sum over its <= 9 slots is a gather through the
+// inverse bin table, in a fixed order, done by the geometry backward).
 
 #include "tts_common.h"
 
@@ -27,6 +28,7 @@ struct SlotLDS {
   float4* tb;  // theta_u 4..5, -, -
   float4* cl;  // col_o r,g,b, o_col
   int* gid;    // gaussian id (proj mode) or original slot (theta mode)
+  int* sid;    // original slot index of the compacted entry
 };
 
 __device__ __forceinline__ SlotLDS carve_slots(unsigned char* base, int K) {
@@ -35,10 +37,11 @@ __device__ __forceinline__ SlotLDS carve_slots(unsigned char* base, int K) {
   s.tb = s.ta + K;
   s.cl = s.tb + K;
   s.gid = reinterpret_cast<int*>(s.cl + K);
+  s.sid = s.gid + K;
   return s;
 }
 
-__device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (3 * 16 + 4); }
+__device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (3 * 16 + 8); }
 
 // Tile-local theta_u for one gaussian record (tools/m4_train_binned.py:130-143).
 __device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
@@ -74,6 +77,7 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
       sl.tb[pos] = tb;
       sl.cl[pos] = cl;
       sl.gid[pos] = g;
+      sl.sid[pos] = s;
     }
     base += total;
   }
@@ -92,6 +96,7 @@ __device__ __forceinline__ void load_slots_theta(const float* __restrict__ theta
     const float* c = col + ((int64_t)t * K + s) * 3;
     sl.cl[s] = make_float4(c[0], c[1], c[2], oc[(int64_t)t * K + s]);
     sl.gid[s] = s;
+    sl.sid[s] = s;
   }
 }
 
@@ -99,14 +104,14 @@ template <int S, bool FROM_PROJ>
 __global__ __launch_bounds__(256) void k_splat_fwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
     const uint8_t* __restrict__ valid, const float* __restrict__ theta,
-    const float* __restrict__ col, const float* __restrict__ oc, int ntx, int W, int K,
-    float inv_k, const float* __restrict__ bg, float* __restrict__ image,
-    float* __restrict__ den_out) {
+    const float* __restrict__ col, const float* __restrict__ oc,
+    const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
+    const float* __restrict__ bg, float* __restrict__ image, float* __restrict__ den_out) {
   constexpr int PPT = S * S / 256;  // pixels per thread
   extern __shared__ unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   const SlotLDS sl = carve_slots(s_dyn, K);
-  const int t = blockIdx.x;
+  const int t = order ? order[blockIdx.x] : blockIdx.x;
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * S, oy = ty * S;
   int n;
@@ -158,15 +163,17 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
 }
 
 template <int S, bool FROM_PROJ>
-__global__ __launch_bounds__(256) void k_splat_bwd(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_splat_bwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
     const uint8_t* __restrict__ valid, const float* __restrict__ theta,
-    const float* __restrict__ col, const float* __restrict__ oc, int ntx, int W, int K,
-    float inv_k, const float* __restrict__ bg, const float* __restrict__ image,
-    const float* __restrict__ den, const float* __restrict__ gimage, float* __restrict__ grad9,
+    const float* __restrict__ col, const float* __restrict__ oc,
+    const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
+    const float* __restrict__ bg, const float* __restrict__ image,
+    const float* __restrict__ den, const float* __restrict__ gimage, float* __restrict__ gslot,
     float* __restrict__ gtheta, float* __restrict__ gcol, float* __restrict__ goc,
     float* __restrict__ gwb) {
   constexpr int P = S * S;
+  constexpr int PPT = P / 256;
   extern __shared__ unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   __shared__ float s_ftmp[4];
@@ -174,9 +181,22 @@ __global__ __launch_bounds__(256) void k_splat_bwd(
   float4* s_px = reinterpret_cast<float4*>(s_dyn + slot_lds_bytes(K) + (16 - slot_lds_bytes(K) % 16) % 16);
   float* s_red = reinterpret_cast<float*>(s_px + P);  // [10][256]
 
-  const int t = blockIdx.x;
+  const int t = order ? order[blockIdx.x] : blockIdx.x;
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * S, oy = ty * S;
+  // Issue this thread's pixel loads first: their latency overlaps the slot prologue.
+  float pg[PPT][3], pc[PPT][3], pd[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int p = threadIdx.x + 256 * i;
+    const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
+    pd[i] = den[pix];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      pg[i][c] = gimage[pix * 3 + c];
+      pc[i][c] = image[pix * 3 + c];
+    }
+  }
   int n;
   if constexpr (FROM_PROJ) {
     n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
@@ -185,20 +205,19 @@ __global__ __launch_bounds__(256) void k_splat_bwd(
     n = K;
   }
   // Per-pixel WSR backward: gnum = gC/den, gden = -(gC . C)/den.
-  const float wb = bg[0];
+  const float bg1 = bg[1], bg2 = bg[2], bg3 = bg[3];
   float wpart = 0.0f;
-  for (int p = threadIdx.x; p < P; p += 256) {
-    const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
-    const float inv = 1.0f / den[pix];
-    const float g0 = gimage[pix * 3 + 0], g1 = gimage[pix * 3 + 1], g2 = gimage[pix * 3 + 2];
-    const float c0 = image[pix * 3 + 0], c1 = image[pix * 3 + 1], c2 = image[pix * 3 + 2];
-    const float4 q = make_float4(g0 * inv, g1 * inv, g2 * inv, -(g0 * c0 + g1 * c1 + g2 * c2) * inv);
-    s_px[p] = q;
-    wpart += q.x * bg[1] + q.y * bg[2] + q.z * bg[3] + q.w;
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const float inv = 1.0f / pd[i];
+    const float4 q = make_float4(pg[i][0] * inv, pg[i][1] * inv, pg[i][2] * inv,
+                                 -(pg[i][0] * pc[i][0] + pg[i][1] * pc[i][1] + pg[i][2] * pc[i][2]) * inv);
+    s_px[threadIdx.x + 256 * i] = q;
+    wpart += q.x * bg1 + q.y * bg2 + q.z * bg3 + q.w;
   }
-  if (gwb) {
+  if (gwb) {  // per-tile partial of dL/dw_b (summed by the caller)
     const float tot = block_sum256(wpart, s_ftmp);
-    if (threadIdx.x == 0) unsafeAtomicAdd(gwb, tot);
+    if (threadIdx.x == 0) gwb[t] = tot;
   }
   __syncthreads();
 
@@ -227,22 +246,27 @@ __global__ __launch_bounds__(256) void k_splat_bwd(
         const float cc1 = A.z * ly + A.w;
         float m0 = 0.f, m1 = 0.f, m2 = 0.f;
         const float4* row = s_px + y * S;
+        // 8-pixel chunks keep the in-flight LDS operands (and so the VGPR count) bounded
+#pragma unroll 1
+        for (int xb = 0; xb < S; xb += 8) {
+          const float xbf = (float)xb;
 #pragma unroll
-        for (int x = 0; x < S; ++x) {
-          const float lx = (float)x + 0.5f;
-          const float u = (A.x * lx + cc1) * lx + cc0;
-          const float r = fmaxf(u, 0.0f);
-          const float w = r * r;
-          const float4 q = row[x];
-          const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
-          const float gu = r * gw;  // half of dL/du
-          gr += w * q.x;
-          gg += w * q.y;
-          gb += w * q.z;
-          go += w * q.w;
-          m0 += gu * (lx * lx);
-          m1 += gu * lx;
-          m2 += gu;
+          for (int x8 = 0; x8 < 8; ++x8) {
+            const float lx = xbf + ((float)x8 + 0.5f);
+            const float u = (A.x * lx + cc1) * lx + cc0;
+            const float r = fmaxf(u, 0.0f);
+            const float w = r * r;
+            const float4 q = row[xb + x8];
+            const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
+            const float gu = r * gw;  // half of dL/du
+            gr += w * q.x;
+            gg += w * q.y;
+            gb += w * q.z;
+            go += w * q.w;
+            m0 += gu * (lx * lx);
+            m1 += gu * lx;
+            m2 += gu;
+          }
         }
         g0 += m0;
         g2 += ly * m1;
@@ -286,16 +310,16 @@ __global__ __launch_bounds__(256) void k_splat_bwd(
         const float gc = q1 - 2.f * my * q4 + my * my * q5;
         const float gmx = -2.f * a * q3 - 2.f * b * q4 + (2.f * a * mx + 2.f * b * my) * q5;
         const float gmy = -2.f * b * q3 - 2.f * c * q4 + (2.f * b * mx + 2.f * c * my) * q5;
-        float* dst = grad9 + (int64_t)g * 9;
-        unsafeAtomicAdd(dst + 0, ga);
-        unsafeAtomicAdd(dst + 1, gbv);
-        unsafeAtomicAdd(dst + 2, gc);
-        unsafeAtomicAdd(dst + 3, gmx);
-        unsafeAtomicAdd(dst + 4, gmy);
-        unsafeAtomicAdd(dst + 5, gr);
-        unsafeAtomicAdd(dst + 6, gg);
-        unsafeAtomicAdd(dst + 7, gb);
-        unsafeAtomicAdd(dst + 8, go);
+        float* dst = gslot + ((int64_t)t * K + sl.sid[s]) * 9;
+        dst[0] = ga;
+        dst[1] = gbv;
+        dst[2] = gc;
+        dst[3] = gmx;
+        dst[4] = gmy;
+        dst[5] = gr;
+        dst[6] = gg;
+        dst[7] = gb;
+        dst[8] = go;
       } else {
         float* th = gtheta + (int64_t)t * 6 * K;
         th[s] = g0; th[K + s] = g1; th[2 * K + s] = g2;
@@ -338,44 +362,46 @@ inline int check_tile(int H, int W, int S, int K) {
   return TTS_OK;
 }
 
-inline size_t fwd_lds(int K) { return (size_t)K * (3 * 16 + 4); }
+inline size_t fwd_lds(int K) { return (size_t)K * (3 * 16 + 8); }
 inline size_t bwd_lds(int K, int S) {
-  size_t a = (size_t)K * (3 * 16 + 4);
+  size_t a = (size_t)K * (3 * 16 + 8);
   a += (16 - a % 16) % 16;
   return a + (size_t)S * S * 16 + 10 * 256 * sizeof(float);
 }
 
 template <bool FROM_PROJ>
 int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
-               const float* col, const float* oc, int H, int W, int S, int K, float k,
+               const float* col, const float* oc, const int32_t* order, int H, int W, int S, int K,
+               float k,
                const float* bg, float* image, float* den, hipStream_t stream) {
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16)
-    k_splat_fwd<16, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(proj, idx, valid, theta, col, oc,
-                                                               ntx, W, K, inv_k, bg, image, den);
+    k_splat_fwd<16, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(
+        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
   else
-    k_splat_fwd<32, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(proj, idx, valid, theta, col, oc,
-                                                               ntx, W, K, inv_k, bg, image, den);
+    k_splat_fwd<32, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(
+        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
   return launch_status();
 }
 
 template <bool FROM_PROJ>
 int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
-               const float* col, const float* oc, int H, int W, int S, int K, float k,
+               const float* col, const float* oc, const int32_t* order, int H, int W, int S, int K,
+               float k,
                const float* bg, const float* image, const float* den, const float* gimage,
-               float* grad9, float* gtheta, float* gcol, float* goc, float* gwb,
+               float* gslot, float* gtheta, float* gcol, float* goc, float* gwb,
                hipStream_t stream) {
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16)
     k_splat_bwd<16, FROM_PROJ><<<T, 256, bwd_lds(K, 16), stream>>>(
-        proj, idx, valid, theta, col, oc, ntx, W, K, inv_k, bg, image, den, gimage, grad9, gtheta,
-        gcol, goc, gwb);
+        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
+        gtheta, gcol, goc, gwb);
   else
     k_splat_bwd<32, FROM_PROJ><<<T, 256, bwd_lds(K, 32), stream>>>(
-        proj, idx, valid, theta, col, oc, ntx, W, K, inv_k, bg, image, den, gimage, grad9, gtheta,
-        gcol, goc, gwb);
+        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
+        gtheta, gcol, goc, gwb);
   return launch_status();
 }
 
@@ -397,14 +423,14 @@ int tts_theta_u_gathered(const float* proj, const int32_t* idx, const uint8_t* v
   return launch_status();
 }
 
-int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, int H, int W,
-                  int S, int K, float k, const float* bg, float* image, float* den,
-                  hipStream_t stream) {
+int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
+                  const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
+                  float* image, float* den, hipStream_t stream) {
   const int e = check_tile(H, W, S, K);
   if (e) return e;
   if (!proj || !idx || !valid || !bg || !image) return TTS_EINVAL;
-  return launch_fwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, H, W, S, K, k, bg, image,
-                          den, stream);
+  return launch_fwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
+                          image, den, stream);
 }
 
 int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc, int H, int W,
@@ -413,18 +439,19 @@ int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc, i
   const int e = check_tile(H, W, S, K);
   if (e) return e;
   if (!theta || !col || !oc || !bg || !image) return TTS_EINVAL;
-  return launch_fwd<false>(nullptr, nullptr, nullptr, theta, col, oc, H, W, S, K, 1.0f, bg,
-                           image, den, stream);
+  return launch_fwd<false>(nullptr, nullptr, nullptr, theta, col, oc, nullptr, H, W, S, K, 1.0f,
+                           bg, image, den, stream);
 }
 
-int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, int H, int W,
-                  int S, int K, float k, const float* bg, const float* image, const float* den,
-                  const float* gimage, float* grad9, float* gwb, hipStream_t stream) {
+int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
+                  const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
+                  const float* image, const float* den, const float* gimage, float* gslot,
+                  float* gwb, hipStream_t stream) {
   const int e = check_tile(H, W, S, K);
   if (e) return e;
-  if (!proj || !idx || !valid || !bg || !image || !den || !gimage || !grad9) return TTS_EINVAL;
-  return launch_bwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, H, W, S, K, k, bg, image,
-                          den, gimage, grad9, nullptr, nullptr, nullptr, gwb, stream);
+  if (!proj || !idx || !valid || !bg || !image || !den || !gimage || !gslot) return TTS_EINVAL;
+  return launch_bwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
+                          image, den, gimage, gslot, nullptr, nullptr, nullptr, gwb, stream);
 }
 
 int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc, int H, int W,
@@ -435,8 +462,8 @@ int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc, i
   if (e) return e;
   if (!theta || !col || !oc || !bg || !image || !den || !gimage || !gtheta || !gcol || !goc)
     return TTS_EINVAL;
-  return launch_bwd<false>(nullptr, nullptr, nullptr, theta, col, oc, H, W, S, K, 1.0f, bg,
-                           image, den, gimage, nullptr, gtheta, gcol, goc, gwb, stream);
+  return launch_bwd<false>(nullptr, nullptr, nullptr, theta, col, oc, nullptr, H, W, S, K, 1.0f,
+                           bg, image, den, gimage, nullptr, gtheta, gcol, goc, gwb, stream);
 }
 
 }  // extern "C"

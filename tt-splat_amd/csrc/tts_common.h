@@ -41,17 +41,19 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return v;
 }
 
-// Block-wide exclusive prefix sum for blockDim.x == 256 (4 waves).  `tmp` holds 4 ints.
+// Block-wide exclusive prefix sum for blockDim.x == NT (NT/64 waves).  `tmp` holds NT/64 ints.
 // Returns the exclusive prefix of `v`; *total receives the block sum.  Contains barriers:
 // every thread of the block must call it.
-__device__ __forceinline__ int block_excl_scan256(int v, int* tmp, int* total) {
+template <int NT>
+__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
+  constexpr int NW = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int incl = wave_incl_scan(v);
   if (lane == 63) tmp[wave] = incl;
   __syncthreads();
   int base = 0, sum = 0;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) {
+  for (int w = 0; w < NW; ++w) {
     int tw = tmp[w];
     if (w < wave) base += tw;
     sum += tw;
@@ -59,6 +61,10 @@ __device__ __forceinline__ int block_excl_scan256(int v, int* tmp, int* total) {
   __syncthreads();
   *total = sum;
   return base + incl - v;
+}
+
+__device__ __forceinline__ int block_excl_scan256(int v, int* tmp, int* total) {
+  return block_excl_scan<256>(v, tmp, total);
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

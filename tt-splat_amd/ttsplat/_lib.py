@@ -22,15 +22,16 @@ SIGNATURES = {
     "tts_geom_bwd": (_c_int, [_vp, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp]),
     "tts_bin_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "tts_assign_bins": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                 _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+                                 _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "tts_theta_u_gathered": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                       _vp, _vp, _vp, _vp]),
-    "tts_splat_fwd": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp,
-                               _vp, _vp, _vp]),
+    "tts_tile_order": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
+    "tts_splat_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                               _vp, _vp, _vp, _vp]),
     "tts_splat_fwd_theta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                      _vp, _vp]),
-    "tts_splat_bwd": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp,
-                               _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tts_splat_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                               _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_splat_bwd_theta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_loss_workspace_bytes": (_c_size, [_c_int, _c_int]),
@@ -40,7 +41,9 @@ SIGNATURES = {
     "tts_adam": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _vp, _c_float, _c_float, _c_float,
                           _vp]),
     "tts_geom_bwd_adam": (_c_int, [_vp, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp, _vp, _vp,
-                                   _vp, _c_float, _c_float, _c_float, _vp]),
+                                   _vp, _vp, _c_float, _c_float, _c_float, _vp]),
+    "tts_slot_reduce": (_c_int, [_vp, _vp, _c_int, _vp, _vp]),
+    "tts_slot_scatter": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _vp, _vp]),
     "tts_zero": (_c_int, [_vp, _c_i64, _vp]),
 }
 

@@ -144,10 +144,10 @@ class DevRenderBinned(torch.autograd.Function):
     def backward(ctx, gimg):
         th, col, oc, bg, img, den = ctx.saved_tensors
         H, W, S, oc_shape = ctx.meta
-        gwb = torch.zeros(1, device=th.device, dtype=F32)
+        gwb = torch.empty(th.shape[0], device=th.device, dtype=F32)
         gth, gcol, goc = kernels.splat_bwd_theta(th, col, oc, bg, H, W, S, img, den,
                                                  gimg.float().contiguous(), gwb)
-        return gth, gcol, goc.reshape(oc_shape), gwb.reshape(()), None, None, None, None, None
+        return gth, gcol, goc.reshape(oc_shape), gwb.sum(), None, None, None, None, None
 
 
 _DevRenderBinned = DevRenderBinned
@@ -155,15 +155,17 @@ _DevRenderBinned = DevRenderBinned
 
 class BinnedRender(torch.autograd.Function):
     """Whole binned render as one differentiable op of the [G,14] parameter block:
-    geometry -> (given bins) -> fused splat; backward: fused splat bwd with theta bwd and
-    slot->gaussian atomics -> geometry bwd."""
+    geometry -> (given bins) -> fused splat; backward: fused splat bwd with theta bwd into
+    per-slot gradients -> slot->gaussian reduce (through the inverse table when the bins came
+    with one, else an atomic scatter) -> geometry bwd."""
 
     @staticmethod
-    def forward(ctx, P, camera, bg, idx32, v8, H, W, S, k):
+    def forward(ctx, P, camera, bg, idx32, v8, inv, H, W, S, k):
         Pc = P.detach().contiguous()
         proj, keep = kernels.geom_fwd(Pc, camera)
         img, den = kernels.splat_fwd(proj, idx32, v8, bg, H, W, S, k)
         ctx.save_for_backward(Pc, camera, bg, idx32, v8, proj, img, den)
+        ctx.inv = inv
         ctx.meta = (H, W, S, k)
         return img
 
@@ -171,12 +173,17 @@ class BinnedRender(torch.autograd.Function):
     def backward(ctx, gimg):
         Pc, camera, bg, idx32, v8, proj, img, den = ctx.saved_tensors
         H, W, S, k = ctx.meta
-        grad9 = torch.zeros(Pc.shape[0], 9, device=Pc.device, dtype=F32)
-        gbg = torch.zeros(4, device=Pc.device, dtype=F32)
-        kernels.splat_bwd(proj, idx32, v8, bg, H, W, S, k, img, den,
-                          gimg.float().contiguous(), grad9, gbg[0:1])
+        gwb = torch.empty(idx32.shape[0], device=Pc.device, dtype=F32)
+        gslot = kernels.splat_bwd(proj, idx32, v8, bg, H, W, S, k, img, den,
+                                  gimg.float().contiguous(), gwb=gwb)
+        if ctx.inv is not None:
+            grad9 = kernels.slot_reduce(gslot, ctx.inv)
+        else:
+            grad9 = kernels.slot_scatter(gslot, idx32, v8, Pc.shape[0])
         gP = kernels.geom_bwd(Pc, camera, grad9)
-        return gP, None, gbg, None, None, None, None, None, None
+        gbg = torch.zeros(4, device=Pc.device, dtype=F32)
+        gbg[0] = gwb.sum()
+        return gP, None, gbg, None, None, None, None, None, None, None
 
 
 def render_binned_device(model, cam, tmap, R=1, K=128, cached_bins=None, return_bins=False,
@@ -186,14 +193,16 @@ def render_binned_device(model, cam, tmap, R=1, K=128, cached_bins=None, return_
     P = params_of(model)
     dev = P.device
     camera = cam.device_block(dev)
+    inv = None
     if cached_bins is None:
         proj, keep = kernels.geom_fwd(P.detach().contiguous(), camera)
+        inv = torch.empty(P.shape[0], 9, device=dev, dtype=torch.int32)
         idx32, v8, _, _ = kernels.assign_bins(proj[:, 0:2], keep, tmap.H, tmap.W, tmap.S, K,
-                                              tmap.span, R)
+                                              tmap.span, R, inv=inv)
         bins = (idx32.long(), v8.bool())
     else:
         bins = cached_bins
         idx32, v8 = _checked_bins(bins, P.shape[0])
-    img = BinnedRender.apply(P, camera, background(model, dev), idx32, v8, tmap.H, tmap.W,
+    img = BinnedRender.apply(P, camera, background(model, dev), idx32, v8, inv, tmap.H, tmap.W,
                              tmap.S, float(k))
     return (img, bins) if return_bins else img

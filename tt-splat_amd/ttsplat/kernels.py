@@ -63,9 +63,10 @@ def bin_workspace(G, H, W, S, device):
 
 
 def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, idx=None,
-                valid=None, count=None, ncand=None):
+                valid=None, count=None, ncand=None, inv=None):
     """mu2d: [G,2] fp32 (or any [G,>=2] row-contiguous view, e.g. the proj record),
-    keep: [G] uint8 or bool.  Returns idx[T,K] int32, valid[T,K] uint8, count[T], ncand[T]."""
+    keep: [G] uint8 or bool.  Returns idx[T,K] int32, valid[T,K] uint8, count[T], ncand[T];
+    the inverse table inv[G,9] is written when a buffer is passed."""
     G = mu2d.shape[0]
     dev = mu2d.device
     if not mu2d.is_cuda or mu2d.dtype != F32 or mu2d.dim() != 2 or mu2d.shape[1] < 2 \
@@ -85,10 +86,12 @@ def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, i
     require(valid, "valid", U8, (T, K), dev)
     require(count, "count", I32, (T,), dev)
     require(ncand, "ncand", I32, (T,), dev)
+    if inv is not None:
+        require(inv, "inv", I32, (G, 9), dev)
     workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
     call("tts_assign_bins", ptr(mu2d), mu2d.stride(0), ptr(keep), 1, G, H, W, S, R, K, span,
-         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(workspace), workspace.numel(),
-         stream())
+         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(workspace),
+         workspace.numel(), stream())
     return idx, valid, count, ncand
 
 
@@ -120,7 +123,17 @@ def theta_gather(proj, idx, valid, H, W, S, k, theta=None, col=None, oc=None):
     return theta, col, oc
 
 
-def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None):
+def tile_order(count, K, order=None):
+    """Tile ids by kept count, heaviest first (scheduling order for the splat kernels)."""
+    T = count.shape[0]
+    require(count, "count", I32, (T,))
+    order = torch.empty(T, device=count.device, dtype=I32) if order is None else order
+    require(order, "order", I32, (T,), count.device)
+    call("tts_tile_order", ptr(count), T, K, ptr(order), stream())
+    return order
+
+
+def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None):
     dev = proj.device
     _aligned16(require(proj, "proj", F32, (proj.shape[0], 12)), "proj")
     T, K, valid = _bins_check(idx, valid, H, W, S, dev)
@@ -129,12 +142,16 @@ def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None):
     den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
     require(image, "image", F32, (H, W, 3), dev)
     require(den, "den", F32, (H, W), dev)
-    call("tts_splat_fwd", ptr(proj), ptr(idx), ptr(valid), H, W, S, K, float(k), ptr(bg),
-         ptr(image), ptr(den), stream())
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
+    call("tts_splat_fwd", ptr(proj), ptr(idx), ptr(valid), ptr(order), H, W, S, K, float(k),
+         ptr(bg), ptr(image), ptr(den), stream())
     return image, den
 
 
-def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, grad9, gwb=None):
+def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, gslot=None, gwb=None,
+              order=None):
+    """Per-slot gradients gslot[T,K,9] (valid slots written); gwb[T] gets per-tile dL/dw_b."""
     dev = proj.device
     G = proj.shape[0]
     _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
@@ -143,11 +160,41 @@ def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, grad9, gwb=N
     require(image, "image", F32, (H, W, 3), dev)
     require(den, "den", F32, (H, W), dev)
     require(gimage, "gimage", F32, (H, W, 3), dev)
-    require(grad9, "grad9", F32, (G, 9), dev)
+    gslot = torch.zeros(T, K, 9, device=dev, dtype=F32) if gslot is None else gslot
+    require(gslot, "gslot", F32, (T, K, 9), dev)
     if gwb is not None:
-        require(gwb, "gwb", F32, (1,), dev)
-    call("tts_splat_bwd", ptr(proj), ptr(idx), ptr(valid), H, W, S, K, float(k), ptr(bg),
-         ptr(image), ptr(den), ptr(gimage), ptr(grad9), ptr(gwb), stream())
+        require(gwb, "gwb", F32, (T,), dev)
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
+    call("tts_splat_bwd", ptr(proj), ptr(idx), ptr(valid), ptr(order), H, W, S, K, float(k),
+         ptr(bg), ptr(image), ptr(den), ptr(gimage), ptr(gslot), ptr(gwb), stream())
+    return gslot
+
+
+def slot_reduce(gslot, inv, grad9=None):
+    """grad9[G,9] = per-gaussian sum of its slots' gradients (through the inverse table)."""
+    G = inv.shape[0]
+    require(inv, "inv", I32, (G, 9))
+    if gslot.dim() != 3 or gslot.shape[2] != 9:
+        raise ValueError("gslot must be [T,K,9]")
+    require(gslot, "gslot", F32, tuple(gslot.shape), inv.device)
+    grad9 = torch.empty(G, 9, device=inv.device, dtype=F32) if grad9 is None else grad9
+    require(grad9, "grad9", F32, (G, 9), inv.device)
+    call("tts_slot_reduce", ptr(gslot), ptr(inv), G, ptr(grad9), stream())
+    return grad9
+
+
+def slot_scatter(gslot, idx, valid, G, grad9=None):
+    """grad9[G,9] += gradients of every valid slot (float atomics; bins without inv)."""
+    T, K = idx.shape
+    if valid.dtype == torch.bool:
+        valid = valid.view(U8)
+    require(idx, "idx", I32, (T, K))
+    require(valid, "valid", U8, (T, K), idx.device)
+    require(gslot, "gslot", F32, (T, K, 9), idx.device)
+    grad9 = torch.zeros(G, 9, device=idx.device, dtype=F32) if grad9 is None else grad9
+    require(grad9, "grad9", F32, (G, 9), idx.device)
+    call("tts_slot_scatter", ptr(gslot), ptr(idx), ptr(valid), T, K, ptr(grad9), stream())
     return grad9
 
 
@@ -167,6 +214,7 @@ def splat_fwd_theta(theta, col, oc, bg, H, W, S, image=None, den=None):
 
 
 def splat_bwd_theta(theta, col, oc, bg, H, W, S, image, den, gimage, gwb=None):
+    """Per-slot gtheta, gcol, goc; gwb[T] (optional) gets per-tile dL/dw_b partials."""
     dev = theta.device
     T = (H // S) * (W // S)
     K = theta.shape[-1]
@@ -177,6 +225,8 @@ def splat_bwd_theta(theta, col, oc, bg, H, W, S, image, den, gimage, gwb=None):
     require(image, "image", F32, (H, W, 3), dev)
     require(den, "den", F32, (H, W), dev)
     require(gimage, "gimage", F32, (H, W, 3), dev)
+    if gwb is not None:
+        require(gwb, "gwb", F32, (T,), dev)
     gtheta = torch.empty_like(theta)
     gcol = torch.empty_like(col)
     goc = torch.empty_like(oc)
@@ -246,20 +296,24 @@ def adam(params, m, v, grad, lr, step, b1=BETA1, b2=BETA2, eps=EPS):
          stream())
 
 
-def geom_bwd_adam(params, camera, grad9, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
+def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
                   b1=BETA1, b2=BETA2, eps=EPS):
+    """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel."""
     G = params.shape[0]
     dev = params.device
     for t, n in ((params, "params"), (m, "m"), (v, "v")):
         require(t, n, F32, (G, 14), dev)
     require(camera, "camera", F32, (16,), dev)
-    require(grad9, "grad9", F32, (G, 9), dev)
+    require(inv, "inv", I32, (G, 9), dev)
+    if gslot.dim() != 3 or gslot.shape[2] != 9:
+        raise ValueError("gslot must be [T,K,9]")
+    require(gslot, "gslot", F32, tuple(gslot.shape), dev)
     require(lr, "lr", F32, (14,), dev)
     require(step, "step", I32, (4,), dev)
     if gparams is not None:
         require(gparams, "gparams", F32, (G, 14), dev)
-    call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(gparams),
-         ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
+    call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
+         ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
 
 
 def zero_(buf):

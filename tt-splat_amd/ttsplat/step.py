@@ -5,9 +5,9 @@ captures the step as ttnn traces (:551-567) and replays them per iteration (:667
 host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
 host round trip:
 
-    geom_fwd -> assign_bins (4 kernels) -> splat_fwd -> loss_grad (2 kernels)
-             -> splat_bwd (theta bwd + slot->gaussian atomics) -> adam_advance
-             -> geom_bwd_adam (geometry bwd + Adam + grad9 reset)
+    geom_fwd -> assign_bins (4 kernels, + inverse table) -> tile_order -> splat_fwd
+             -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
+             -> adam_advance -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
 captured once per camera into a HIP graph (torch.cuda.CUDAGraph) and replayed.  The step
 counter and Adam bias corrections live in device memory, so replays need no re-capture.
@@ -66,12 +66,14 @@ class TrainStep:
         self.valid = torch.empty(T, K, device=dev, dtype=U8)
         self.count = torch.empty(T, device=dev, dtype=I32)
         self.ncand = torch.empty(T, device=dev, dtype=I32)
+        self.order = torch.empty(T, device=dev, dtype=I32)
+        self.inv = torch.empty(G, 9, device=dev, dtype=I32)
+        self.gslot = torch.zeros(T, K, 9, device=dev, dtype=F32)
         self.image = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.den = torch.empty(H, W, device=dev, dtype=F32)
         self.gimage = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.loss_ws = kernels.loss_workspace(H, W, dev)
         self.partials = torch.empty(kernels.loss_partials_count(H, W)[0], device=dev, dtype=F32)
-        self.grad9 = torch.zeros(G, 9, device=dev, dtype=F32)
         self.graphs = {}
 
     # ---------------------------------------------------------------------------------
@@ -80,9 +82,10 @@ class TrainStep:
         kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep)
         kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
-                            self.ncand)
+                            self.ncand, self.inv)
+        kernels.tile_order(self.count, self.K, self.order)
         kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
-                          self.k, self.image, self.den)
+                          self.k, self.image, self.den, self.order)
         return self.image
 
     def enqueue(self, ci=0):
@@ -91,10 +94,11 @@ class TrainStep:
         kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
                           self.loss_ws)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
-                          self.k, self.image, self.den, self.gimage, self.grad9)
+                          self.k, self.image, self.den, self.gimage, self.gslot,
+                          order=self.order)
         kernels.adam_advance(self.step_block)
-        kernels.geom_bwd_adam(self.P, self.cams[ci], self.grad9, self.m, self.v, self.lr,
-                              self.step_block)
+        kernels.geom_bwd_adam(self.P, self.cams[ci], self.gslot, self.inv, self.m, self.v,
+                              self.lr, self.step_block)
 
     def capture(self, cams=None):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
