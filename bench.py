@@ -37,7 +37,23 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-reps", type=int, default=100)
+    ap.add_argument("--no-small", action="store_true", help="skip the G=2000 128x128 run")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="also run a plain device copy of this many MiB 5 times (a known-size "
+                         "kernel to calibrate hardware byte counters against)")
     return ap.parse_args()
+
+
+def load_traffic(kernel, cfg_name):
+    """HBM bytes per launch of `kernel` on this workload, measured with rocprofv3 PMC counters
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy) and recorded in
+    profiles/traffic.json; None when no measurement is recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        rec = json.load(f).get(f"{kernel}/{cfg_name}")
+    return None if rec is None else rec.get("bytes_per_launch")
 
 
 def build_step(cfg, torch, TrainStep):
@@ -193,14 +209,22 @@ def main():
         rows[name] = dict(us=kt[name], tflops=tfl, frac=tfl / PEAK_FP32_TFLOPS)
     dom = max(("splat_fwd", "splat_bwd"), key=lambda n: kt[n])
     roofline = dict(bound="valu", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
-                    unit="TFLOP/s", frac=rows[dom]["frac"], traffic=None,
+                    unit="TFLOP/s", frac=rows[dom]["frac"], traffic=load_traffic(dom, cfg.name),
                     flops_per_launch=FLOP_PER_PAIR[dom] * pairs, pairs_per_launch=pairs,
                     us_per_launch=kt[dom])
     # the small configuration (G=2000, 128x128)
-    small = scenes.CONFIGS["c2"]
-    ts2 = build_step(small, torch, TrainStep)
-    its2 = 1000 / time_train(ts2, 1000, 50, torch)
-    fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
+    its2 = fps2 = None
+    if not args.no_small:
+        small = scenes.CONFIGS["c2"]
+        ts2 = build_step(small, torch, TrainStep)
+        its2 = 1000 / time_train(ts2, 1000, 50, torch)
+        fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
+    if args.copy_mib:
+        src = torch.ones(args.copy_mib * (1 << 18), device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(cfg, args.cpu_seconds, torch)
