@@ -198,6 +198,39 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
 /* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */
 int tts_zero(float* buf, int64_t n, hipStream_t stream);
 
+/* ---- dense (unbinned) forms, O(H*W*G): every gaussian against every pixel ---- */
+
+/* Workspace for the two dense backward entry points (G gaussians, P pixels). */
+size_t tts_dense_workspace_bytes(int G, int P);
+
+/* Dense arm-A render from proj[G,12]: Q = a dx^2 + 2b dx dy + c dy^2 at pixel centres
+ * (col+0.5, row+0.5), w = max(0, 1 - Q/k)^2, WSR blend with bg = (w_b, c_b).  Any H, W.
+ * image [H,W,3]; den [H,W] (may be NULL) = sum w*o_col + w_b.
+ * Replaces spike/render.py:14-49 (arm "A": forward.quad_form + poly_splat_wgeo + arms.blend_A). */
+int tts_render_dense(const float* proj, int G, int H, int W, float k, const float* bg,
+                     float* image, float* den, hipStream_t stream);
+
+/* Backward of tts_render_dense: grad9 [G,9] = dL/d(a, b, c, mu_x, mu_y, col_o rgb, o_col) (the
+ * geometry backward's input), gwb[0] = dL/dw_b (gwb may be NULL).  Deterministic (band partials
+ * summed in a fixed order).  Replaces autograd through spike/render.py:14-49. */
+int tts_render_dense_bwd(const float* proj, int G, int H, int W, float k, const float* bg,
+                         const float* image, const float* den, const float* gimage, float* grad9,
+                         float* gwb, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* WSR poly-splat over an explicit basis: u[p,g] = phi[p,:6] . theta[g,:6],
+ * w = o[g]*keep[g]*max(u,0)^2, C [P,3] = (w@color + w_b c_b)/(sum w + w_b); den [P] may be NULL;
+ * keep (u8) may be NULL (all kept).  Replaces spike/backward.py:11-20 / :23-39 (forward). */
+int tts_wsr_dense(const float* theta, const float* o, const float* color, const uint8_t* keep,
+                  const float* phi, int G, int P, const float* bg, float* C, float* den,
+                  hipStream_t stream);
+
+/* Backward of tts_wsr_dense: gtheta10 [G,10] = (dL/dtheta 0..5, dL/do, dL/dcolor rgb);
+ * gwb[0] = dL/dw_b (may be NULL).  Replaces WSRPolySplatHot.backward, spike/backward.py:41-58. */
+int tts_wsr_dense_bwd(const float* theta, const float* o, const float* color,
+                      const uint8_t* keep, const float* phi, int G, int P, const float* bg,
+                      const float* C, const float* den, const float* gC, float* gtheta10,
+                      float* gwb, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

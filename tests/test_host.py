@@ -65,3 +65,24 @@ def test_model_views():
     m = GaussianModel(P)
     assert torch.equal(m.means3d, P[:, 0:3]) and torch.equal(m.opacity_raw, P[:, 13])
     assert m.G == 10
+
+
+def test_render_rejects_arms_off_the_hip_path():
+    import pytest
+    from ttsplat import render, train
+    for arm in ("B", "C0", "C", "SZ", "RV", "D"):
+        with pytest.raises(NotImplementedError):
+            render.render(None, None, arm)
+    with pytest.raises(NotImplementedError):
+        render.render(None, None, "A", sh_degree=1)
+    assert train.DEFAULT_LR["means"] == 5e-3 and train.DEFAULT_LR["wb"] == 1e-2
+
+
+def test_tensor_helpers_refuse_cpu_tensors():
+    import pytest
+    from ttsplat import forward, geometry
+    x = torch.zeros(4)
+    with pytest.raises(ValueError):
+        forward.phi(x, x)
+    with pytest.raises(ValueError):
+        geometry.quat_to_rotmat(torch.zeros(2, 4))

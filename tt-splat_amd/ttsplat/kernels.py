@@ -320,3 +320,86 @@ def zero_(buf):
     require(buf, "buf", F32)
     call("tts_zero", ptr(buf), buf.numel(), stream())
     return buf
+
+
+# ---------------------------------------------------------------------------------- dense --
+def dense_workspace(G, P, device):
+    n = _lib.load().tts_dense_workspace_bytes(G, P)
+    return torch.empty(max(n, 1), device=device, dtype=U8)
+
+
+def render_dense(proj, H, W, k, bg, image=None, den=None):
+    """Dense arm-A render of every projected gaussian onto an H x W image (any H, W)."""
+    G = proj.shape[0]
+    dev = proj.device
+    _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    call("tts_render_dense", ptr(proj), G, H, W, float(k), ptr(bg), ptr(image), ptr(den),
+         stream())
+    return image, den
+
+
+def render_dense_bwd(proj, H, W, k, bg, image, den, gimage, grad9=None, gwb=None, workspace=None):
+    """Returns grad9 [G,9] (conic, mean, col_o, o_col gradients) and gwb [1]."""
+    G = proj.shape[0]
+    dev = proj.device
+    _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
+    require(bg, "bg", F32, (4,), dev)
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    grad9 = torch.empty(G, 9, device=dev, dtype=F32) if grad9 is None else grad9
+    gwb = torch.empty(1, device=dev, dtype=F32) if gwb is None else gwb
+    require(grad9, "grad9", F32, (G, 9), dev)
+    require(gwb, "gwb", F32, (1,), dev)
+    workspace = dense_workspace(G, H * W, dev) if workspace is None else workspace
+    call("tts_render_dense_bwd", ptr(proj), G, H, W, float(k), ptr(bg), ptr(image), ptr(den),
+         ptr(gimage), ptr(grad9), ptr(gwb), ptr(workspace), workspace.numel(), stream())
+    return grad9, gwb
+
+
+def _wsr_operands(theta, o, color, keep, phi):
+    G, P = theta.shape[0], phi.shape[0]
+    dev = theta.device
+    require(theta, "theta", F32, (G, 6))
+    require(o, "o", F32, (G,), dev)
+    require(color, "color", F32, (G, 3), dev)
+    require(phi, "phi", F32, (P, 6), dev)
+    if keep is not None:
+        if keep.dtype == torch.bool:
+            keep = keep.view(U8)
+        require(keep, "keep", U8, (G,), dev)
+    return G, P, dev, keep
+
+
+def wsr_dense(theta, o, color, keep, phi, bg, C=None, den=None):
+    """C [P,3] = WSR of w = o*keep*max(phi@theta^T, 0)^2; also returns den [P]."""
+    G, P, dev, keep = _wsr_operands(theta, o, color, keep, phi)
+    require(bg, "bg", F32, (4,), dev)
+    C = torch.empty(P, 3, device=dev, dtype=F32) if C is None else C
+    den = torch.empty(P, device=dev, dtype=F32) if den is None else den
+    require(C, "C", F32, (P, 3), dev)
+    require(den, "den", F32, (P,), dev)
+    call("tts_wsr_dense", ptr(theta), ptr(o), ptr(color), ptr(keep), ptr(phi), G, P, ptr(bg),
+         ptr(C), ptr(den), stream())
+    return C, den
+
+
+def wsr_dense_bwd(theta, o, color, keep, phi, bg, C, den, gC, workspace=None):
+    """Returns (gtheta [G,6], go [G], gcolor [G,3], gwb [1]) as views of one [G,10] buffer."""
+    G, P, dev, keep = _wsr_operands(theta, o, color, keep, phi)
+    require(bg, "bg", F32, (4,), dev)
+    require(C, "C", F32, (P, 3), dev)
+    require(den, "den", F32, (P,), dev)
+    require(gC, "gC", F32, (P, 3), dev)
+    g10 = torch.empty(G, 10, device=dev, dtype=F32)
+    gwb = torch.empty(1, device=dev, dtype=F32)
+    workspace = dense_workspace(G, P, dev) if workspace is None else workspace
+    call("tts_wsr_dense_bwd", ptr(theta), ptr(o), ptr(color), ptr(keep), ptr(phi), G, P,
+         ptr(bg), ptr(C), ptr(den), ptr(gC), ptr(g10), ptr(gwb), ptr(workspace),
+         workspace.numel(), stream())
+    return g10[:, 0:6], g10[:, 6], g10[:, 7:10], gwb

@@ -1,0 +1,114 @@
+"""The overfit loop under its reference names: spike/train.py:9-47.
+
+`fit(model, cameras, gt_images, arm, iters, lambda_ssim, lr, k, blur_eps, near, log_every,
+sh_degree)` minimises the mean photometric loss over all views per iteration (full batch), as
+the reference does, with every op on the HIP path: dense render (tts_render_dense + geometry),
+loss (tts_loss_grad), their backward kernels, and Adam (tts_adam) with the reference's
+per-group learning rates.  The trained parameters are written back into `model`.
+"""
+import torch
+
+from . import kernels
+from .binned import params_of
+from .loss import loss_fn, psnr
+from .render import _check_arm, render
+
+F32 = torch.float32
+
+# spike/train.py:9-12
+DEFAULT_LR = {
+    "means": 5e-3, "scales": 5e-3, "quats": 1e-3, "opacity": 5e-2,
+    "opacity_sh": 5e-2, "color": 1e-2, "wb": 1e-2, "depth": 1e-2,
+}
+
+# columns of the [G,14] block per Adam group (spike/model.py:82-95 group names)
+_GROUP_COLS = (("means", 0, 3), ("quats", 3, 7), ("scales", 7, 10), ("color", 10, 13),
+               ("opacity", 13, 14))
+
+
+class _Fitted:
+    """The trainable state fit() works on: the [G,14] block and w_b_raw as leaves."""
+
+    def __init__(self, model):
+        P = params_of(model).detach().float().contiguous().clone()
+        if not P.is_cuda:
+            raise ValueError("fit() needs the model on a GPU")
+        self.params = P
+        self.w_b_raw = torch.as_tensor(model.w_b_raw, dtype=F32).detach().to(P.device).reshape(())
+        self.c_b = torch.as_tensor(model.c_b, dtype=F32).detach().to(P.device)
+
+
+def _write_back(model, st):
+    with torch.no_grad():
+        P = st.params
+        if isinstance(getattr(model, "params", None), torch.Tensor) and model.params.shape == P.shape:
+            model.params.copy_(P)
+        else:
+            model.means3d.copy_(P[:, 0:3])
+            model.quats.copy_(P[:, 3:7])
+            model.log_scales.copy_(P[:, 7:10])
+            model.color_dc.copy_(P[:, 10:13])
+            model.opacity_raw.copy_(P[:, 13].reshape(model.opacity_raw.shape))
+        if torch.is_tensor(model.w_b_raw):
+            model.w_b_raw.copy_(st.w_b_raw.reshape(model.w_b_raw.shape))
+        else:
+            model.w_b_raw = float(st.w_b_raw)
+
+
+def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4.0, blur_eps=0.3,
+        near=0.2, log_every=0, sh_degree=0):
+    """Returns the per-iteration mean loss history (list of floats)."""
+    _check_arm(arm, sh_degree)
+    lr = {**DEFAULT_LR, **(lr or {})}
+    st = _Fitted(model)
+    dev = st.params.device
+    G = st.params.shape[0]
+    lrv = torch.zeros(14, dtype=F32)
+    for name, a, b in _GROUP_COLS:
+        lrv[a:b] = float(lr[name])
+    lrv = lrv.to(dev)
+    lrw = torch.zeros(14, dtype=F32)
+    lrw[0] = float(lr["wb"])
+    lrw = lrw.to(dev)
+    # Adam state: [G,14] moments, plus w_b_raw carried as column 0 of a one-row block
+    m, v = torch.zeros(G, 14, device=dev, dtype=F32), torch.zeros(G, 14, device=dev, dtype=F32)
+    wrow = torch.zeros(1, 14, device=dev, dtype=F32)
+    mw, vw = torch.zeros_like(wrow), torch.zeros_like(wrow)
+    step = kernels.adam_state(dev)
+    gts = [g.to(dev).float().contiguous() for g in gt_images]
+
+    class _View:                     # the duck-typed model render() reads
+        pass
+
+    history = []
+    for it in range(iters):
+        Pl = st.params.clone().requires_grad_(True)
+        wl = st.w_b_raw.clone().requires_grad_(True)
+        view = _View()
+        view.params, view.w_b_raw, view.c_b = Pl, wl, st.c_b
+        total = 0.0
+        for cam, gt in zip(cameras, gts):
+            img = render(view, cam, arm, k=k, blur_eps=blur_eps, near=near)
+            total = total + loss_fn(img, gt, lambda_ssim)
+        total = total / len(cameras)
+        gP, gw = torch.autograd.grad(total, (Pl, wl))
+        kernels.adam_advance(step)
+        kernels.adam(st.params, m, v, gP.contiguous(), lrv, step)
+        wrow[0, 0] = st.w_b_raw
+        gwrow = torch.zeros_like(wrow)
+        gwrow[0, 0] = gw
+        kernels.adam(wrow, mw, vw, gwrow, lrw, step)
+        st.w_b_raw = wrow[0, 0].clone()
+        history.append(float(total.detach()))
+        if log_every and (it % log_every == 0 or it == iters - 1):
+            print(f"    iter {it:4d}  loss {history[-1]:.5f}")
+    _write_back(model, st)
+    return history
+
+
+@torch.no_grad()
+def eval_psnr(model, cameras, gt_images, arm, **kw):
+    """Mean PSNR over the given views (spike/train.py:42-47)."""
+    vals = [float(psnr(render(model, cam, arm, **kw), gt.to(params_of(model).device)))
+            for cam, gt in zip(cameras, gt_images)]
+    return sum(vals) / len(vals)
