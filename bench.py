@@ -38,6 +38,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--kernel-reps", type=int, default=100)
     ap.add_argument("--no-small", action="store_true", help="skip the G=2000 128x128 run")
+    ap.add_argument("--no-c3", action="store_true", help="skip the G=10k 800x800 run")
+    ap.add_argument("--no-c5", action="store_true", help="skip the G=1M 1920x1072 batch run")
+    ap.add_argument("--c5-batches", type=int, default=3)
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB 5 times (a known-size "
                          "kernel to calibrate hardware byte counters against)")
@@ -56,22 +59,23 @@ def load_traffic(kernel, cfg_name):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
-def build_step(cfg, torch, TrainStep):
+def build_step(cfg, torch, TrainStep, batch=1):
     """TrainStep for the configuration; targets are the GPU render of the seed-1 set."""
     cams = cfg.cameras()
     P0 = cfg.params(seed=0)
-    tgt_maker = TrainStep(cfg.params(seed=1), cams, [torch.zeros(cfg.H, cfg.W, 3)] * len(cams),
-                          K=cfg.K, S=cfg.S, k=cfg.k)
+    zero = torch.zeros(cfg.H, cfg.W, 3, device="cuda")
+    tgt_maker = TrainStep(cfg.params(seed=1), cams, [zero] * len(cams), K=cfg.K, S=cfg.S,
+                          k=cfg.k)
     targets = []
     for ci in range(len(cams)):
         targets.append(tgt_maker.forward(ci).clone())
-    del tgt_maker
-    ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k)
+    del tgt_maker, zero
+    ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k, batch=batch)
     return ts
 
 
 def time_train(ts, steps, warmup, torch):
-    ncam = len(ts.cams)
+    ncam = ts.n_steps
     ts.capture()
     for i in range(warmup):
         ts.step(i % ncam)
@@ -128,6 +132,10 @@ def time_kernels(ts, reps, torch, kernels):
         "geom_bwd_adam": lambda: kernels.geom_bwd_adam(ts.P, cam, ts.gslot, ts.inv, ts.m, ts.v,
                                                        ts.lr, ts.step_block),
     }
+    if ts.batch > 1:
+        del jobs["geom_bwd_adam"]
+        jobs["geom_bwd_accum"] = lambda: kernels.geom_bwd_accum(ts.P, cam, ts.gslot, ts.inv,
+                                                                ts.gacc, 1.0 / ts.batch)
     out = {}
     for name, fn in jobs.items():
         for _ in range(3):
@@ -144,9 +152,75 @@ def time_kernels(ts, reps, torch, kernels):
     # restore the state the measurement perturbed
     for dst, src in zip((ts.P, ts.m, ts.v, ts.step_block), (P_save, m_save, v_save, s_save)):
         dst.copy_(src)
+    if ts.gacc is not None:
+        ts.gacc.zero_()
     ts.forward(0)
     torch.cuda.synchronize()
     return out
+
+
+def splat_bytes(ts, torch):
+    """Algorithmic HBM bytes of one fused splat launch at the current bins: per tile
+    40 B per valid slot (theta 6 + col 3 + oc 1, fp32) + 4 B per slot of the bin table,
+    12 B per pixel of image; the backward adds 16 B per pixel (dL/dC, den) and 36 B per valid
+    slot (the slot's 9 gradients)."""
+    nvalid = int(ts.count.long().sum())
+    T, P = ts.tmap.T, ts.H * ts.W
+    fwd = 40 * nvalid + 4 * ts.K * T + 12 * P
+    return fwd, fwd + 16 * P + 36 * nvalid
+
+
+def run_c3(args, torch, scenes, TrainStep):
+    cfg = scenes.CONFIGS["c3"]
+    ts = build_step(cfg, torch, TrainStep)
+    n = 300
+    its = n / time_train(ts, n, 30, torch)
+    fps = n / time_forward(ts, n, 30, torch)
+    return dict(c3_train_its=its, c3_train_ms=1e3 / its, c3_fwd_fps=fps, c3_fwd_ms=1e3 / fps)
+
+
+def run_c5(args, torch, scenes, kernels, TrainStep):
+    """G=1M clustered, 1920x1072, K=256: batches of 64 views (fwd + bwd of every view, mean
+    gradient, one Adam update), one graph per batch."""
+    cfg = scenes.CONFIGS["c5"]
+    ts = build_step(cfg, torch, TrainStep, batch=len(cfg.cameras()))
+    nb = max(1, args.c5_batches)
+    t_batch = time_train(ts, nb, 1, torch) / nb
+    # forward only, all 64 views, one graph
+    for ci in range(len(ts.cams)):
+        ts.forward(ci)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for ci in range(len(ts.cams)):
+            ts.forward(ci)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(nb):
+        g.replay()
+    torch.cuda.synchronize()
+    t_fwd = (time.perf_counter() - t0) / nb
+    # overflow over the batch: candidates beyond the budget K
+    cand = over = kept = 0
+    for ci in range(len(ts.cams)):
+        ts.forward(ci)
+        nc = ts.ncand.long()
+        cand += int(nc.sum())
+        over += int((nc - ts.K).clamp(min=0).sum())
+        kept += int(ts.count.long().sum())
+    kt = time_kernels(ts, 20, torch, kernels)
+    bf, bb = splat_bytes(ts, torch)
+    nv = len(ts.cams)
+    return dict(
+        c5_views_per_batch=nv, c5_batch_ms=t_batch * 1e3, c5_train_views_per_s=nv / t_batch,
+        c5_fwd_views_per_s=nv / t_fwd, c5_overflow_rate=over / max(cand, 1),
+        c5_candidates_per_view=cand / nv, c5_kept_per_view=kept / nv,
+        c5_kernel_us_view0=kt,
+        c5_binning_gaussians_per_s=cfg.G / (kt["binning"] * 1e-6),
+        c5_splat_fwd_GBs=bf / (kt["splat_fwd"] * 1e-6) / 1e9,
+        c5_splat_bwd_GBs=bb / (kt["splat_bwd"] * 1e-6) / 1e9,
+        c5_dtype="fp32", c5_crop="1080 rows cropped to 1072 (whole 16-px tiles)")
 
 
 def cpu_baseline(cfg, seconds, torch):
@@ -219,6 +293,8 @@ def main():
         ts2 = build_step(small, torch, TrainStep)
         its2 = 1000 / time_train(ts2, 1000, 50, torch)
         fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
+    extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
+    extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
     if args.copy_mib:
         src = torch.ones(args.copy_mib * (1 << 18), device="cuda")
         dst = torch.empty_like(src)
@@ -259,6 +335,8 @@ def main():
             "c2_train_its": its2,
             "c2_fwd_fps": fps2,
             "c2_note": "G=2000 128x128 fp32 (render operands not rounded to bf16)",
+            **extra_c3,
+            **extra_c5,
         },
     }
     print(json.dumps(out))

@@ -195,6 +195,16 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
                       const float* lr, const int32_t* step, float beta1, float beta2, float eps,
                       hipStream_t stream);
 
+/* Gradient accumulation over a batch of views: gacc[G,14] += scale * dL/dparams, with the
+ * slot gradients gathered through inv and pushed through the geometry backward (as in
+ * tts_geom_bwd_adam, without the Adam update).  A batch of views accumulates one view at a time;
+ * tts_adam then applies the update and tts_zero clears gacc.  Replaces the reference's
+ * full-batch accumulation (spike/train.py:25-31; gacc accumulation of
+ * tools/resident_traced.py:718-727). */
+int tts_geom_bwd_accum(const float* params, int G, const float* camera, float near_z,
+                       float blur, const float* gslot, const int32_t* inv, float scale,
+                       float* gacc, hipStream_t stream);
+
 /* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */
 int tts_zero(float* buf, int64_t n, hipStream_t stream);
 

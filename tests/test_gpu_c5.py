@@ -1,0 +1,83 @@
+"""The stress configuration at full size: G = 1M clustered gaussians, 1920x1072, K = 256.
+
+Bins: bit-exact with the oracle (stable order; above the 32768-pair radix threshold this is the
+reference order too) for one view.  Splat forward and backward: a sample of tiles against the
+oracle (the whole-frame oracle splat is 5e8 pairs), through the pre-gathered operand entry
+points so the sample's operands are exactly the GPU's.
+"""
+import pytest
+import torch
+
+from helpers import cam_dict, max_abs, rel_l2
+from oracle import binning as obin
+from oracle import splat as osplat
+from ttsplat import kernels, scenes
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def c5():
+    cfg = scenes.CONFIGS["c5"]
+    P = cfg.params(0)
+    cam = cfg.cameras()[5]
+    print(f"[c5] G={cfg.G} {cfg.W}x{cfg.H} K={cfg.K}", flush=True)
+    proj, keep = kernels.geom_fwd(P.cuda(), cam.device_block("cuda"))
+    idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S,
+                                                   cfg.K, cfg.span)
+    torch.cuda.synchronize()
+    return cfg, P, cam, proj, keep, idx, valid, count, ncand
+
+
+def test_c5_bins_bit_exact(c5):
+    cfg, P, cam, proj, keep, idx, valid, count, ncand = c5
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    mu = proj[:, 0:2].cpu()
+    kp = keep.cpu().bool()
+    ridx, rvalid, rn = obin.assign_bins(mu, kp, tmap, 1, cfg.K, span=cfg.span, stable=True,
+                                        return_stats=True)
+    print(f"[c5] pairs {int(rn.sum())}, overflow tiles {int((rn > cfg.K).sum())}", flush=True)
+    assert int(rn.sum()) >= obin.RADIX_STABLE_MIN_PAIRS
+    assert torch.equal(ncand.cpu().long(), rn)
+    assert torch.equal(valid.cpu().bool(), rvalid)
+    assert torch.equal(idx.cpu().long(), ridx)
+    assert torch.equal(count.cpu().long(), rvalid.sum(1))
+
+
+def test_c5_splat_sampled_tiles(c5):
+    cfg, P, cam, proj, keep, idx, valid, count, ncand = c5
+    T = idx.shape[0]
+    bg = torch.tensor([float(torch.nn.functional.softplus(torch.tensor(-3.0))), 1.0, 1.0, 1.0],
+                      device="cuda")
+    th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, cfg.k)
+    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
+    # the fused kernel and the pre-gathered-operand kernel agree over the whole frame
+    img2, _ = kernels.splat_fwd_theta(th, col, oc, bg, cfg.H, cfg.W, cfg.S)
+    assert max_abs(img, img2) <= 1e-5
+    g = torch.Generator().manual_seed(9)
+    heavy = torch.argsort(count.cpu(), descending=True)[:24]
+    sel = torch.cat([heavy, torch.randint(0, T, (40,), generator=g)]).unique()
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    Phi = tmap.Phi.double()
+    ths = th[sel.cuda()].cpu().double().requires_grad_(True)
+    cols = col[sel.cuda()].cpu().double().requires_grad_(True)
+    ocs = oc[sel.cuda()][..., None].cpu().double().requires_grad_(True)
+    wb = float(bg[0])
+    C, _ = osplat.splat_tiles(ths, cols, ocs, Phi, torch.tensor(wb, dtype=torch.float64),
+                              torch.ones(3, dtype=torch.float64))
+    pix = tmap.gidx.reshape(T, -1)[sel]                       # [n,256] pixel ids
+    mine = img.reshape(-1, 3)[pix.reshape(-1).cuda()].reshape(C.shape)
+    err = max_abs(mine, C)
+    print(f"[c5] {len(sel)} tiles, forward max|err| {err:.2e}", flush=True)
+    assert err <= 1e-4
+    # backward on the same tiles: a random dL/dimage over the frame
+    R = torch.randn(cfg.H, cfg.W, 3, generator=g)
+    gth, gcol, goc = kernels.splat_bwd_theta(th, col, oc, bg, cfg.H, cfg.W, cfg.S, img2, den,
+                                             R.cuda())
+    (C * R.reshape(-1, 3)[pix.reshape(-1)].reshape(C.shape).double()).sum().backward()
+    s = sel.cuda()
+    for mine_g, ref_g, n in ((gth[s], ths.grad, "theta"), (gcol[s], cols.grad, "col"),
+                             (goc[s], ocs.grad[..., 0], "oc")):
+        e = rel_l2(mine_g, ref_g)
+        print(f"[c5] d{n}: rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-3, n

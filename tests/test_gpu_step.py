@@ -76,3 +76,43 @@ def test_training_reduces_loss():
         ts.step(0)
     l1 = float(ts.loss())
     assert l1 < 0.8 * l0, (l0, l1)
+
+
+def test_batch_step_matches_oracle_mean_gradient():
+    """batch = 4: one Adam update on the mean gradient of 4 views (spike/train.py:21-33)."""
+    from ttsplat import scenes
+    from ttsplat.camera import pinhole
+    cfg, P, _ = config_inputs("c1_ref")
+    cams = [pinhole(cfg.H, cfg.W, e) for e in scenes.orbit_eyes(4)]
+    tgts = [target_for(cfg, c) for c in cams]
+    ts = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, batch=4)
+    assert ts.n_steps == 1
+    ts.enqueue(0)
+    torch.cuda.synchronize()
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    grads = []
+    for c, t in zip(cams, tgts):
+        _, _, g, _ = opipe.render_and_grad(P, cam_dict(c), tmap, t.cpu(), K=cfg.K, k=cfg.k,
+                                           stable=True)
+        grads.append(g)
+    g = torch.stack(grads).mean(0)
+    Pr, m, v = P.clone(), torch.zeros_like(P), torch.zeros_like(P)
+    oadam.adam_step(Pr, m, v, g, lr_vector(device="cpu"), 1)
+    assert rel_l2(ts.P.cpu() - P, Pr - P) <= 1e-2
+    assert int(ts.step_block[0]) == 1
+    assert float(ts.gacc.abs().max()) == 0.0          # cleared for the next batch
+    with pytest.raises(ValueError):
+        TrainStep(P, cams[:3], tgts[:3], K=cfg.K, batch=2)
+
+
+def test_geom_bwd_accum_adds_scaled_gradients():
+    cfg, P, cam = config_inputs("c1_ref")
+    tgt = target_for(cfg, cam)
+    ts = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k)
+    ts._view_backward(0)
+    grad9 = kernels.slot_reduce(ts.gslot, ts.inv)
+    g14 = kernels.geom_bwd(ts.P, ts.cams[0], grad9)
+    acc = torch.zeros_like(g14)
+    kernels.geom_bwd_accum(ts.P, ts.cams[0], ts.gslot, ts.inv, acc, 0.25)
+    kernels.geom_bwd_accum(ts.P, ts.cams[0], ts.gslot, ts.inv, acc, 0.5)
+    assert rel_l2(acc, 0.75 * g14) <= 1e-6

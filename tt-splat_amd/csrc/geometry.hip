@@ -340,6 +340,28 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
   }
 }
 
+// Batch form: gacc[g] += scale * dL/dparams[g] for one view (one writer per gaussian).
+__global__ __launch_bounds__(256) void k_geom_bwd_accum(
+    const float* __restrict__ params, int G, const float* __restrict__ camera, float near_z,
+    float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv, float scale,
+    float* __restrict__ gacc) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  const Camera cam = load_camera(camera);
+  const float* p = params + (int64_t)g * 14;
+  float pl[14];
+#pragma unroll
+  for (int i = 0; i < 14; ++i) pl[i] = p[i];
+  GeoState s;
+  geo_forward(pl, cam, near_z, blur, s);
+  float gin[9], gout[14];
+  gather_slot_grads(gslot, inv, g, gin);
+  geo_backward(pl, cam, s, gin, gout);
+  float* a = gacc + (int64_t)g * 14;
+#pragma unroll
+  for (int i = 0; i < 14; ++i) a[i] += scale * gout[i];
+}
+
 __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) buf[i] = 0.0f;
@@ -398,6 +420,17 @@ int tts_adam(float* params, float* m, float* v, const float* grad, const float* 
   if (G == 0) return TTS_OK;
   const int64_t n = (int64_t)G * 14;
   k_adam<<<grid1d(n, 256), 256, 0, stream>>>(params, m, v, grad, lr, n, step, beta1, beta2, eps);
+  return launch_status();
+}
+
+int tts_geom_bwd_accum(const float* params, int G, const float* camera, float near_z,
+                       float blur, const float* gslot, const int32_t* inv, float scale,
+                       float* gacc, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !gacc))) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd_accum<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, gslot,
+                                                       inv, scale, gacc);
   return launch_status();
 }
 

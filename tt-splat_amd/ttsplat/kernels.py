@@ -296,6 +296,20 @@ def adam(params, m, v, grad, lr, step, b1=BETA1, b2=BETA2, eps=EPS):
          stream())
 
 
+def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=BLUR):
+    """gacc[G,14] += scale * dL/dparams for one view (slot gradients gathered through inv)."""
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(camera, "camera", F32, (16,), dev)
+    require(gslot, "gslot", F32, None, dev)
+    require(inv, "inv", I32, (G, 9), dev)
+    require(gacc, "gacc", F32, (G, 14), dev)
+    call("tts_geom_bwd_accum", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
+         float(scale), ptr(gacc), stream())
+    return gacc
+
+
 def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
                   b1=BETA1, b2=BETA2, eps=EPS):
     """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel."""

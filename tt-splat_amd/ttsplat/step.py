@@ -32,10 +32,16 @@ def lr_vector(lr=DEFAULT_LR, means_lr=MEANS_LR, device="cuda"):
 
 class TrainStep:
     """Owns params [G,14], Adam moments and every work buffer for training against one or more
-    (camera, target) pairs; step(i) runs one full training step on camera i."""
+    (camera, target) pairs.
+
+    batch = 1: step(i) is one full training step on camera i (one Adam update per view, the
+    round-robin loop of tools/resident_traced.py:667-757).
+    batch = B > 1: the views are grouped into consecutive batches of B; step(i) renders and
+    backpropagates every view of batch i, accumulating the mean gradient, then applies one Adam
+    update (the full-batch loop of spike/train.py:21-33 over B views)."""
 
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
-                 c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda"):
+                 c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1):
         dev = torch.device(device)
         self.dev = dev
         self.G = params.shape[0]
@@ -74,6 +80,10 @@ class TrainStep:
         self.gimage = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.loss_ws = kernels.loss_workspace(H, W, dev)
         self.partials = torch.empty(kernels.loss_partials_count(H, W)[0], device=dev, dtype=F32)
+        self.batch = int(batch)
+        if self.batch < 1 or len(self.cams) % self.batch:
+            raise ValueError(f"{len(self.cams)} views do not split into batches of {batch}")
+        self.gacc = torch.zeros(G, 14, device=dev, dtype=F32) if self.batch > 1 else None
         self.graphs = {}
 
     # ---------------------------------------------------------------------------------
@@ -88,22 +98,40 @@ class TrainStep:
                           self.k, self.image, self.den, self.order)
         return self.image
 
-    def enqueue(self, ci=0):
-        """Enqueue one full training step for camera ci on the current stream."""
+    @property
+    def n_steps(self):
+        """Number of distinct steps (views for batch = 1, batches otherwise)."""
+        return len(self.cams) // self.batch
+
+    def _view_backward(self, ci):
+        """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
         self.forward(ci)
         kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
                           self.loss_ws)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                           self.k, self.image, self.den, self.gimage, self.gslot,
                           order=self.order)
+
+    def enqueue(self, i=0):
+        """Enqueue training step i (camera i, or batch i) on the current stream."""
+        if self.batch == 1:
+            self._view_backward(i)
+            kernels.adam_advance(self.step_block)
+            kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
+                                  self.lr, self.step_block)
+            return
+        scale = 1.0 / self.batch
+        for ci in range(i * self.batch, (i + 1) * self.batch):
+            self._view_backward(ci)
+            kernels.geom_bwd_accum(self.P, self.cams[ci], self.gslot, self.inv, self.gacc, scale)
         kernels.adam_advance(self.step_block)
-        kernels.geom_bwd_adam(self.P, self.cams[ci], self.gslot, self.inv, self.m, self.v,
-                              self.lr, self.step_block)
+        kernels.adam(self.P, self.m, self.v, self.gacc, self.lr, self.step_block)
+        kernels.zero_(self.gacc)
 
     def capture(self, cams=None):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
         kernel's code object is resident) and its effect on the state is rolled back."""
-        cams = range(len(self.cams)) if cams is None else cams
+        cams = range(self.n_steps) if cams is None else cams
         state = [t.clone() for t in (self.P, self.m, self.v, self.step_block)]
         side = torch.cuda.Stream(device=self.dev)
         side.wait_stream(torch.cuda.current_stream(self.dev))
@@ -122,7 +150,7 @@ class TrainStep:
         torch.cuda.synchronize(self.dev)
 
     def step(self, ci=0):
-        """One training step on camera ci (graph replay when captured, else eager)."""
+        """Training step ci: camera ci, or batch ci (graph replay when captured, else eager)."""
         g = self.graphs.get(ci)
         if g is not None:
             g.replay()
