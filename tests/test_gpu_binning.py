@@ -126,3 +126,68 @@ def test_bins_bad_arguments_raise():
         kernels.assign_bins(mu, keep, 100, 64, 16, 32, 2048)     # H not a multiple of S
     with pytest.raises(Exception):
         kernels.assign_bins(mu, keep, 64, 64, 16, 4096, 2048)    # K too large
+
+
+def _offscreen_mu(G, H, W, seed, inside_frac=0.01, near_frac=0.03):
+    """Mostly off-screen centres at mixed distances: far from every reachable tile (stored as
+    far ids), just beyond the border (saturated for some tiles, not others), a few on-screen
+    ones (so border tiles run out of unsaturated candidates and the saturated tie decides slot
+    K), exact duplicates and a far corner pile."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.rand(G, 2, generator=g)
+    mu = torch.empty(G, 2)
+    v = torch.rand(G, generator=g)
+    inside = v < inside_frac
+    near = (v >= inside_frac) & (v < inside_frac + near_frac)
+    far = ~(inside | near)
+    mu[far] = u[far] * torch.tensor([W + 800.0, H + 800.0]) - 400.0          # up to 400 px out
+    mu[near] = u[near] * torch.tensor([W + 120.0, H + 120.0]) - 60.0         # saturation edge
+    mu[inside] = u[inside] * torch.tensor([float(W), float(H)])
+    mu[G // 2: G // 2 + 40] = mu[G // 2]                                     # duplicates
+    mu[G // 3: G // 3 + 20] = torch.tensor([-1000.0, -1000.0])               # far corner pile
+    keep = torch.rand(G, generator=g) > 0.1
+    return mu.contiguous(), keep
+
+
+@pytest.mark.parametrize("S,K,G,H,W", [(16, 32, 3000, 48, 64), (16, 128, 8000, 64, 80),
+                                       (16, 256, 30000, 96, 160), (32, 64, 6000, 96, 128),
+                                       (16, 1, 2000, 32, 32), (16, 200, 5000, 16, 96),
+                                       (16, 100, 4000, 96, 16), (16, 512, 60000, 64, 64)])
+def test_bins_offscreen_far_populations(S, K, G, H, W):
+    mu, keep = _offscreen_mu(G, H, W, seed=G + K)
+    span = 2048 if S == 16 else 8192
+    print(f"[bins] off-screen G={G} {H}x{W} S={S} K={K}", flush=True)
+    inv = torch.empty(G, 9, dtype=torch.int32, device="cuda")
+    idx, valid, count, ncand = kernels.assign_bins(mu.cuda(), keep.to(torch.uint8).cuda(), H, W,
+                                                   S, K, span, inv=inv)
+    tmap = obin.TileMap(H, W, S)
+    ridx, rvalid, rncand = obin.assign_bins(mu, keep, tmap, 1, K, span, stable=True,
+                                            return_stats=True)
+    ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+    assert ndiff == 0, f"{ndiff} tiles differ, first {tiles[:8].tolist()}"
+    assert torch.equal(ncand.cpu().long(), rncand)
+    # every kept slot is recorded once in the inverse table
+    iv = inv.cpu().long()
+    slots = iv[iv >= 0]
+    assert slots.numel() == int(rvalid.sum())
+    assert torch.equal(torch.sort(slots).values,
+                       torch.nonzero(rvalid.flatten()).flatten())
+
+
+def test_bins_workspace_reused_across_sizes():
+    """One workspace (sized for the largest call) serves calls with different G in a row: the
+    counters it keeps zero between calls, including the far counts, must not leak."""
+    H, W, S, K = 64, 96, 16, 48
+    ws = kernels.bin_workspace(20000, H, W, S, "cuda")
+    tmap = obin.TileMap(H, W, S)
+    for G, seed in ((20000, 1), (0, 2), (700, 3), (20000, 4), (3000, 5)):
+        mu, keep = _offscreen_mu(max(G, 1), H, W, seed=seed)
+        mu, keep = mu[:G].contiguous(), keep[:G]
+        print(f"[bins] workspace reuse G={G}", flush=True)
+        idx, valid, count, ncand = kernels.assign_bins(mu.cuda(), keep.to(torch.uint8).cuda(), H,
+                                                       W, S, K, 2048, workspace=ws)
+        ridx, rvalid, rncand = obin.assign_bins(mu, keep, tmap, 1, K, 2048, stable=True,
+                                                return_stats=True)
+        ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+        assert ndiff == 0, f"G={G}: {ndiff} tiles differ, first {tiles[:8].tolist()}"
+        assert torch.equal(ncand.cpu().long(), rncand)
