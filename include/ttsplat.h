@@ -116,6 +116,16 @@ int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
                   const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
                   float* image, float* den, hipStream_t stream);
 
+/* tts_splat_fwd on the matrix cores (S = 16 only): per 32-slot chunk, u = Phi.theta_u as one
+ * bf16 MFMA whose spare contraction depth carries split-precision terms (theta in three bf16
+ * parts, Phi in two), then [num|den] = w.[col_o|o_col] as a second MFMA.  bf16 = 0: w and the
+ * colours split hi+lo as well (fp32-level accuracy); bf16 = 1: the bf16 render variant (w and the
+ * colours rounded to bf16, fp32 accumulation; tools/resident_traced.py:265-274).
+ * Same operands, outputs and tile order as tts_splat_fwd. */
+int tts_splat_fwd_mx(const float* proj, const int32_t* idx, const uint8_t* valid,
+                     const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
+                     float* image, float* den, int bf16, hipStream_t stream);
+
 /* Splat forward from pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K].
  * Replaces _DevRenderBinned.forward, tools/m4_train_binned.py:154-166 (ops :146-151). */
 int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc,

@@ -163,3 +163,42 @@ def test_backward_is_deterministic():
         gslot = kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R)
         outs.append(kernels.geom_bwd(P.cuda(), camera, kernels.slot_reduce(gslot, setup.inv)))
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("name,bf16", [("c1_ref", False), ("c3", False), ("c4", False),
+                                       ("c1_ref", True), ("c3", True), ("c4", True)])
+def test_splat_fwd_matrix_cores(name, bf16):
+    """Matrix-core forward: fp32 mode within 1e-4 of the oracle, the bf16 render variant within
+    1e-2 (the contract's two image tolerances); den likewise (relative to its scale)."""
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup(name)
+    print(f"[fwd-mx] {name} bf16={bf16}", flush=True)
+    img, den = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, bf16=bf16)
+    ref, ex = osplat.render_binned(P, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins,
+                                   return_all=True)
+    tol = 1e-2 if bf16 else 1e-4
+    err = max_abs(img, ref)
+    print(f"[fwd-mx] {name} bf16={bf16} max|err|={err:.3e}")
+    assert err <= tol
+    assert max_abs(den, ex["den"]) <= tol * float(ex["den"].abs().max())
+    # same result with a tile order
+    order = kernels.tile_order(torch.randint(0, cfg.K + 1, (tmap.T,), dtype=torch.int32,
+                                             device="cuda"), cfg.K)
+    img2, _ = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, order=order,
+                                   bf16=bf16)
+    assert torch.equal(img, img2)
+
+
+def test_splat_fwd_matrix_cores_full_slots():
+    """K = 512 with every slot of many tiles valid (16 chunks of 32), ragged last chunks."""
+    cfg, P, cam = config_inputs("c4")
+    proj, keep = kernels.geom_fwd(P.cuda(), cam.device_block("cuda"))
+    idx, valid, count, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, 512,
+                                               cfg.span)
+    assert int(count.max()) == 512 and int((count % 32 != 0).sum()) > 0
+    bg = torch.tensor([0.05, 1.0, 1.0, 1.0], device="cuda")
+    a, da = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
+    b, db = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
+    assert max_abs(a, b) <= 1e-4
+    assert max_abs(da, db) <= 1e-4 * float(da.abs().max())
+    with pytest.raises(Exception):
+        kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, 32, cfg.k)

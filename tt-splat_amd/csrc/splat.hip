@@ -332,6 +332,209 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   }
 }
 
+// ------------------------------------------------------------------ matrix-core forward --
+// The same per-tile contraction on the gfx950 matrix cores (v_mfma_f32_16x16x32_bf16, S = 16).
+//   GEMM1  u^T[slot][pixel] = Theta[slot][k] . Phi^T[k][pixel].  The basis has 6 monomials but
+//          the instruction contracts 32: the spare depth carries split-precision terms, so with
+//          theta = th_hi + th_mid + th_lo and Phi = phi_hi + phi_lo (bf16 parts; lx, ly, 1 are
+//          exact in bf16) u is accumulated from
+//            k 0-5 th_hi.phi_hi | 6-11 th_mid.phi_hi | 12-17 th_lo.phi_hi |
+//            18-20 th_hi.phi_lo | 21-23 th_mid.phi_lo | 24-31 zero
+//          i.e. to about fp32 accuracy at no extra matrix-core cost.
+//   GEMM2  [num | den][pixel][n] = w[pixel][slot] . [col_o | o_col][slot][n], w = max(u,0)^2.
+//          The GEMM1 result layout (lane: pixel, registers: 4 consecutive slots of each 16-slot
+//          half) is exactly the A-operand layout of GEMM2 with the slot order permuted, so the
+//          colour operand is stored in that permuted order and no data moves between lanes.
+//          SPLIT_W (fp32 mode): w = w_hi + w_lo and colours c_hi | c_lo in columns 0-3 | 4-7,
+//          num = D[:, 0:4] + D[:, 4:8] (relative error ~2^-16).  bf16 mode: w and the colours
+//          rounded once to bf16 (the reference's bf16 render operands,
+//          tools/resident_traced.py:265-274), fp32 accumulation.
+// Wave w owns tile rows 4w..4w+3 (one 16-pixel group each); slots are processed 32 at a time.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __bf16 to_bf(float x) { return (__bf16)x; }
+__device__ __forceinline__ float from_bf(__bf16 x) { return (float)x; }
+
+// One 32-element theta row (bf16x8 x 4) in the k layout above.
+__device__ __forceinline__ void theta_row(const float* th, bf16x8* dst) {
+  __bf16 hi[6], mid[6], lo[6];
+#pragma unroll
+  for (int m = 0; m < 6; ++m) {
+    hi[m] = to_bf(th[m]);
+    const float r = th[m] - from_bf(hi[m]);
+    mid[m] = to_bf(r);
+    lo[m] = to_bf(r - from_bf(mid[m]));
+  }
+  __bf16 row[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) row[k] = to_bf(0.0f);
+#pragma unroll
+  for (int m = 0; m < 6; ++m) {
+    row[m] = hi[m];
+    row[6 + m] = mid[m];
+    row[12 + m] = lo[m];
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    row[18 + m] = hi[m];
+    row[21 + m] = mid[m];
+  }
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    bf16x8 x;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = row[8 * v + e];
+    dst[v] = x;
+  }
+}
+
+// The lane's 8-element slice (q = lane / 16) of the Phi^T operand for pixel (lx, ly).
+__device__ __forceinline__ bf16x8 phi_slice(float lx, float ly, int q) {
+  const float f[6] = {lx * lx, ly * ly, lx * ly, lx, ly, 1.0f};
+  __bf16 fh[6], fl[3];
+#pragma unroll
+  for (int m = 0; m < 6; ++m) fh[m] = to_bf(f[m]);
+#pragma unroll
+  for (int m = 0; m < 3; ++m) fl[m] = to_bf(f[m] - from_bf(fh[m]));
+  __bf16 row[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) row[k] = to_bf(0.0f);
+#pragma unroll
+  for (int m = 0; m < 6; ++m) {
+    row[m] = fh[m];
+    row[6 + m] = fh[m];
+    row[12 + m] = fh[m];
+  }
+#pragma unroll
+  for (int m = 0; m < 3; ++m) {
+    row[18 + m] = fl[m];
+    row[21 + m] = fl[m];
+  }
+  bf16x8 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[j][e] = row[8 * j + e];
+  return q == 0 ? v[0] : (q == 1 ? v[1] : (q == 2 ? v[2] : v[3]));
+}
+
+inline size_t fwd_mx_lds(int K) {
+  const int kpad = (K + 31) & ~31;
+  return (size_t)kpad * 64 + (size_t)(kpad / 32) * 512;
+}
+
+template <bool SPLIT_W>
+__global__ __launch_bounds__(256) void k_splat_fwd_mx(
+    const float* __restrict__ proj, const int32_t* __restrict__ idx,
+    const uint8_t* __restrict__ valid, const int32_t* __restrict__ order, int ntx, int W, int K,
+    float inv_k, const float* __restrict__ bg, float* __restrict__ image,
+    float* __restrict__ den_out) {
+  extern __shared__ unsigned char s_dyn[];
+  __shared__ int s_tmp[4];
+  const int kpad = (K + 31) & ~31;
+  bf16x8* s_th = reinterpret_cast<bf16x8*>(s_dyn);  // [kpad][4]
+  __bf16* s_col = reinterpret_cast<__bf16*>(s_th + (size_t)kpad * 4);  // [kpad/32][4][8][8]
+  const int t = order ? order[blockIdx.x] : blockIdx.x;
+  const int tx = t % ntx, ty = t / ntx;
+  const int ox = tx * 16, oy = ty * 16;
+  const float oxf = (float)ox, oyf = (float)oy;
+  // compact the valid slots, build theta in fp32 and store its split row and the colours
+  int n = 0;
+  for (int s0 = 0; s0 < K; s0 += 256) {
+    const int s = s0 + threadIdx.x;
+    const int v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
+    int total;
+    const int pos = n + block_excl_scan256(v, s_tmp, &total);
+    if (v) {
+      float4 ta, tb, cl;
+      build_slot(proj, idx[(int64_t)t * K + s], oxf, oyf, inv_k, ta, tb, cl);
+      const float th[6] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y};
+      theta_row(th, s_th + (size_t)pos * 4);
+      const float c4[4] = {cl.x, cl.y, cl.z, cl.w};
+      const int c = pos >> 5, r = pos & 31;
+      const int q = (r & 15) >> 2, e = (r & 3) + ((r >> 4) << 2);
+      __bf16* dst = s_col + (((size_t)(c * 4 + q)) * 8) * 8 + e;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const __bf16 h = to_bf(c4[m]);
+        dst[m * 8] = h;
+        dst[(4 + m) * 8] = SPLIT_W ? to_bf(c4[m] - from_bf(h)) : to_bf(0.0f);
+      }
+    }
+    n += total;
+  }
+  const int nch = (n + 31) >> 5;
+  // zero the padding slots of the last chunk
+  for (int pos = n + threadIdx.x; pos < nch * 32; pos += 256) {
+    const bf16x8 z = {};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s_th[(size_t)pos * 4 + v] = z;
+    const int c = pos >> 5, r = pos & 31;
+    const int q = (r & 15) >> 2, e = (r & 3) + ((r >> 4) << 2);
+    __bf16* dst = s_col + (((size_t)(c * 4 + q)) * 8) * 8 + e;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) dst[m * 8] = to_bf(0.0f);
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, q = lane >> 4;
+  bf16x8 bphi[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    bphi[i] = phi_slice((float)l16 + 0.5f, (float)(4 * wave + i) + 0.5f, q);
+  floatx4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  const bf16x8 zero8 = {};
+  for (int c = 0; c < nch; ++c) {
+    const bf16x8 a0 = s_th[(size_t)(c * 32 + l16) * 4 + q];
+    const bf16x8 a1 = s_th[(size_t)(c * 32 + 16 + l16) * 4 + q];
+    const bf16x8 bc = l16 < 8 ? *reinterpret_cast<const bf16x8*>(s_col + ((size_t)(c * 4 + q) * 8 + l16) * 8)
+                              : zero8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const floatx4 u0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bphi[i], zero4, 0, 0, 0);
+      const floatx4 u1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bphi[i], zero4, 0, 0, 0);
+      float w[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float r0 = fmaxf(u0[e], 0.0f), r1 = fmaxf(u1[e], 0.0f);
+        w[e] = r0 * r0;
+        w[4 + e] = r1 * r1;
+      }
+      bf16x8 wh;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wh[e] = to_bf(w[e]);
+      acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wh, bc, acc[i], 0, 0, 0);
+      if constexpr (SPLIT_W) {
+        bf16x8 wl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) wl[e] = to_bf(w[e] - from_bf(wh[e]));
+        acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wl, bc, acc[i], 0, 0, 0);
+      }
+    }
+  }
+  // lane (q, n = l16) holds column n for pixels 4q..4q+3 of each of its rows
+  const float wb = bg[0];
+  const float cbn = l16 < 3 ? wb * bg[1 + l16] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * wave + i;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = acc[i][e];
+      if constexpr (SPLIT_W) v += __shfl(v, (lane + 4) & 63);
+      const float d = __shfl(v, (lane & ~15) + 3) + wb;
+      const int64_t pix = (int64_t)(oy + row) * W + ox + 4 * q + e;
+      if (l16 < 3) image[pix * 3 + l16] = (v + cbn) / d;
+      if (l16 == 3 && den_out) den_out[pix] = d;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_theta_gather(const float* __restrict__ proj,
                                                       const int32_t* __restrict__ idx,
                                                       const uint8_t* __restrict__ valid, int ntx,
@@ -431,6 +634,24 @@ int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
   if (!proj || !idx || !valid || !bg || !image) return TTS_EINVAL;
   return launch_fwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
                           image, den, stream);
+}
+
+int tts_splat_fwd_mx(const float* proj, const int32_t* idx, const uint8_t* valid,
+                     const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
+                     float* image, float* den, int bf16, hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (S != 16) return TTS_ETILE;
+  if (!proj || !idx || !valid || !bg || !image) return TTS_EINVAL;
+  const int ntx = W / S, T = (H / S) * ntx;
+  const float inv_k = (float)(1.0 / (double)k);
+  if (bf16)
+    k_splat_fwd_mx<false><<<T, 256, fwd_mx_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K,
+                                                            inv_k, bg, image, den);
+  else
+    k_splat_fwd_mx<true><<<T, 256, fwd_mx_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K,
+                                                           inv_k, bg, image, den);
+  return launch_status();
 }
 
 int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc, int H, int W,

@@ -28,6 +28,8 @@ SIGNATURES = {
     "tts_tile_order": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
     "tts_splat_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                _vp, _vp, _vp, _vp]),
+    "tts_splat_fwd_mx": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                  _vp, _vp, _vp, _c_int, _vp]),
     "tts_splat_fwd_theta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                      _vp, _vp]),
     "tts_splat_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,

@@ -149,6 +149,23 @@ def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None
     return image, den
 
 
+def splat_fwd_mx(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None, bf16=False):
+    """Matrix-core splat forward (S = 16): fp32-level accuracy, or the bf16 render variant."""
+    dev = proj.device
+    _aligned16(require(proj, "proj", F32, (proj.shape[0], 12)), "proj")
+    T, K, valid = _bins_check(idx, valid, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
+    call("tts_splat_fwd_mx", ptr(proj), ptr(idx), ptr(valid), ptr(order), H, W, S, K, float(k),
+         ptr(bg), ptr(image), ptr(den), int(bool(bf16)), stream())
+    return image, den
+
+
 def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, gslot=None, gwb=None,
               order=None):
     """Per-slot gradients gslot[T,K,9] (valid slots written); gwb[T] gets per-tile dL/dw_b."""

@@ -34,6 +34,9 @@ class TrainStep:
     """Owns params [G,14], Adam moments and every work buffer for training against one or more
     (camera, target) pairs.
 
+    dtype = "bf16": the render forward is the bf16 variant (matrix-core splat with bf16 weights
+    and colours, fp32 accumulation); geometry, binning, loss, backward and Adam stay fp32
+    (the reference's bf16 device path keeps its parameters and Adam state in fp32).
     batch = 1: step(i) is one full training step on camera i (one Adam update per view, the
     round-robin loop of tools/resident_traced.py:667-757).
     batch = B > 1: the views are grouped into consecutive batches of B; step(i) renders and
@@ -41,8 +44,14 @@ class TrainStep:
     update (the full-batch loop of spike/train.py:21-33 over B views)."""
 
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
-                 c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1):
+                 c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
+                 dtype="fp32"):
         dev = torch.device(device)
+        if dtype not in ("fp32", "bf16"):
+            raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
+        if dtype == "bf16" and S != 16:
+            raise ValueError("the bf16 render variant runs on 16x16 tiles")
+        self.dtype = dtype
         self.dev = dev
         self.G = params.shape[0]
         self.H, self.W = cameras[0].H, cameras[0].W
@@ -94,8 +103,12 @@ class TrainStep:
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
                             self.ncand, self.inv)
         kernels.tile_order(self.count, self.K, self.order)
-        kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
-                          self.k, self.image, self.den, self.order)
+        if self.dtype == "bf16":
+            kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
+                                 self.S, self.k, self.image, self.den, self.order, bf16=True)
+        else:
+            kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
+                              self.k, self.image, self.den, self.order)
         return self.image
 
     @property
