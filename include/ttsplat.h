@@ -183,6 +183,18 @@ int tts_loss_grad(const float* image, const float* target, int H, int W, float l
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);
 
+/* Target statistics of the SSIM term: stats [2][3][H-10][W-10] = mu_y and
+ * E[y^2] - mu_y^2 of the clamped target on the valid map.  They depend on the target alone, so a
+ * training loop computes them once per view (the precomputed y maps of
+ * tools/resident_traced.py:431-464). */
+int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream);
+
+/* tts_loss_grad with the target statistics supplied; workspace: 9 (H-10)(W-10) floats (the
+ * partial maps). */
+int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
+                        int W, float lambda, float* gimage, float* partials, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 /* -------------------------------------------------------------------- adam ---------- */
 
 /* Advance the device step counter (int32, step[0] += 1) and derive the bias corrections the

@@ -2,11 +2,13 @@
 // SSIM: 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4
 // (spike/metrics.py:6-28; the manual gradient of tools/loss_manual.py:76-103).
 //
-// Two kernels over 32x16 tiles, one colour channel per block, separable filters with register
-// blocking (each value read from LDS once per pass instead of once per tap):
-//   k_ssim_maps   per OUTPUT pixel of the valid SSIM map: mu_x, mu_y, s_x, s_y, s_xy from five
-//                 filtered images; writes dS/dfx, dS/dfxx, dS/dfxy to the workspace
-//                 maps[3][3][Ho][Wo] and the tile's sum of S.
+// Two kernels, one colour channel per block, separable filters with register blocking (each
+// value read from LDS once per pass instead of once per tap):
+//   k_ssim_stats  the target's statistics mu_y, s_y on the valid SSIM map (once per target in a
+//                 training loop).
+//   k_ssim_maps   per OUTPUT pixel of the valid SSIM map: the image's filtered moments, S and
+//                 its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] -> maps[3][3][Ho][Wo], the
+//                 tile's sum of S.
 //   k_ssim_grad   per INPUT pixel: the transposed filter (zero outside the valid map) of the
 //                 three maps, combined as  dmeanS/dx = (F'(A) + 2 x F'(B) + y F'(Cxy)) / Ns,
 //                 gated by 0 <= x <= 1 (the clamp), plus the L1 term (1-l) sign(x-y) / N.
@@ -32,100 +34,188 @@ struct Taps {
 
 __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
 
+// Target statistics (per valid map pixel, per channel): mu_y = G*y and s_y = G*(y^2) - mu_y^2
+// of the clamped target.  They depend on the target only, so a training loop computes them once
+// per view (as tools/resident_traced.py:431-464 precomputes its y maps).
+__global__ __launch_bounds__(256) void k_ssim_stats(const float* __restrict__ y, int H, int W,
+                                                    Taps taps, float* __restrict__ stats) {
+  const int Ho = H - kHalo, Wo = W - kHalo;
+  const int ox0 = blockIdx.x * kTW, oy0 = blockIdx.y * kTH, ch = blockIdx.z;
+  __shared__ float sy[kRH][kRW + 1];
+  __shared__ float v[2][kTH][kRW + 1];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kRH * kRW; i += 256) {
+    const int r = i / kRW, c = i % kRW;
+    const int gr = oy0 + r, gc = ox0 + c;
+    sy[r][c] = (gr < H && gc < W) ? clamp01(y[((int64_t)gr * W + gc) * 3 + ch]) : 0.f;
+  }
+  __syncthreads();
+  if (tid < kRW * (kTH / kVRows)) {
+    const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
+    float acc[2][kVRows];
+#pragma unroll
+    for (int o = 0; o < kVRows; ++o) acc[0][o] = acc[1][o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kVRows + kHalo; ++k) {
+      const float yv = sy[r0 + k][c], yy = yv * yv;
+#pragma unroll
+      for (int o = 0; o < kVRows; ++o) {
+        const int tap = k - o;
+        if (tap >= 0 && tap < kWin) {
+          acc[0][o] += taps.g[tap] * yv;
+          acc[1][o] += taps.g[tap] * yy;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < kVRows; ++o) {
+      v[0][r0 + o][c] = acc[0][o];
+      v[1][r0 + o][c] = acc[1][o];
+    }
+  }
+  __syncthreads();
+  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
+  float f[2][kHCols];
+#pragma unroll
+  for (int o = 0; o < kHCols; ++o) f[0][o] = f[1][o] = 0.f;
+#pragma unroll
+  for (int k = 0; k < kHCols + kHalo; ++k) {
+    const float a = v[0][r][c0 + k], b = v[1][r][c0 + k];
+#pragma unroll
+    for (int o = 0; o < kHCols; ++o) {
+      const int tap = k - o;
+      if (tap >= 0 && tap < kWin) {
+        f[0][o] += taps.g[tap] * a;
+        f[1][o] += taps.g[tap] * b;
+      }
+    }
+  }
+  const int64_t plane = (int64_t)Ho * Wo;
+#pragma unroll
+  for (int o = 0; o < kHCols; ++o) {
+    const int orow = oy0 + r, ocol = ox0 + c0 + o;
+    if (orow < Ho && ocol < Wo) {
+      const int64_t oi = (int64_t)orow * Wo + ocol;
+      stats[(0 * 3 + ch) * plane + oi] = f[0][o];
+      stats[(1 * 3 + ch) * plane + oi] = f[1][o] - f[0][o] * f[0][o];
+    }
+  }
+}
+
+// Map kernel: per output pixel of the valid SSIM map, the image moments mu_x, E[x^2], E[xy]
+// (three filtered images; the target's mu_y, s_y come precomputed), S and its partials
+// dS/dmu_x, dS/dE[x^2], dS/dE[xy] -> maps[3][3][Ho][Wo]; the tile's sum of S.
 __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
-                                                   const float* __restrict__ y, int H, int W,
+                                                   const float* __restrict__ y,
+                                                   const float* __restrict__ stats, int H, int W,
                                                    Taps taps, float* __restrict__ maps,
                                                    float* __restrict__ partials) {
   const int Ho = H - kHalo, Wo = W - kHalo;
   const int ox0 = blockIdx.x * kTW, oy0 = blockIdx.y * kTH, ch = blockIdx.z;
   __shared__ float sx[kRH][kRW + 1], sy[kRH][kRW + 1];
-  __shared__ float v[5][kTH][kRW + 1];
+  __shared__ float v[3][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
   const int tid = threadIdx.x;
-  for (int i = tid; i < kRH * kRW; i += 256) {
-    const int r = i / kRW, c = i % kRW;
-    const int gr = oy0 + r, gc = ox0 + c;
-    float a = 0.f, b = 0.f;
-    if (gr < H && gc < W) {
+  const int64_t plane = (int64_t)Ho * Wo;
+  {
+    constexpr int kPer = (kRH * kRW + 255) / 256;
+    float a[kPer], b[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {  // every load in flight before any is used
+      const int i = min(tid + 256 * k, kRH * kRW - 1);
+      const int gr = min(oy0 + i / kRW, H - 1), gc = min(ox0 + i % kRW, W - 1);
       const int64_t pi = ((int64_t)gr * W + gc) * 3 + ch;
-      a = clamp01(x[pi]);
-      b = clamp01(y[pi]);
+      a[k] = x[pi];
+      b[k] = y[pi];
     }
-    sx[r][c] = a;
-    sy[r][c] = b;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = tid + 256 * k;
+      if (i < kRH * kRW) {
+        const int r = i / kRW, c = i % kRW;
+        const bool in = oy0 + r < H && ox0 + c < W;
+        sx[r][c] = in ? clamp01(a[k]) : 0.f;
+        sy[r][c] = in ? clamp01(b[k]) : 0.f;
+      }
+    }
+  }
+  // this thread's output pixels and their target statistics (loaded ahead of the filtering)
+  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
+  const int orow = oy0 + r;
+  float smu[kHCols], ssy[kHCols];
+#pragma unroll
+  for (int o = 0; o < kHCols; ++o) {
+    const int64_t oi = (int64_t)min(orow, Ho - 1) * Wo + min(ox0 + c0 + o, Wo - 1);
+    smu[o] = stats[(0 * 3 + ch) * plane + oi];
+    ssy[o] = stats[(1 * 3 + ch) * plane + oi];
   }
   __syncthreads();
   // vertical: thread = (column c, chunk of kVRows output rows)
   if (tid < kRW * (kTH / kVRows)) {
     const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
-    float acc[5][kVRows];
+    float acc[3][kVRows];
 #pragma unroll
-    for (int m = 0; m < 5; ++m)
+    for (int m = 0; m < 3; ++m)
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) acc[m][o] = 0.f;
 #pragma unroll
     for (int k = 0; k < kVRows + kHalo; ++k) {
       const float xv = sx[r0 + k][c], yv = sy[r0 + k][c];
-      const float xx = xv * xv, yy = yv * yv, xy = xv * yv;
+      const float xx = xv * xv, xy = xv * yv;
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) {
         const int tap = k - o;
         if (tap >= 0 && tap < kWin) {
           const float gk = taps.g[tap];
           acc[0][o] += gk * xv;
-          acc[1][o] += gk * yv;
-          acc[2][o] += gk * xx;
-          acc[3][o] += gk * yy;
-          acc[4][o] += gk * xy;
+          acc[1][o] += gk * xx;
+          acc[2][o] += gk * xy;
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < 5; ++m)
+    for (int m = 0; m < 3; ++m)
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) v[m][r0 + o][c] = acc[m][o];
   }
   __syncthreads();
   // horizontal: thread = (output row r, chunk of kHCols outputs)
-  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
-  float f[5][kHCols];
+  float f[3][kHCols];
 #pragma unroll
-  for (int m = 0; m < 5; ++m)
+  for (int m = 0; m < 3; ++m)
 #pragma unroll
     for (int o = 0; o < kHCols; ++o) f[m][o] = 0.f;
 #pragma unroll
   for (int k = 0; k < kHCols + kHalo; ++k) {
-    float vv[5];
+    float vv[3];
 #pragma unroll
-    for (int m = 0; m < 5; ++m) vv[m] = v[m][r][c0 + k];
+    for (int m = 0; m < 3; ++m) vv[m] = v[m][r][c0 + k];
 #pragma unroll
     for (int o = 0; o < kHCols; ++o) {
       const int tap = k - o;
       if (tap >= 0 && tap < kWin) {
         const float gk = taps.g[tap];
 #pragma unroll
-        for (int m = 0; m < 5; ++m) f[m][o] += gk * vv[m];
+        for (int m = 0; m < 3; ++m) f[m][o] += gk * vv[m];
       }
     }
   }
   float ssum = 0.0f;
-  const int orow = oy0 + r;
-  const int64_t plane = (int64_t)Ho * Wo;
 #pragma unroll
   for (int o = 0; o < kHCols; ++o) {
     const int ocol = ox0 + c0 + o;
     if (orow < Ho && ocol < Wo) {
-      const float mx = f[0][o], my = f[1][o];
+      const float mx = f[0][o], my = smu[o];
       const float A1 = 2.f * mx * my + kC1;
-      const float A2 = 2.f * (f[4][o] - mx * my) + kC2;
+      const float A2 = 2.f * (f[2][o] - mx * my) + kC2;
       const float B1 = mx * mx + my * my + kC1;
-      const float B2 = (f[2][o] - mx * mx) + (f[3][o] - my * my) + kC2;
-      const float D = B1 * B2;
-      const float Sv = (A1 * A2) / D;
+      const float B2 = (f[1][o] - mx * mx) + ssy[o] + kC2;
+      const float inv_d = 1.0f / (B1 * B2);  // one division; 1/B2 = B1/(B1 B2)
+      const float Sv = A1 * A2 * inv_d;
       const int64_t oi = (int64_t)orow * Wo + ocol;
-      maps[(0 * 3 + ch) * plane + oi] = (2.f / D) * (my * (A2 - A1) - Sv * mx * (B2 - B1));
-      maps[(1 * 3 + ch) * plane + oi] = -Sv / B2;
-      maps[(2 * 3 + ch) * plane + oi] = 2.f * A1 / D;
+      maps[(0 * 3 + ch) * plane + oi] = 2.f * inv_d * (my * (A2 - A1) - Sv * mx * (B2 - B1));
+      maps[(1 * 3 + ch) * plane + oi] = -Sv * B1 * inv_d;
+      maps[(2 * 3 + ch) * plane + oi] = 2.f * A1 * inv_d;
       ssum += Sv;
     }
   }
@@ -147,13 +237,39 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
   const int tid = threadIdx.x;
   const int64_t plane = (int64_t)Ho * Wo;
   // map rows [iy0-10, iy0+16), cols [ix0-10, ix0+32); zero outside the valid map
-  for (int i = tid; i < kRH * kRW; i += 256) {
-    const int r = i / kRW, c = i % kRW;
-    const int mr = iy0 - kHalo + r, mc = ix0 - kHalo + c;
-    const bool ok = mr >= 0 && mr < Ho && mc >= 0 && mc < Wo;
-    const int64_t o = (int64_t)mr * Wo + mc;
+  {
+    constexpr int kPer = (kRH * kRW + 255) / 256;
+    float mv[3][kPer];
 #pragma unroll
-    for (int m = 0; m < 3; ++m) sm[m][r][c] = ok ? maps[(m * 3 + ch) * plane + o] : 0.f;
+    for (int k = 0; k < kPer; ++k) {  // every load in flight before any is used
+      const int i = min(tid + 256 * k, kRH * kRW - 1);
+      const int mr = min(max(iy0 - kHalo + i / kRW, 0), Ho - 1);
+      const int mc = min(max(ix0 - kHalo + i % kRW, 0), Wo - 1);
+      const int64_t o = (int64_t)mr * Wo + mc;
+#pragma unroll
+      for (int m = 0; m < 3; ++m) mv[m][k] = maps[(m * 3 + ch) * plane + o];
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = tid + 256 * k;
+      if (i < kRH * kRW) {
+        const int r = i / kRW, c = i % kRW;
+        const int mr = iy0 - kHalo + r, mc = ix0 - kHalo + c;
+        const bool ok = mr >= 0 && mr < Ho && mc >= 0 && mc < Wo;
+#pragma unroll
+        for (int m = 0; m < 3; ++m) sm[m][r][c] = ok ? mv[m][k] : 0.f;
+      }
+    }
+  }
+  // this thread's pixels (loaded ahead of the filtering)
+  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
+  const int gr = iy0 + r;
+  float xv[kHCols], yv[kHCols];
+#pragma unroll
+  for (int o = 0; o < kHCols; ++o) {
+    const int64_t pi = ((int64_t)min(gr, H - 1) * W + min(ix0 + c0 + o, W - 1)) * 3 + ch;
+    xv[o] = x[pi];
+    yv[o] = y[pi];
   }
   __syncthreads();
   // transposed vertical: input row r receives sum_k g[k] * map[r + 10 - k]
@@ -185,7 +301,6 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
       for (int o = 0; o < kVRows; ++o) v[m][r0 + o][c] = acc[m][o];
   }
   __syncthreads();
-  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
   float t[3][kHCols];
 #pragma unroll
   for (int m = 0; m < 3; ++m)
@@ -209,13 +324,12 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
   const float inv_n = 1.0f / (3.0f * (float)H * (float)W);
   const float inv_ns = 1.0f / (3.0f * (float)Ho * (float)Wo);
   float l1sum = 0.0f;
-  const int gr = iy0 + r;
 #pragma unroll
   for (int o = 0; o < kHCols; ++o) {
     const int gc = ix0 + c0 + o;
     if (gr < H && gc < W) {
       const int64_t pi = ((int64_t)gr * W + gc) * 3 + ch;
-      const float xr = x[pi], yr = y[pi];
+      const float xr = xv[o], yr = yv[o];
       const float d = xr - yr;
       const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
       const bool pass = xr >= 0.f && xr <= 1.f;
@@ -230,10 +344,24 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
     partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = tot;
 }
 
-inline void loss_grids(int H, int W, dim3* gm, dim3* gg) {
+inline dim3 maps_grid(int H, int W) {
   const int Ho = H - kHalo, Wo = W - kHalo;
-  *gm = dim3((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH, 3);
-  *gg = dim3((W + kTW - 1) / kTW, (H + kTH - 1) / kTH, 3);
+  return dim3((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH, 3);
+}
+inline dim3 grad_grid(int H, int W) {
+  return dim3((W + kTW - 1) / kTW, (H + kTH - 1) / kTH, 3);
+}
+
+inline Taps make_taps() {
+  Taps taps;
+  double gd[kWin], sum = 0.0;
+  for (int i = 0; i < kWin; ++i) {
+    const double c = (double)(i - kWin / 2);
+    gd[i] = exp(-(c * c) / (2.0 * 1.5 * 1.5));
+    sum += gd[i];
+  }
+  for (int i = 0; i < kWin; ++i) taps.g[i] = (float)(gd[i] / sum);
+  return taps;
 }
 
 }  // namespace tts
@@ -243,16 +371,43 @@ using namespace tts;
 extern "C" {
 
 size_t tts_loss_workspace_bytes(int H, int W) {
+  // target statistics [2][3] + SSIM partial maps [3][3] planes of (H-10) x (W-10)
   if (H < kWin || W < kWin) return 0;
+  return sizeof(float) * 15 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
+}
+
+// workspace for tts_loss_grad_stats: the three partial maps
+static size_t maps_bytes(int H, int W) {
   return sizeof(float) * 9 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
 }
 
 int tts_loss_partials_count(int H, int W, int* n_ssim) {
   if (H < kWin || W < kWin) return 0;
-  dim3 gm, gg;
-  loss_grids(H, W, &gm, &gg);
+  const dim3 gm = maps_grid(H, W), gg = grad_grid(H, W);
   if (n_ssim) *n_ssim = (int)(gm.x * gm.y * gm.z);
   return (int)(gm.x * gm.y * gm.z + gg.x * gg.y * gg.z);
+}
+
+int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream) {
+  if (!target || !stats) return TTS_EINVAL;
+  if (H < kWin || W < kWin) return TTS_EINVAL;
+  k_ssim_stats<<<maps_grid(H, W), 256, 0, stream>>>(target, H, W, make_taps(), stats);
+  return launch_status();
+}
+
+int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
+                        int W, float lambda, float* gimage, float* partials, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+  if (!image || !target || !stats || !gimage) return TTS_EINVAL;
+  if (H < kWin || W < kWin) return TTS_EINVAL;
+  if (!workspace || workspace_bytes < maps_bytes(H, W)) return TTS_EWORKSPACE;
+  const Taps taps = make_taps();
+  const dim3 gm = maps_grid(H, W), gg = grad_grid(H, W);
+  float* maps = static_cast<float*>(workspace);
+  k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, stats, H, W, taps, maps, partials);
+  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
+                                      partials ? partials + gm.x * gm.y * gm.z : nullptr);
+  return launch_status();
 }
 
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
@@ -261,21 +416,12 @@ int tts_loss_grad(const float* image, const float* target, int H, int W, float l
   if (!image || !target || !gimage) return TTS_EINVAL;
   if (H < kWin || W < kWin) return TTS_EINVAL;
   if (!workspace || workspace_bytes < tts_loss_workspace_bytes(H, W)) return TTS_EWORKSPACE;
-  Taps taps;
-  double gd[kWin], sum = 0.0;
-  for (int i = 0; i < kWin; ++i) {
-    const double c = (double)(i - kWin / 2);
-    gd[i] = exp(-(c * c) / (2.0 * 1.5 * 1.5));
-    sum += gd[i];
-  }
-  for (int i = 0; i < kWin; ++i) taps.g[i] = (float)(gd[i] / sum);
-  dim3 gm, gg;
-  loss_grids(H, W, &gm, &gg);
-  float* maps = static_cast<float*>(workspace);
-  k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, H, W, taps, maps, partials);
-  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
-                                      partials ? partials + gm.x * gm.y * gm.z : nullptr);
-  return launch_status();
+  float* stats = static_cast<float*>(workspace);
+  float* maps = stats + 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
+  const int e = tts_loss_target_stats(target, H, W, stats, stream);
+  if (e) return e;
+  return tts_loss_grad_stats(image, target, stats, H, W, lambda, gimage, partials, maps,
+                             maps_bytes(H, W), stream);
 }
 
 }  // extern "C"
