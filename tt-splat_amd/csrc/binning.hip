@@ -928,10 +928,9 @@ __global__ __launch_bounds__(1024) void k_tile_order(const int32_t* __restrict__
   __shared__ int s_tmp[16];
   for (int c = threadIdx.x; c <= K + 1; c += blockDim.x) s_bins[c] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const int c = min(max(count[t], 0), K);
-    atomicAdd(&s_bins[K - c], 1);
-  }
+  // many tiles share a count (every full tile has K): wave-aggregated increments
+  for (int t = threadIdx.x; t < T; t += blockDim.x)
+    agg_inc(s_bins, K - min(max(count[t], 0), K));
   __syncthreads();
   // K + 1 <= 513 bins: one per thread
   const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
@@ -939,10 +938,8 @@ __global__ __launch_bounds__(1024) void k_tile_order(const int32_t* __restrict__
   const int ex = block_excl_scan<1024>(v, s_tmp, &total);
   if (threadIdx.x <= K) s_bins[threadIdx.x] = ex;
   __syncthreads();
-  for (int t = threadIdx.x; t < T; t += blockDim.x) {
-    const int c = min(max(count[t], 0), K);
-    order[atomicAdd(&s_bins[K - c], 1)] = t;
-  }
+  for (int t = threadIdx.x; t < T; t += blockDim.x)
+    order[agg_inc(s_bins, K - min(max(count[t], 0), K))] = t;
 }
 
 struct BinWorkspace {

@@ -265,22 +265,28 @@ __global__ __launch_bounds__(256) void k_adam(float* __restrict__ params, float*
 // (tile*K + slot, or -1) in stencil order: the slot->gaussian reduce of
 // tools/m9_scatter_oracle.py:35-42 / tools/resident_traced.py:383-395, without atomics and in a
 // fixed order (so the result is reproducible bit for bit).
+// Per-gaussian sum of its slot gradients, in stencil order j (a fixed order: deterministic).
+// Every load is issued before any is used (missing slots read row 0 and are masked), so the
+// gather costs one dependent round trip after the inverse-table load.
 __device__ __forceinline__ void gather_slot_grads(const float* __restrict__ gslot,
                                                   const int32_t* __restrict__ inv, int g,
                                                   float* gin) {
   int e[9];
 #pragma unroll
   for (int j = 0; j < 9; ++j) e[j] = inv[(int64_t)g * 9 + j];
+  float v[9][9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const float* src = gslot + (int64_t)(e[j] >= 0 ? e[j] : 0) * 9;
+#pragma unroll
+    for (int c = 0; c < 9; ++c) v[j][c] = src[c];
+  }
 #pragma unroll
   for (int c = 0; c < 9; ++c) gin[c] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 9; ++j) {
-    if (e[j] >= 0) {
-      const float* src = gslot + (int64_t)e[j] * 9;
+  for (int j = 0; j < 9; ++j)
 #pragma unroll
-      for (int c = 0; c < 9; ++c) gin[c] += src[c];
-    }
-  }
+    for (int c = 0; c < 9; ++c) gin[c] += e[j] >= 0 ? v[j][c] : 0.0f;
 }
 
 __global__ __launch_bounds__(256) void k_slot_reduce(const float* __restrict__ gslot,
@@ -315,27 +321,32 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     float eps) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
-  const Camera cam = load_camera(camera);
   float* p = params + (int64_t)g * 14;
-  float pl[14];
+  float* mg = m + (int64_t)g * 14;
+  float* vg = v + (int64_t)g * 14;
+  // independent loads first: parameters, Adam moments (their latency overlaps the gathers)
+  float pl[14], mm[14], vv[14];
 #pragma unroll
-  for (int i = 0; i < 14; ++i) pl[i] = p[i];
-  GeoState s;
-  geo_forward(pl, cam, near_z, blur, s);
+  for (int i = 0; i < 14; ++i) {
+    pl[i] = p[i];
+    mm[i] = mg[i];
+    vv[i] = vg[i];
+  }
   float gin[9], gout[14];
   gather_slot_grads(gslot, inv, g, gin);
+  const Camera cam = load_camera(camera);
+  GeoState s;
+  geo_forward(pl, cam, near_z, blur, s);
   geo_backward(pl, cam, s, gin, gout);
   const float* f = reinterpret_cast<const float*>(step);
   const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
-  float* mg = m + (int64_t)g * 14;
-  float* vg = v + (int64_t)g * 14;
 #pragma unroll
   for (int i = 0; i < 14; ++i) {
-    float mm = mg[i], vv = vg[i];
-    adam_update(pl[i], mm, vv, gout[i], lr[i], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
-    p[i] = pl[i];
-    mg[i] = mm;
-    vg[i] = vv;
+    float pi = pl[i];
+    adam_update(pi, mm[i], vv[i], gout[i], lr[i], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
+    p[i] = pi;
+    mg[i] = mm[i];
+    vg[i] = vv[i];
     if (gparams) gparams[(int64_t)g * 14 + i] = gout[i];
   }
 }
