@@ -32,6 +32,18 @@ struct Taps {
   float g[kWin];
 };
 
+// Work item of a 1-D grid of gx * gy * 3 blocks: (tile column, tile row, channel), channels
+// innermost and tiles row-major, renumbered so that each XCD sweeps one contiguous band of tiles.
+struct TileItem {
+  int tx, ty, ch;
+};
+__device__ __forceinline__ TileItem tile_item(int gx, int gy) {
+  const int n = gx * gy * 3;
+  const int w = xcd_item(blockIdx.x, n);
+  const int t = w / 3;
+  return {t % gx, t / gx, w - 3 * t};
+}
+
 __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
 
 // Target statistics (per valid map pixel, per channel): mu_y = G*y and s_y = G*(y^2) - mu_y^2
@@ -40,7 +52,8 @@ __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 
 __global__ __launch_bounds__(256) void k_ssim_stats(const float* __restrict__ y, int H, int W,
                                                     Taps taps, float* __restrict__ stats) {
   const int Ho = H - kHalo, Wo = W - kHalo;
-  const int ox0 = blockIdx.x * kTW, oy0 = blockIdx.y * kTH, ch = blockIdx.z;
+  const TileItem it = tile_item((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH);
+  const int ox0 = it.tx * kTW, oy0 = it.ty * kTH, ch = it.ch;
   __shared__ float sy[kRH][kRW + 1];
   __shared__ float v[2][kTH][kRW + 1];
   const int tid = threadIdx.x;
@@ -111,7 +124,8 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
                                                    Taps taps, float* __restrict__ maps,
                                                    float* __restrict__ partials) {
   const int Ho = H - kHalo, Wo = W - kHalo;
-  const int ox0 = blockIdx.x * kTW, oy0 = blockIdx.y * kTH, ch = blockIdx.z;
+  const TileItem it = tile_item((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH);
+  const int ox0 = it.tx * kTW, oy0 = it.ty * kTH, ch = it.ch;
   __shared__ float sx[kRH][kRW + 1], sy[kRH][kRW + 1];
   __shared__ float v[3][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
@@ -221,7 +235,7 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
   }
   const float tot = block_sum256(ssum, s_ftmp);
   if (partials && tid == 0)
-    partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = tot;
+    partials[blockIdx.x] = tot;
 }
 
 __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
@@ -230,7 +244,8 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
                                                    float lambda, float* __restrict__ gout,
                                                    float* __restrict__ partials) {
   const int Ho = H - kHalo, Wo = W - kHalo;
-  const int ix0 = blockIdx.x * kTW, iy0 = blockIdx.y * kTH, ch = blockIdx.z;
+  const TileItem it = tile_item((W + kTW - 1) / kTW, (H + kTH - 1) / kTH);
+  const int ix0 = it.tx * kTW, iy0 = it.ty * kTH, ch = it.ch;
   __shared__ float sm[3][kRH][kRW + 1];
   __shared__ float v[3][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
@@ -341,15 +356,16 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
   }
   const float tot = block_sum256(l1sum, s_ftmp);
   if (partials && tid == 0)
-    partials[(blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = tot;
+    partials[blockIdx.x] = tot;
 }
 
-inline dim3 maps_grid(int H, int W) {
+// 1-D grids (see tile_item): one block per (tile, channel)
+inline int maps_grid(int H, int W) {
   const int Ho = H - kHalo, Wo = W - kHalo;
-  return dim3((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH, 3);
+  return ((Wo + kTW - 1) / kTW) * ((Ho + kTH - 1) / kTH) * 3;
 }
-inline dim3 grad_grid(int H, int W) {
-  return dim3((W + kTW - 1) / kTW, (H + kTH - 1) / kTH, 3);
+inline int grad_grid(int H, int W) {
+  return ((W + kTW - 1) / kTW) * ((H + kTH - 1) / kTH) * 3;
 }
 
 inline Taps make_taps() {
@@ -383,9 +399,9 @@ static size_t maps_bytes(int H, int W) {
 
 int tts_loss_partials_count(int H, int W, int* n_ssim) {
   if (H < kWin || W < kWin) return 0;
-  const dim3 gm = maps_grid(H, W), gg = grad_grid(H, W);
-  if (n_ssim) *n_ssim = (int)(gm.x * gm.y * gm.z);
-  return (int)(gm.x * gm.y * gm.z + gg.x * gg.y * gg.z);
+  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
+  if (n_ssim) *n_ssim = gm;
+  return gm + gg;
 }
 
 int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream) {
@@ -402,11 +418,11 @@ int tts_loss_grad_stats(const float* image, const float* target, const float* st
   if (H < kWin || W < kWin) return TTS_EINVAL;
   if (!workspace || workspace_bytes < maps_bytes(H, W)) return TTS_EWORKSPACE;
   const Taps taps = make_taps();
-  const dim3 gm = maps_grid(H, W), gg = grad_grid(H, W);
+  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
   float* maps = static_cast<float*>(workspace);
   k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, stats, H, W, taps, maps, partials);
   k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
-                                      partials ? partials + gm.x * gm.y * gm.z : nullptr);
+                                      partials ? partials + gm : nullptr);
   return launch_status();
 }
 

@@ -67,6 +67,18 @@ __device__ __forceinline__ int block_excl_scan256(int v, int* tmp, int* total) {
   return block_excl_scan<256>(v, tmp, total);
 }
 
+// MI355X dispatches the workgroups of a 1-D grid round-robin over its 8 XCDs, each with its own
+// L2.  xcd_item(p, n) renumbers physical block p of n so that every XCD takes one contiguous run
+// of work items (XCD x gets items [x*per + min(x, extra), ...), per = n / 8, extra = n % 8): work
+// items that share input lines (neighbouring image tiles, the channels of one tile) then meet in
+// the same L2.  A bijection on [0, n) for any n.
+constexpr int kNumXcd = 8;
+__device__ __forceinline__ int xcd_item(int p, int n) {
+  const int per = n / kNumXcd, extra = n % kNumXcd;
+  const int x = p % kNumXcd, k = p / kNumXcd;
+  return x * per + min(x, extra) + k;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
