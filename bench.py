@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--no-c3", action="store_true", help="skip the G=10k 800x800 run")
     ap.add_argument("--no-c5", action="store_true", help="skip the G=1M 1920x1072 batch run")
     ap.add_argument("--c5-batches", type=int, default=3)
+    ap.add_argument("--no-sh", action="store_true",
+                    help="skip the SH degree 3 run of the headline workload")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB 5 times (a known-size "
                          "kernel to calibrate hardware byte counters against)")
@@ -59,18 +61,28 @@ def load_traffic(kernel, cfg_name):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
-def build_step(cfg, torch, TrainStep, batch=1):
-    """TrainStep for the configuration; targets are the GPU render of the seed-1 set."""
+def sh_rest_init(torch, G, seed, scale=0.1):
+    """Synthetic SH rest coefficients [G,15,3] (seeded normal draws)."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(G, 15, 3, generator=g) * scale
+
+
+def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0):
+    """TrainStep for the configuration; targets are the GPU render of the seed-1 set (with
+    sh_degree > 0: SH rest coefficients drawn from seeds 4 (target) and 3 (trained set))."""
     cams = cfg.cameras()
     P0 = cfg.params(seed=0)
     zero = torch.zeros(cfg.H, cfg.W, 3, device="cuda")
+    sh_t = dict(sh_degree=sh_degree, sh_rest=sh_rest_init(torch, cfg.G, 4)) if sh_degree else {}
+    sh_0 = dict(sh_degree=sh_degree, sh_rest=sh_rest_init(torch, cfg.G, 3)) if sh_degree else {}
     tgt_maker = TrainStep(cfg.params(seed=1), cams, [zero] * len(cams), K=cfg.K, S=cfg.S,
-                          k=cfg.k, dtype=cfg.dtype)
+                          k=cfg.k, dtype=cfg.dtype, **sh_t)
     targets = []
     for ci in range(len(cams)):
         targets.append(tgt_maker.forward(ci).clone())
     del tgt_maker, zero
-    ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k, batch=batch, dtype=cfg.dtype)
+    ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k, batch=batch, dtype=cfg.dtype,
+                   **sh_0)
     return ts
 
 
@@ -116,8 +128,11 @@ def time_kernels(ts, reps, torch, kernels):
     stream = torch.cuda.current_stream()
     P_save, m_save, v_save, s_save = (t.clone() for t in (ts.P, ts.m, ts.v, ts.step_block))
     cam = ts.cams[0]
+    sh = dict(sh_rest=ts.sh, sh_degree=ts.sh_degree)
+    shs = [ts.sh, ts.sh_m, ts.sh_v] if ts.sh is not None else []
+    saved_sh = [t.clone() for t in shs]
     jobs = {
-        "geom_fwd": lambda: kernels.geom_fwd(ts.P, cam, proj=ts.proj, keep=ts.keep),
+        "geom_fwd": lambda: kernels.geom_fwd(ts.P, cam, proj=ts.proj, keep=ts.keep, **sh),
         "binning": lambda: kernels.assign_bins(ts.proj[:, 0:2], ts.keep, ts.H, ts.W, ts.S, ts.K,
                                                ts.span, 1, ts.bin_ws, ts.idx, ts.valid,
                                                ts.count, ts.ncand, ts.inv),
@@ -134,12 +149,14 @@ def time_kernels(ts, reps, torch, kernels):
                                                ts.S, ts.k, ts.image, ts.den, ts.gimage,
                                                ts.gslot, order=ts.order),
         "geom_bwd_adam": lambda: kernels.geom_bwd_adam(ts.P, cam, ts.gslot, ts.inv, ts.m, ts.v,
-                                                       ts.lr, ts.step_block),
+                                                       ts.lr, ts.step_block, sh_m=ts.sh_m,
+                                                       sh_v=ts.sh_v, lr_sh=ts.lr_sh, **sh),
     }
     if ts.batch > 1:
         del jobs["geom_bwd_adam"]
         jobs["geom_bwd_accum"] = lambda: kernels.geom_bwd_accum(ts.P, cam, ts.gslot, ts.inv,
-                                                                ts.gacc, 1.0 / ts.batch)
+                                                                ts.gacc, 1.0 / ts.batch,
+                                                                gacc_sh=ts.gacc_sh, **sh)
     out = {}
     for name, fn in jobs.items():
         for _ in range(3):
@@ -154,10 +171,13 @@ def time_kernels(ts, reps, torch, kernels):
         e1.synchronize()
         out[name] = e0.elapsed_time(e1) / reps * 1e3      # microseconds per launch
     # restore the state the measurement perturbed
-    for dst, src in zip((ts.P, ts.m, ts.v, ts.step_block), (P_save, m_save, v_save, s_save)):
+    for dst, src in zip((ts.P, ts.m, ts.v, ts.step_block, *shs),
+                        (P_save, m_save, v_save, s_save, *saved_sh)):
         dst.copy_(src)
     if ts.gacc is not None:
         ts.gacc.zero_()
+    if ts.gacc_sh is not None:
+        ts.gacc_sh.zero_()
     ts.forward(0)
     torch.cuda.synchronize()
     return out
@@ -181,6 +201,20 @@ def run_c3(args, torch, scenes, TrainStep):
     its = n / time_train(ts, n, 30, torch)
     fps = n / time_forward(ts, n, 30, torch)
     return dict(c3_train_its=its, c3_train_ms=1e3 / its, c3_fwd_fps=fps, c3_fwd_ms=1e3 / fps)
+
+
+def run_sh(args, torch, scenes, kernels, TrainStep):
+    """The headline workload with view-dependent colour: SH degree 3 (45 rest coefficients per
+    gaussian, trained with Adam in the fused geometry backward)."""
+    cfg = scenes.CONFIGS[args.config]
+    ts = build_step(cfg, torch, TrainStep, sh_degree=3)
+    n = 300
+    its = n / time_train(ts, n, 30, torch)
+    fps = n / time_forward(ts, n, 30, torch)
+    kt = time_kernels(ts, 50, torch, kernels)
+    return dict(sh3_train_its=its, sh3_fwd_fps=fps,
+                sh3_kernel_us={k: kt[k] for k in ("geom_fwd", "geom_bwd_adam")},
+                sh3_note="SH degree 3 view-dependent colour on the same workload")
 
 
 def run_c5(args, torch, scenes, kernels, TrainStep):
@@ -300,6 +334,7 @@ def main():
         fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
     extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
+    extra_sh = {} if args.no_sh else run_sh(args, torch, scenes, kernels, TrainStep)
     if args.copy_mib:
         src = torch.ones(args.copy_mib * (1 << 18), device="cuda")
         dst = torch.empty_like(src)
@@ -342,6 +377,7 @@ def main():
             "c2_note": "G=2000 128x128, bf16 render forward (matrix cores), fp32 params/Adam",
             **extra_c3,
             **extra_c5,
+            **extra_sh,
         },
     }
     print(json.dumps(out))

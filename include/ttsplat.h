@@ -50,6 +50,7 @@ extern "C" {
 #define TTS_ESPAN (-5)      /* quantised-distance span outside [1, 8192] */
 #define TTS_EG (-6)         /* G above 2^30 (2^28 for binning) */
 #define TTS_ERADIUS (-7)    /* stencil radius other than 1 */
+#define TTS_ESH (-8)        /* SH degree outside [0, 3], or rest coefficients missing */
 
 /* Library version, (major << 16) | minor. */
 int tts_version(void);
@@ -226,6 +227,50 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
 int tts_geom_bwd_accum(const float* params, int G, const float* camera, float near_z,
                        float blur, const float* gslot, const int32_t* inv, float scale,
                        float* gacc, hipStream_t stream);
+
+/* ---- view-dependent colour: real spherical harmonics, degree sh_degree in [0, 3] ----
+ *
+ * sh_rest holds the rest coefficients (SH indices 1..15) coefficient-major:
+ *   sh_rest[(l * 3 + c) * G + g], l = 0..14, channel c   (spike's color_rest[G,15,3] permuted)
+ * Only the first (sh_degree+1)^2 - 1 rows are read.  colour = max(0.5 + C0*dc + sum_l b_l(dir)
+ * rest_l, 0) with dir = means3d - camera centre (spike/sh.py:54-72 as used by the device step,
+ * tools/resident_traced.py:246-264,339-341).  In the backward the direction is a constant
+ * (tools/resident_traced.py:405-410): dL/drest_l = b_l(dir) * dL/dcolour through the clamp gate. */
+
+/* Geometry forward with SH colour.  Replaces the SHD > 0 branch of
+ * tools/resident_traced.py:339-341 (sh_color_dev). */
+int tts_geom_fwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                    const float* camera, float near_z, float blur, float* proj, uint8_t* keep,
+                    hipStream_t stream);
+
+/* Geometry backward with SH colour: grad9 -> gparams[G,14] and gsh_rest (rest layout; rows
+ * beyond the degree written as zero).  Replaces the SHD > 0 branch of
+ * tools/resident_traced.py:405-410. */
+int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                    const float* camera, float near_z, float blur, const float* grad9,
+                    float* gparams, float* gsh_rest, hipStream_t stream);
+
+/* tts_geom_bwd_adam with SH colour: the rest coefficients and their Adam moments sh_m, sh_v
+ * (rest layout) take the same Adam step with learning rate lr_sh[0] (device scalar; the
+ * reference uses the colour rate / 20).  Replaces adam_crest, tools/resident_traced.py:492-501. */
+int tts_geom_bwd_adam_sh(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
+                         int G, const float* camera, float near_z, float blur, const float* gslot,
+                         const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
+                         const float* lr_sh, const int32_t* step, float beta1, float beta2,
+                         float eps, hipStream_t stream);
+
+/* tts_geom_bwd_accum with SH colour: also gacc_sh += scale * dL/drest (rest layout). */
+int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                          const float* camera, float near_z, float blur, const float* gslot,
+                          const int32_t* inv, float scale, float* gacc, float* gacc_sh,
+                          hipStream_t stream);
+
+/* Adam over n values with one learning rate lr1[0] (device scalar), bias factors from `step`
+ * (tts_adam_advance): the SH rest block's update in batch mode (torch.optim.Adam's step for
+ * one parameter group, spike/train.py:19; tools/resident_traced.py:492-501). */
+int tts_adam_flat(float* params, float* m, float* v, const float* grad, const float* lr1,
+                  int64_t n, const int32_t* step, float beta1, float beta2, float eps,
+                  hipStream_t stream);
 
 /* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */
 int tts_zero(float* buf, int64_t n, hipStream_t stream);

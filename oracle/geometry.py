@@ -99,11 +99,13 @@ def softplus(x):
     return torch.nn.functional.softplus(torch.as_tensor(x))
 
 
-def project_params(P, cam, blur_eps=0.3, near=0.2):
+def project_params(P, cam, blur_eps=0.3, near=0.2, rest=None, sh_degree=0):
     """Geometry + activations of the binned trainer (tools/m4_train_binned.py:194-202).
 
     `cam` is a dict with R_v[3,3], t_v[3], fx, fy, cx, cy.  Returns a dict with
-    mu2d, conic, depth, keep, color_o[G,3], o_col[G] -- differentiable w.r.t. P."""
+    mu2d, conic, depth, keep, color_o[G,3], o_col[G] -- differentiable w.r.t. P (and `rest`).
+    With sh_degree > 0 and rest [G,15,3] the colour is the device step's view-dependent SH
+    colour (oracle/sh.py: view_color); otherwise the DC colour."""
     means, quats, log_scales, color_dc, op = split_params(P)
     R = quat_to_rotmat(quats)
     cov = cov3d(torch.exp(log_scales), R)
@@ -111,7 +113,12 @@ def project_params(P, cam, blur_eps=0.3, near=0.2):
     mu2d, conic, depth, keep = project_ewa(means, cov, cam["R_v"].to(dt), cam["t_v"].to(dt),
                                            cam["fx"], cam["fy"], cam["cx"], cam["cy"],
                                            blur_eps, near)
-    color = color_from_dc(color_dc)
+    if sh_degree > 0 and rest is not None:
+        from . import sh
+        color = sh.view_color(means, color_dc, rest, sh_degree, cam["R_v"].to(dt),
+                              cam["t_v"].to(dt))
+    else:
+        color = color_from_dc(color_dc)
     keo = keep.to(dt) * torch.sigmoid(op)
     return dict(mu2d=mu2d, conic=conic, depth=depth, keep=keep,
                 color_o=keo[:, None] * color, o_col=keo)

@@ -15,13 +15,18 @@ from . import adam, loss, splat
 
 
 def render_and_grad(P, cam, tmap, target, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2,
-                    w_b_raw=-3.0, lambda_ssim=0.2, bins=None, span=2048, stable=False):
-    """Forward + loss + autograd backward.  Returns (img, loss, dL/dP[G,14], extras)."""
+                    w_b_raw=-3.0, lambda_ssim=0.2, bins=None, span=2048, stable=False, rest=None,
+                    sh_degree=0):
+    """Forward + loss + autograd backward.  Returns (img, loss, dL/dP[G,14], extras); with
+    SH rest coefficients (rest [G,15,3], sh_degree > 0) extras["grest"] is dL/drest."""
     Pg = P.detach().clone().requires_grad_(True)
+    rg = None if rest is None else rest.detach().clone().requires_grad_(True)
     img, ex = splat.render_binned(Pg, cam, tmap, R, K, k, blur_eps, near, w_b_raw, None, bins,
-                                  span, stable, return_all=True)
+                                  span, stable, return_all=True, rest=rg, sh_degree=sh_degree)
     L = loss.loss_fn(img, target, lambda_ssim)
     L.backward()
+    if rg is not None:
+        ex["grest"] = rg.grad.detach() if rg.grad is not None else torch.zeros_like(rg)
     return img.detach(), L.detach(), Pg.grad.detach(), ex
 
 

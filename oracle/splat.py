@@ -106,12 +106,12 @@ def theta_u_gathered(conic_t, mu_t, origins, k):
 
 
 def operands(P, cam, tmap, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2, bins=None, span=2048,
-             stable=False):
+             stable=False, rest=None, sh_degree=0):
     """Geometry, binning and per-tile gather (tools/m4_train_binned.py:189-212).
 
     Returns (theta_u[T,6,K], color_o_t[T,K,3], o_col_t[T,K,1], proj, (idx, valid));
     differentiable w.r.t. P except through the bin indices."""
-    pr = geometry.project_params(P, cam, blur_eps, near)
+    pr = geometry.project_params(P, cam, blur_eps, near, rest, sh_degree)
     if bins is None:
         bins = binning.assign_bins(pr["mu2d"], pr["keep"], tmap, R, K, span=span, stable=stable)
     idx, valid = bins
@@ -139,10 +139,13 @@ def tiles_to_image(C, tmap):
 
 
 def render_binned(P, cam, tmap, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0,
-                  c_b=None, bins=None, span=2048, stable=False, return_all=False):
-    """Binned arm-A render (tools/bh_views.py:65-71 on _operands).  Differentiable w.r.t. P."""
+                  c_b=None, bins=None, span=2048, stable=False, return_all=False, rest=None,
+                  sh_degree=0):
+    """Binned arm-A render (tools/bh_views.py:65-71 on _operands).  Differentiable w.r.t. P
+    (and the SH rest coefficients `rest` [G,15,3] when sh_degree > 0)."""
     dt = P.dtype
-    theta, col, oc, pr, bins = operands(P, cam, tmap, R, K, k, blur_eps, near, bins, span, stable)
+    theta, col, oc, pr, bins = operands(P, cam, tmap, R, K, k, blur_eps, near, bins, span, stable,
+                                        rest, sh_degree)
     w_b = geometry.softplus(torch.tensor(w_b_raw, dtype=dt))
     c_b = torch.ones(3, dtype=dt) if c_b is None else c_b.to(dt)
     C, den = splat_tiles(theta, col, oc, tmap.Phi.to(dt), w_b, c_b)

@@ -2,6 +2,14 @@
 // One thread per gaussian; all fp32.  The math follows spike/geometry.py:10-57,
 // spike/forward.py:69-71 and tools/m4_train_binned.py:194-202; the backward is the chain rule
 // of that forward (derived below, checked against torch autograd of the CPU oracle).
+//
+// View-dependent colour (the *_sh kernels): real spherical harmonics of degree 1-3 on top of the
+// DC term, evaluated in the direction means3d - camera centre (spike/sh.py:54-72, as the device
+// step uses it, tools/resident_traced.py:246-264,339-341).  The rest coefficients are stored
+// coefficient-major, rest[(l * 3 + c) * G + g] for l = 0..14 (SH index l + 1) and channel c, so
+// every load and store of a wave is coalesced.  Their gradient is b_{l+1}(dir) * dL/dcolour
+// through the clamp gate; the direction is a constant of the backward, as in
+// tools/resident_traced.py:405-410 (no gradient reaches the means through it).
 
 #include <math.h>
 
@@ -26,9 +34,20 @@ struct GeoState {
   float det_inv;     // 1 / max(det, 1e-12)
   bool dmask;        // det >= 1e-12
   float mux, muy, a, b, c;
-  float color[3];    // max(0.5 + C0*dc, 0)
+  float craw[3];     // colour before the clamp: 0.5 + C0*dc (+ the SH rest terms)
+  float color[3];    // max(craw, 0)
   float o;           // sigmoid(op)
 };
+
+// SH constants (spike/sh.py:9-19,43-51): normalisation of the real SH basis, inria/gsplat signs.
+constexpr float kSC1 = 0.4886025119029199f;
+constexpr float kSC2[5] = {1.0925484305920792f, -1.0925484305920792f, 0.31539156525252005f,
+                           -1.0925484305920792f, 0.5462742152960396f};
+constexpr float kSC3[7] = {-0.5900435899266435f, 2.890611442640554f, -0.4570457994644658f,
+                           0.3731763325901154f, -0.4570457994644658f, 1.445305721320277f,
+                           -0.5900435899266435f};
+constexpr int kShRest = 15;  // rest coefficients per channel at degree 3
+__host__ __device__ __forceinline__ int sh_rest_count(int deg) { return (deg + 1) * (deg + 1) - 1; }
 
 __device__ __forceinline__ void geo_forward(const float* __restrict__ p, const Camera& cam,
                                             float near_z, float blur, GeoState& s) {
@@ -82,14 +101,70 @@ __device__ __forceinline__ void geo_forward(const float* __restrict__ p, const C
   s.b = -s.s01 * s.det_inv;
   s.c = s.s00 * s.det_inv;
 #pragma unroll
-  for (int i = 0; i < 3; ++i) s.color[i] = fmaxf(0.5f + kC0 * p[10 + i], 0.0f);
+  for (int i = 0; i < 3; ++i) {
+    s.craw[i] = 0.5f + kC0 * p[10 + i];
+    s.color[i] = fmaxf(s.craw[i], 0.0f);
+  }
   s.o = sigmoidf_(p[13]);
+}
+
+// Basis b[1..15] of the rest coefficients in the direction mean - camera centre
+// (spike/sh.py:54-72; dir / max(|dir|, 1e-12)).  b[0] = C0 is the DC term's.
+__device__ __forceinline__ void sh_basis(const float* __restrict__ p, const Camera& cam, float* b) {
+  float d[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)  // centre = -R_v^T t_v
+    d[i] = p[i] + (cam.R[0 * 3 + i] * cam.t[0] + cam.R[1 * 3 + i] * cam.t[1] +
+                   cam.R[2 * 3 + i] * cam.t[2]);
+  const float nrm = fmaxf(sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]), 1e-12f);
+  const float x = d[0] / nrm, y = d[1] / nrm, z = d[2] / nrm;
+  const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+  b[0] = kC0;
+  b[1] = -kSC1 * y;
+  b[2] = kSC1 * z;
+  b[3] = -kSC1 * x;
+  b[4] = kSC2[0] * xy;
+  b[5] = kSC2[1] * yz;
+  b[6] = kSC2[2] * (2.0f * zz - xx - yy);
+  b[7] = kSC2[3] * xz;
+  b[8] = kSC2[4] * (xx - yy);
+  b[9] = kSC3[0] * y * (3.0f * xx - yy);
+  b[10] = kSC3[1] * xy * z;
+  b[11] = kSC3[2] * y * (4.0f * zz - xx - yy);
+  b[12] = kSC3[3] * z * (2.0f * zz - 3.0f * xx - 3.0f * yy);
+  b[13] = kSC3[4] * x * (4.0f * zz - xx - yy);
+  b[14] = kSC3[5] * z * (xx - yy);
+  b[15] = kSC3[6] * x * (xx - 3.0f * yy);
+}
+
+// Loads this gaussian's first n rest coefficients of each channel (rv[l * 3 + c]).
+__device__ __forceinline__ void sh_load(const float* __restrict__ rest, int64_t G, int g, int n,
+                                        float* rv) {
+#pragma unroll
+  for (int i = 0; i < 3 * kShRest; ++i) rv[i] = i < 3 * n ? rest[(int64_t)i * G + g] : 0.0f;
+}
+
+// Colour with the rest terms: craw = (C0*dc + sum_l b[l+1] rest[l]) + 0.5, color = max(craw, 0).
+__device__ __forceinline__ void sh_apply(const float* __restrict__ p, const float* b,
+                                         const float* rv, int n, GeoState& s) {
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    float r = kC0 * p[10 + c];
+#pragma unroll
+    for (int l = 0; l < kShRest; ++l)
+      if (l < n) r += b[l + 1] * rv[l * 3 + c];
+    s.craw[c] = r + 0.5f;
+    s.color[c] = fmaxf(s.craw[c], 0.0f);
+  }
 }
 
 // Chain rule of geo_forward.  gin = (ga, gb, gc, gmux, gmuy, gcol_o r,g,b, go_col);
 // gout = the 14 parameter gradients in [G,14] column order.
+// gcolor (optional): dL/dcolour through the clamp gate, the factor of every colour coefficient's
+// gradient (the DC one is gcolor * C0, the SH rest ones gcolor * b_l).
 __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const Camera& cam,
-                                             const GeoState& s, const float* gin, float* gout) {
+                                             const GeoState& s, const float* gin, float* gout,
+                                             float* gcolor = nullptr) {
   // conic = (s11, -s01, s00) / det
   const float di = s.det_inv;
   float gs11 = gin[0] * di, gs01 = -gin[1] * di, gs00 = gin[2] * di;
@@ -174,8 +249,9 @@ __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const 
   const float gkeo = gin[5] * s.color[0] + gin[6] * s.color[1] + gin[7] * s.color[2] + gin[8];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
-    const bool pass = (0.5f + kC0 * p[10 + c]) >= 0.0f;
-    gout[10 + c] = pass ? gin[5 + c] * keo * kC0 : 0.0f;
+    const float gc = s.craw[c] >= 0.0f ? gin[5 + c] * keo : 0.0f;
+    gout[10 + c] = gc * kC0;
+    if (gcolor) gcolor[c] = gc;
   }
   gout[13] = s.keep ? gkeo * s.o * (1.0f - s.o) : 0.0f;
 }
@@ -190,15 +266,26 @@ __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
   return c;
 }
 
+// SH = true: view-dependent colour from the first n = sh_rest_count(deg) rest coefficients.
+template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
+                                                  const float* __restrict__ rest, int n_rest,
                                                   const float* __restrict__ camera, float near_z,
                                                   float blur, float* __restrict__ proj,
                                                   uint8_t* __restrict__ keep) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const Camera cam = load_camera(camera);
+  const float* p = params + (int64_t)g * 14;
+  float rv[SH ? 3 * kShRest : 1];
+  if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
-  geo_forward(params + (int64_t)g * 14, cam, near_z, blur, s);
+  geo_forward(p, cam, near_z, blur, s);
+  if (SH) {
+    float b[16];
+    sh_basis(p, cam, b);
+    sh_apply(p, b, rv, n_rest, s);
+  }
   const float keo = s.keep ? s.o : 0.0f;
   float4* out = reinterpret_cast<float4*>(proj + (int64_t)g * 12);
   out[0] = make_float4(s.mux, s.muy, s.a, s.b);
@@ -207,22 +294,40 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
   keep[g] = s.keep ? 1 : 0;
 }
 
+// gsh (SH only): dL/drest in the rest layout; rows l >= n_rest are written as zero.
+template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ params, int G,
+                                                  const float* __restrict__ rest, int n_rest,
                                                   const float* __restrict__ camera, float near_z,
                                                   float blur, const float* __restrict__ grad9,
-                                                  float* __restrict__ gparams) {
+                                                  float* __restrict__ gparams,
+                                                  float* __restrict__ gsh) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const Camera cam = load_camera(camera);
   const float* p = params + (int64_t)g * 14;
+  float rv[SH ? 3 * kShRest : 1];
+  if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
   geo_forward(p, cam, near_z, blur, s);
-  float gin[9], gout[14];
+  float b[16];
+  if (SH) {
+    sh_basis(p, cam, b);
+    sh_apply(p, b, rv, n_rest, s);
+  }
+  float gin[9], gout[14], gcol[3];
 #pragma unroll
   for (int i = 0; i < 9; ++i) gin[i] = grad9[(int64_t)g * 9 + i];
-  geo_backward(p, cam, s, gin, gout);
+  geo_backward(p, cam, s, gin, gout, gcol);
 #pragma unroll
   for (int i = 0; i < 14; ++i) gparams[(int64_t)g * 14 + i] = gout[i];
+  if (SH) {
+#pragma unroll
+    for (int l = 0; l < kShRest; ++l)
+#pragma unroll
+      for (int c = 0; c < 3; ++c)
+        gsh[(int64_t)(l * 3 + c) * G + g] = l < n_rest ? b[l + 1] * gcol[c] : 0.0f;
+  }
 }
 
 // step[0]: int32 step number; step[1..2]: fp32 1/bc1 and 1/sqrt(bc2) for that step.
@@ -313,12 +418,16 @@ __global__ __launch_bounds__(256) void k_slot_scatter(const float* __restrict__ 
   for (int c = 0; c < 9; ++c) unsafeAtomicAdd(dst + c, gslot[i * 9 + c]);
 }
 
+// SH: the rest coefficients (and their moments sh_m, sh_v, same layout) take the same Adam step
+// with the scalar learning rate lr_sh[0]; rows l >= n_rest are not touched.
+template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd_adam(
-    float* __restrict__ params, int G, const float* __restrict__ camera, float near_z, float blur,
-    const float* __restrict__ gslot, const int32_t* __restrict__ inv,
+    float* __restrict__ params, int G, float* __restrict__ rest, float* __restrict__ sh_m,
+    float* __restrict__ sh_v, int n_rest, const float* __restrict__ camera, float near_z,
+    float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv,
     float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
-    const float* __restrict__ lr, const int32_t* __restrict__ step, float b1, float b2,
-    float eps) {
+    const float* __restrict__ lr, const float* __restrict__ lr_sh,
+    const int32_t* __restrict__ step, float b1, float b2, float eps) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   float* p = params + (int64_t)g * 14;
@@ -332,12 +441,19 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     mm[i] = mg[i];
     vv[i] = vg[i];
   }
-  float gin[9], gout[14];
+  float rv[SH ? 3 * kShRest : 1];
+  if (SH) sh_load(rest, G, g, n_rest, rv);
+  float gin[9], gout[14], gcol[3];
   gather_slot_grads(gslot, inv, g, gin);
   const Camera cam = load_camera(camera);
   GeoState s;
   geo_forward(pl, cam, near_z, blur, s);
-  geo_backward(pl, cam, s, gin, gout);
+  float b[16];
+  if (SH) {
+    sh_basis(pl, cam, b);
+    sh_apply(pl, b, rv, n_rest, s);
+  }
+  geo_backward(pl, cam, s, gin, gout, gcol);
   const float* f = reinterpret_cast<const float*>(step);
   const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
 #pragma unroll
@@ -349,13 +465,33 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     vg[i] = vv[i];
     if (gparams) gparams[(int64_t)g * 14 + i] = gout[i];
   }
+  if (SH) {
+    const float lrs = lr_sh[0];
+#pragma unroll
+    for (int l = 0; l < kShRest; ++l) {
+      if (l < n_rest) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          const int64_t o = (int64_t)(l * 3 + c) * G + g;
+          float pr = rv[l * 3 + c], mr = sh_m[o], vr = sh_v[o];
+          adam_update(pr, mr, vr, b[l + 1] * gcol[c], lrs, inv_bc1, inv_sqrt_bc2, b1, b2, eps);
+          rest[o] = pr;
+          sh_m[o] = mr;
+          sh_v[o] = vr;
+        }
+      }
+    }
+  }
 }
 
-// Batch form: gacc[g] += scale * dL/dparams[g] for one view (one writer per gaussian).
+// Batch form: gacc[g] += scale * dL/dparams[g] for one view (one writer per gaussian); with SH
+// also gacc_sh += scale * dL/drest (rows l < n_rest).
+template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd_accum(
-    const float* __restrict__ params, int G, const float* __restrict__ camera, float near_z,
-    float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv, float scale,
-    float* __restrict__ gacc) {
+    const float* __restrict__ params, int G, const float* __restrict__ rest, int n_rest,
+    const float* __restrict__ camera, float near_z, float blur, const float* __restrict__ gslot,
+    const int32_t* __restrict__ inv, float scale, float* __restrict__ gacc,
+    float* __restrict__ gacc_sh) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const Camera cam = load_camera(camera);
@@ -363,14 +499,48 @@ __global__ __launch_bounds__(256) void k_geom_bwd_accum(
   float pl[14];
 #pragma unroll
   for (int i = 0; i < 14; ++i) pl[i] = p[i];
+  float rv[SH ? 3 * kShRest : 1];
+  if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
   geo_forward(pl, cam, near_z, blur, s);
-  float gin[9], gout[14];
+  float b[16];
+  if (SH) {
+    sh_basis(pl, cam, b);
+    sh_apply(pl, b, rv, n_rest, s);
+  }
+  float gin[9], gout[14], gcol[3];
   gather_slot_grads(gslot, inv, g, gin);
-  geo_backward(pl, cam, s, gin, gout);
+  geo_backward(pl, cam, s, gin, gout, gcol);
   float* a = gacc + (int64_t)g * 14;
 #pragma unroll
   for (int i = 0; i < 14; ++i) a[i] += scale * gout[i];
+  if (SH) {
+#pragma unroll
+    for (int l = 0; l < kShRest; ++l) {
+      if (l < n_rest) {
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+          gacc_sh[(int64_t)(l * 3 + c) * G + g] += scale * (b[l + 1] * gcol[c]);
+      }
+    }
+  }
+}
+
+// Adam over a flat array with one learning rate lr1[0] (the SH rest block in batch mode).
+__global__ __launch_bounds__(256) void k_adam_flat(float* __restrict__ params,
+                                                   float* __restrict__ m, float* __restrict__ v,
+                                                   const float* __restrict__ grad,
+                                                   const float* __restrict__ lr1, int64_t n,
+                                                   const int32_t* __restrict__ step, float b1,
+                                                   float b2, float eps) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float* f = reinterpret_cast<const float*>(step);
+  float pp = params[i], mm = m[i], vv = v[i];
+  adam_update(pp, mm, vv, grad[i], lr1[0], f[1], f[2], b1, b2, eps);
+  params[i] = pp;
+  m[i] = mm;
+  v[i] = vv;
 }
 
 __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
@@ -396,6 +566,7 @@ const char* tts_strerror(int code) {
     case TTS_ESPAN: return "span must be in [1, 8192]";
     case TTS_EG: return "G must be below 2^30 (at most 2^28 for binning)";
     case TTS_ERADIUS: return "only stencil radius R = 1 is supported";
+    case TTS_ESH: return "SH degree must be in [0, 3], with rest coefficients when above 0";
     default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }
 }
@@ -405,7 +576,28 @@ int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, 
   if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_fwd<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, proj, keep);
+  k_geom_fwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera, near_z,
+                                                        blur, proj, keep);
+  return launch_status();
+}
+
+// SH degree check shared by the *_sh entry points: 0 <= deg <= 3, rest present when deg > 0.
+static int sh_args(int deg, const void* rest) {
+  if (deg < 0 || deg > 3) return TTS_ESH;
+  if (deg > 0 && !rest) return TTS_ESH;
+  return TTS_OK;
+}
+
+int tts_geom_fwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                    const float* camera, float near_z, float blur, float* proj, uint8_t* keep,
+                    hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
+  if (const int e = sh_args(sh_degree, sh_rest)) return e;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_fwd<true><<<grid1d(G, 256), 256, 0, stream>>>(params, G, sh_rest,
+                                                       sh_rest_count(sh_degree), camera, near_z,
+                                                       blur, proj, keep);
   return launch_status();
 }
 
@@ -414,7 +606,32 @@ int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, 
   if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, grad9, gparams);
+  k_geom_bwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera, near_z,
+                                                        blur, grad9, gparams, nullptr);
+  return launch_status();
+}
+
+int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                    const float* camera, float near_z, float blur, const float* grad9,
+                    float* gparams, float* gsh_rest, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams || !gsh_rest)))
+    return TTS_EINVAL;
+  if (const int e = sh_args(sh_degree, sh_rest)) return e;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd<true><<<grid1d(G, 256), 256, 0, stream>>>(params, G, sh_rest,
+                                                       sh_rest_count(sh_degree), camera, near_z,
+                                                       blur, grad9, gparams, gsh_rest);
+  return launch_status();
+}
+
+int tts_adam_flat(float* params, float* m, float* v, const float* grad, const float* lr1,
+                  int64_t n, const int32_t* step, float beta1, float beta2, float eps,
+                  hipStream_t stream) {
+  if (n < 0 || (n > 0 && (!params || !m || !v || !grad || !lr1 || !step))) return TTS_EINVAL;
+  if (n == 0) return TTS_OK;
+  k_adam_flat<<<grid1d(n, 256), 256, 0, stream>>>(params, m, v, grad, lr1, n, step, beta1, beta2,
+                                                  eps);
   return launch_status();
 }
 
@@ -440,8 +657,24 @@ int tts_geom_bwd_accum(const float* params, int G, const float* camera, float ne
   if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !gacc))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_accum<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, gslot,
-                                                       inv, scale, gacc);
+  k_geom_bwd_accum<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera,
+                                                              near_z, blur, gslot, inv, scale,
+                                                              gacc, nullptr);
+  return launch_status();
+}
+
+int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degree, int G,
+                          const float* camera, float near_z, float blur, const float* gslot,
+                          const int32_t* inv, float scale, float* gacc, float* gacc_sh,
+                          hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !gacc))) return TTS_EINVAL;
+  if (const int e = sh_args(sh_degree, sh_rest)) return e;
+  if (sh_degree > 0 && !gacc_sh) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd_accum<true><<<grid1d(G, 256), 256, 0, stream>>>(
+      params, G, sh_rest, sh_rest_count(sh_degree), camera, near_z, blur, gslot, inv, scale, gacc,
+      gacc_sh);
   return launch_status();
 }
 
@@ -453,9 +686,26 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
     return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_adam<<<grid1d(G, 256), 256, 0, stream>>>(params, G, camera, near_z, blur, gslot,
-                                                      inv, gparams, m, v, lr, step, beta1, beta2,
-                                                      eps);
+  k_geom_bwd_adam<false><<<grid1d(G, 256), 256, 0, stream>>>(
+      params, G, nullptr, nullptr, nullptr, 0, camera, near_z, blur, gslot, inv, gparams, m, v,
+      lr, nullptr, step, beta1, beta2, eps);
+  return launch_status();
+}
+
+int tts_geom_bwd_adam_sh(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
+                         int G, const float* camera, float near_z, float blur, const float* gslot,
+                         const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
+                         const float* lr_sh, const int32_t* step, float beta1, float beta2,
+                         float eps, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !m || !v || !lr || !step)))
+    return TTS_EINVAL;
+  if (const int e = sh_args(sh_degree, sh_rest)) return e;
+  if (sh_degree > 0 && (!sh_m || !sh_v || !lr_sh)) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_geom_bwd_adam<true><<<grid1d(G, 256), 256, 0, stream>>>(
+      params, G, sh_rest, sh_m, sh_v, sh_rest_count(sh_degree), camera, near_z, blur, gslot, inv,
+      gparams, m, v, lr, lr_sh, step, beta1, beta2, eps);
   return launch_status();
 }
 

@@ -52,6 +52,16 @@ SIGNATURES = {
     "tts_zero": (_c_int, [_vp, _c_i64, _vp]),
     "tts_geom_bwd_accum": (_c_int, [_vp, _c_int, _vp, _c_float, _c_float, _vp, _vp, _c_float,
                                     _vp, _vp]),
+    "tts_geom_fwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp]),
+    "tts_geom_bwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp,
+                                 _vp]),
+    "tts_geom_bwd_adam_sh": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
+                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_float, _c_float,
+                                      _c_float, _vp]),
+    "tts_geom_bwd_accum_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp,
+                                       _c_float, _vp, _vp, _vp]),
+    "tts_adam_flat": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_float, _c_float, _c_float,
+                               _vp]),
     "tts_dense_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "tts_render_dense": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _vp, _vp, _vp]),
     "tts_render_dense_bwd": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _vp, _vp, _vp,

@@ -30,27 +30,69 @@ def version():
 
 
 # ------------------------------------------------------------------------------- geometry --
-def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None):
+SH_REST = 15   # rest coefficients per channel (SH degrees 1-3)
+
+
+def sh_rest_layout(color_rest):
+    """spike's color_rest [G,15,3] -> the library's coefficient-major rest block [15,3,G]."""
+    if color_rest.dim() != 3 or tuple(color_rest.shape[1:]) != (SH_REST, 3):
+        raise ValueError(f"color_rest must be [G,{SH_REST},3], got {tuple(color_rest.shape)}")
+    return color_rest.permute(1, 2, 0).contiguous()
+
+
+def sh_rest_model(rest):
+    """The library's rest block [15,3,G] -> spike's color_rest layout [G,15,3]."""
+    return rest.permute(2, 0, 1).contiguous()
+
+
+def _sh_check(sh_rest, sh_degree, G, dev):
+    if not 0 <= int(sh_degree) <= 3:
+        raise ValueError(f"sh_degree must be in [0, 3], got {sh_degree}")
+    if int(sh_degree) > 0:
+        if sh_rest is None:
+            raise ValueError("sh_degree > 0 needs the rest coefficients sh_rest [15,3,G]")
+        require(sh_rest, "sh_rest", F32, (SH_REST, 3, G), dev)
+
+
+def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest=None,
+             sh_degree=0):
+    """Projection + activations -> proj[G,12], keep[G].  sh_degree > 0: view-dependent colour
+    from the rest coefficients sh_rest [15,3,G] (sh_rest_layout of spike's color_rest)."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
     require(camera, "camera", F32, (16,), dev)
+    _sh_check(sh_rest, sh_degree, G, dev)
     proj = torch.empty(G, 12, device=dev, dtype=F32) if proj is None else proj
     keep = torch.empty(G, device=dev, dtype=U8) if keep is None else keep
     _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
     require(keep, "keep", U8, (G,), dev)
-    call("tts_geom_fwd", ptr(params), G, ptr(camera), near, blur, ptr(proj), ptr(keep), stream())
+    if sh_degree > 0:
+        call("tts_geom_fwd_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera), near,
+             blur, ptr(proj), ptr(keep), stream())
+    else:
+        call("tts_geom_fwd", ptr(params), G, ptr(camera), near, blur, ptr(proj), ptr(keep),
+             stream())
     return proj, keep
 
 
-def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None):
+def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None, sh_rest=None, sh_degree=0,
+             gsh_out=None):
+    """grad9[G,9] -> dL/dparams[G,14]; with sh_degree > 0 returns (gparams, dL/dsh_rest)."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
     require(camera, "camera", F32, (16,), dev)
     require(grad9, "grad9", F32, (G, 9), dev)
+    _sh_check(sh_rest, sh_degree, G, dev)
     out = torch.empty(G, 14, device=dev, dtype=F32) if out is None else out
     require(out, "gparams", F32, (G, 14), dev)
+    if sh_degree > 0:
+        gsh = torch.empty(SH_REST, 3, G, device=dev, dtype=F32) if gsh_out is None else gsh_out
+        require(gsh, "gsh_out", F32, (SH_REST, 3, G), dev)
+        call("tts_geom_bwd_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera), near,
+             blur, ptr(grad9), ptr(out), ptr(gsh), stream())
+        return out, gsh
     call("tts_geom_bwd", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(out), stream())
     return out
 
@@ -347,8 +389,21 @@ def adam(params, m, v, grad, lr, step, b1=BETA1, b2=BETA2, eps=EPS):
          stream())
 
 
-def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=BLUR):
-    """gacc[G,14] += scale * dL/dparams for one view (slot gradients gathered through inv)."""
+def adam_flat(params, m, v, grad, lr1, step, b1=BETA1, b2=BETA2, eps=EPS):
+    """Adam over any contiguous fp32 block with one learning rate lr1[1] (device scalar)."""
+    dev = params.device
+    for t, n in ((params, "params"), (m, "m"), (v, "v"), (grad, "grad")):
+        require(t, n, F32, tuple(params.shape), dev)
+    require(lr1, "lr1", F32, (1,), dev)
+    require(step, "step", I32, (4,), dev)
+    call("tts_adam_flat", ptr(params), ptr(m), ptr(v), ptr(grad), ptr(lr1), params.numel(),
+         ptr(step), b1, b2, eps, stream())
+
+
+def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=BLUR,
+                   sh_rest=None, sh_degree=0, gacc_sh=None):
+    """gacc[G,14] += scale * dL/dparams for one view (slot gradients gathered through inv);
+    with sh_degree > 0 also gacc_sh[15,3,G] += scale * dL/dsh_rest."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
@@ -356,14 +411,23 @@ def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=
     require(gslot, "gslot", F32, None, dev)
     require(inv, "inv", I32, (G, 9), dev)
     require(gacc, "gacc", F32, (G, 14), dev)
+    _sh_check(sh_rest, sh_degree, G, dev)
+    if sh_degree > 0:
+        require(gacc_sh, "gacc_sh", F32, (SH_REST, 3, G), dev)
+        call("tts_geom_bwd_accum_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera),
+             near, blur, ptr(gslot), ptr(inv), float(scale), ptr(gacc), ptr(gacc_sh), stream())
+        return gacc
     call("tts_geom_bwd_accum", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
          float(scale), ptr(gacc), stream())
     return gacc
 
 
 def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
-                  b1=BETA1, b2=BETA2, eps=EPS):
-    """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel."""
+                  b1=BETA1, b2=BETA2, eps=EPS, sh_rest=None, sh_m=None, sh_v=None, lr_sh=None,
+                  sh_degree=0):
+    """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel.
+    With sh_degree > 0 the rest coefficients sh_rest (moments sh_m, sh_v, all [15,3,G]) take
+    the same Adam step at learning rate lr_sh[1] (device scalar)."""
     G = params.shape[0]
     dev = params.device
     for t, n in ((params, "params"), (m, "m"), (v, "v")):
@@ -377,6 +441,15 @@ def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BL
     require(step, "step", I32, (4,), dev)
     if gparams is not None:
         require(gparams, "gparams", F32, (G, 14), dev)
+    _sh_check(sh_rest, sh_degree, G, dev)
+    if sh_degree > 0:
+        require(sh_m, "sh_m", F32, (SH_REST, 3, G), dev)
+        require(sh_v, "sh_v", F32, (SH_REST, 3, G), dev)
+        require(lr_sh, "lr_sh", F32, (1,), dev)
+        call("tts_geom_bwd_adam_sh", ptr(params), ptr(sh_rest), ptr(sh_m), ptr(sh_v),
+             int(sh_degree), G, ptr(camera), near, blur, ptr(gslot), ptr(inv), ptr(gparams),
+             ptr(m), ptr(v), ptr(lr), ptr(lr_sh), ptr(step), b1, b2, eps, stream())
+        return
     call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
          ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
 

@@ -41,11 +41,15 @@ class TrainStep:
     round-robin loop of tools/resident_traced.py:667-757).
     batch = B > 1: the views are grouped into consecutive batches of B; step(i) renders and
     backpropagates every view of batch i, accumulating the mean gradient, then applies one Adam
-    update (the full-batch loop of spike/train.py:21-33 over B views)."""
+    update (the full-batch loop of spike/train.py:21-33 over B views).
+    sh_degree = 1..3: view-dependent colour (the SHD > 0 mode of tools/resident_traced.py:237-264):
+    sh_rest is spike's color_rest [G,15,3] (zeros if omitted), trained with Adam at lr_sh
+    (default: the colour learning rate / 20, as the reference); the direction is constant in
+    the backward, as there."""
 
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
-                 dtype="fp32"):
+                 dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -66,6 +70,18 @@ class TrainStep:
         self.v = torch.zeros(G, 14, device=dev, dtype=F32)
         self.step_block = kernels.adam_state(dev)
         self.lr = (lr_vector(device=dev) if lr is None else torch.as_tensor(lr, dtype=F32).to(dev)).contiguous()
+        self.sh_degree = int(sh_degree)
+        if not 0 <= self.sh_degree <= 3:
+            raise ValueError(f"sh_degree must be in [0, 3], got {sh_degree}")
+        if self.sh_degree > 0:
+            rest = (torch.zeros(G, kernels.SH_REST, 3) if sh_rest is None else sh_rest)
+            self.sh = kernels.sh_rest_layout(rest.to(dev, F32))
+            self.sh_m = torch.zeros_like(self.sh)
+            self.sh_v = torch.zeros_like(self.sh)
+            lrs = float(self.lr[10]) / 20.0 if lr_sh is None else float(lr_sh)
+            self.lr_sh = torch.tensor([lrs], dtype=F32, device=dev)
+        else:
+            self.sh = self.sh_m = self.sh_v = self.lr_sh = None
         w_b = torch.nn.functional.softplus(torch.tensor(float(w_b_raw)))
         self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
         # per-view inputs
@@ -95,12 +111,20 @@ class TrainStep:
         if self.batch < 1 or len(self.cams) % self.batch:
             raise ValueError(f"{len(self.cams)} views do not split into batches of {batch}")
         self.gacc = torch.zeros(G, 14, device=dev, dtype=F32) if self.batch > 1 else None
+        self.gacc_sh = (torch.zeros_like(self.sh) if self.batch > 1 and self.sh_degree > 0
+                        else None)
         self.graphs = {}
+
+    @property
+    def color_rest(self):
+        """The SH rest coefficients in spike's layout [G,15,3] (None without SH)."""
+        return None if self.sh is None else kernels.sh_rest_model(self.sh)
 
     # ---------------------------------------------------------------------------------
     def forward(self, ci=0):
         """Geometry + binning + fused splat for camera ci into self.image (no training)."""
-        kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep)
+        kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep, sh_rest=self.sh,
+                         sh_degree=self.sh_degree)
         kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
                             self.ncand, self.inv)
@@ -129,32 +153,42 @@ class TrainStep:
 
     def enqueue(self, i=0):
         """Enqueue training step i (camera i, or batch i) on the current stream."""
+        sh = dict(sh_rest=self.sh, sh_degree=self.sh_degree)
         if self.batch == 1:
             self._view_backward(i)
             kernels.adam_advance(self.step_block)
             kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
-                                  self.lr, self.step_block)
+                                  self.lr, self.step_block, sh_m=self.sh_m, sh_v=self.sh_v,
+                                  lr_sh=self.lr_sh, **sh)
             return
         scale = 1.0 / self.batch
         for ci in range(i * self.batch, (i + 1) * self.batch):
             self._view_backward(ci)
-            kernels.geom_bwd_accum(self.P, self.cams[ci], self.gslot, self.inv, self.gacc, scale)
+            kernels.geom_bwd_accum(self.P, self.cams[ci], self.gslot, self.inv, self.gacc, scale,
+                                   gacc_sh=self.gacc_sh, **sh)
         kernels.adam_advance(self.step_block)
         kernels.adam(self.P, self.m, self.v, self.gacc, self.lr, self.step_block)
         kernels.zero_(self.gacc)
+        if self.sh_degree > 0:
+            kernels.adam_flat(self.sh, self.sh_m, self.sh_v, self.gacc_sh, self.lr_sh,
+                              self.step_block)
+            kernels.zero_(self.gacc_sh)
 
     def capture(self, cams=None):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
         kernel's code object is resident) and its effect on the state is rolled back."""
         cams = range(self.n_steps) if cams is None else cams
-        state = [t.clone() for t in (self.P, self.m, self.v, self.step_block)]
+        live = [self.P, self.m, self.v, self.step_block]
+        if self.sh is not None:
+            live += [self.sh, self.sh_m, self.sh_v]
+        state = [t.clone() for t in live]
         side = torch.cuda.Stream(device=self.dev)
         side.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(side):
             for ci in cams:
                 self.enqueue(ci)
         torch.cuda.current_stream(self.dev).wait_stream(side)
-        for dst, src in zip((self.P, self.m, self.v, self.step_block), state):
+        for dst, src in zip(live, state):
             dst.copy_(src)
         torch.cuda.synchronize(self.dev)
         for ci in cams:
