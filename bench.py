@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--c5-batches", type=int, default=3)
     ap.add_argument("--no-sh", action="store_true",
                     help="skip the SH degree 3 run of the headline workload")
+    ap.add_argument("--no-mcmc", action="store_true",
+                    help="skip the MCMC density-control run of the headline workload")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB 5 times (a known-size "
                          "kernel to calibrate hardware byte counters against)")
@@ -67,7 +69,7 @@ def sh_rest_init(torch, G, seed, scale=0.1):
     return torch.randn(G, 15, 3, generator=g) * scale
 
 
-def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0):
+def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0, mcmc=None):
     """TrainStep for the configuration; targets are the GPU render of the seed-1 set (with
     sh_degree > 0: SH rest coefficients drawn from seeds 4 (target) and 3 (trained set))."""
     cams = cfg.cameras()
@@ -82,7 +84,7 @@ def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0):
         targets.append(tgt_maker.forward(ci).clone())
     del tgt_maker, zero
     ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k, batch=batch, dtype=cfg.dtype,
-                   **sh_0)
+                   mcmc=mcmc, **sh_0)
     return ts
 
 
@@ -217,6 +219,44 @@ def run_sh(args, torch, scenes, kernels, TrainStep):
                 sh3_note="SH degree 3 view-dependent colour on the same workload")
 
 
+MCMC_OPTS = dict(lambda_o=0.01, lambda_s=0.01, noise_lr=5e5, relocate_every=100,
+                 dead_thr=0.005, offset=0.005, seed=1)
+
+
+def run_mcmc(args, torch, scenes, TrainStep):
+    """The headline workload with fixed-count MCMC density control (spike/mcmc.py defaults:
+    regulariser 0.01/0.01, SGLD noise_lr 5e5, relocation every 100 steps, threshold 0.005),
+    starting with a seeded 10 % of the gaussians dead (opacity 1e-3): train it/s over 300 steps
+    (3 relocations inside the timed region), then one relocation of a fresh 10 % dead set timed
+    with HIP events (state restored before each repetition)."""
+    import math
+    cfg = scenes.CONFIGS[args.config]
+    ts = build_step(cfg, torch, TrainStep, mcmc=MCMC_OPTS)
+    g = torch.Generator().manual_seed(5)
+    dead = (torch.rand(cfg.G, generator=g) < 0.1).cuda()
+    dead_op = math.log(1e-3 / (1 - 1e-3))
+    ts.P[dead, 13] = dead_op
+    n = 300
+    its = n / time_train(ts, n, 30, torch)
+    relocated = int(ts.relocations)
+    snap = ts.P.clone()
+    snap[dead, 13] = dead_op
+    stream = torch.cuda.current_stream()
+    reps, total_ms = 20, 0.0
+    for _ in range(reps):
+        ts.P.copy_(snap)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        ts.reloc_graph.replay()
+        e1.record(stream)
+        e1.synchronize()
+        total_ms += e0.elapsed_time(e1)
+    return dict(mcmc_train_its=its, mcmc_relocate_us=total_ms / reps * 1e3,
+                mcmc_relocate_moved=int(ts.moved), mcmc_relocations_in_run=relocated,
+                mcmc_opts=MCMC_OPTS)
+
+
 def run_c5(args, torch, scenes, kernels, TrainStep):
     """G=1M clustered, 1920x1072, K=256: batches of 64 views (fwd + bwd of every view, mean
     gradient, one Adam update), one graph per batch."""
@@ -335,6 +375,7 @@ def main():
     extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
     extra_sh = {} if args.no_sh else run_sh(args, torch, scenes, kernels, TrainStep)
+    extra_mc = {} if args.no_mcmc else run_mcmc(args, torch, scenes, TrainStep)
     if args.copy_mib:
         src = torch.ones(args.copy_mib * (1 << 18), device="cuda")
         dst = torch.empty_like(src)
@@ -378,6 +419,7 @@ def main():
             **extra_c3,
             **extra_c5,
             **extra_sh,
+            **extra_mc,
         },
     }
     print(json.dumps(out))

@@ -250,14 +250,24 @@ int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, in
                     const float* camera, float near_z, float blur, const float* grad9,
                     float* gparams, float* gsh_rest, hipStream_t stream);
 
-/* tts_geom_bwd_adam with SH colour: the rest coefficients and their Adam moments sh_m, sh_v
- * (rest layout) take the same Adam step with learning rate lr_sh[0] (device scalar; the
- * reference uses the colour rate / 20).  Replaces adam_crest, tools/resident_traced.py:492-501. */
-int tts_geom_bwd_adam_sh(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
+/* tts_geom_bwd_adam with the optional extensions of the device step, in one kernel:
+ *  - SH colour (sh_degree > 0): the rest coefficients and their Adam moments sh_m, sh_v (rest
+ *    layout) take the same Adam step with learning rate lr_sh[0] (device scalar; the reference
+ *    uses the colour rate / 20).  Replaces adam_crest, tools/resident_traced.py:492-501.
+ *  - MCMC regulariser (lambda_o, lambda_s > 0): the gradient of lambda_o mean(sigmoid(op)) +
+ *    lambda_s mean(exp(log_scales)) is added before Adam (spike/mcmc.py:18-22; device form
+ *    tools/resident_traced.py:732-738).
+ *  - SGLD (noise_lr > 0): after Adam, means += R(q) diag(exp(ls)) eps * sigmoid(100 ((1 - o) -
+ *    0.995)) * noise_lr * lr[0] with eps three Philox4x32-10 normals for counter (g, step[0],
+ *    1, 0) and key (seed, 0) (spike/mcmc.py:25-34; the reference draws eps on the host,
+ *    tools/resident_traced.py:620-629).
+ * sh_rest, sh_m, sh_v, lr_sh may be NULL when sh_degree is 0. */
+int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
                          int G, const float* camera, float near_z, float blur, const float* gslot,
                          const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
                          const float* lr_sh, const int32_t* step, float beta1, float beta2,
-                         float eps, hipStream_t stream);
+                         float eps, float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
+                         hipStream_t stream);
 
 /* tts_geom_bwd_accum with SH colour: also gacc_sh += scale * dL/drest (rest layout). */
 int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degree, int G,
@@ -271,6 +281,34 @@ int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degr
 int tts_adam_flat(float* params, float* m, float* v, const float* grad, const float* lr1,
                   int64_t n, const int32_t* step, float beta1, float beta2, float eps,
                   hipStream_t stream);
+
+/* ---- fixed-count MCMC density control (spike/mcmc.py) ---- */
+
+/* Batch form of the MCMC regulariser: grad[G,14] += d/dparams of lambda_o mean(sigmoid(op)) +
+ * lambda_s mean(exp(log_scales)) (spike/mcmc.py:18-22). */
+int tts_mcmc_reg_grad(const float* params, int G, float lambda_o, float lambda_s, float* grad,
+                      hipStream_t stream);
+
+/* Batch form of the SGLD step on the means (see tts_geom_bwd_adam_ex; noise scale
+ * noise_lr * lr[0]).  Replaces add_sgld_noise, spike/mcmc.py:25-34. */
+int tts_sgld_noise(float* params, int G, const float* lr, float noise_lr, uint32_t seed,
+                   const int32_t* step, hipStream_t stream);
+
+/* Workspace for tts_relocate (G gaussians). */
+size_t tts_relocate_workspace_bytes(int G);
+
+/* Relocation (spike/mcmc.py:41-93; host code in the reference, tools/resident_traced.py:631-663):
+ * dead slots (sigmoid(op) < dead_thr), in ascending index order, each copy a live gaussian drawn
+ * with probability proportional to its opacity (inverse CDF over the live gaussians in index
+ * order, uniform from Philox counter (i, step[0], 2, 0), key (seed, 0)); the copy's means are
+ * offset by offset * N(0,1) (Philox counter (i, step[0], 3, 0)); a target drawn n times and its
+ * copies get opacity clamp(o / (n + 1), 1e-6, 1 - 1e-6); the Adam moments of dead slots and
+ * targets are zeroed (m, v [G,14]; sh_m, sh_v when sh_rest is given, whose 15 rest rows are
+ * copied too).  moved (optional, device int32) receives the number of relocated slots (0 when no
+ * gaussian is live).  Six kernels with fixed grids: no host synchronisation, graph-capturable. */
+int tts_relocate(float* params, float* m, float* v, float* sh_rest, float* sh_m, float* sh_v,
+                 int G, float dead_thr, float offset, uint32_t seed, const int32_t* step,
+                 int32_t* moved, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Fill n fp32 values with zero (a kernel, so graph captures hold no memset node). */
 int tts_zero(float* buf, int64_t n, hipStream_t stream);

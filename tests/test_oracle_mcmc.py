@@ -1,0 +1,137 @@
+"""The oracle's MCMC pieces, pinned without the reference:
+
+* Philox4x32-10 against the known-answer vectors of the Random123 distribution (the published
+  generator the device kernels use); moments of the derived normals and uniforms;
+* spike/tests/test_mcmc.py restated on the oracle's dense render: n coincident copies at o/n
+  render exactly like one gaussian at o (with a negative control), a relocation with zero
+  offset leaves the render nearly unchanged, SGLD noise is gated to near-dead gaussians;
+* the regularisation gradient in closed form (d/dop = lambda_o/G o(1-o),
+  d/dlog_s = lambda_s/(3G) s);
+* the inverse-CDF target pick: empirical frequencies proportional to opacity.
+"""
+import math
+
+import numpy as np
+import torch
+
+from oracle import geometry, mcmc, rng, splat
+
+D = torch.float64
+
+
+def test_philox_known_answers():
+    kat = [
+        ([0, 0, 0, 0], [0, 0], "6627e8d5 e169c58d bc57ac4c 9b00dbd8"),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, "408f276d 41c83b0e a20bc7c6 6d5451fd"),
+        ([0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344], [0xA4093822, 0x299F31D0],
+         "d16cfe09 94fdcceb 5001e420 24126ea1"),
+    ]
+    for ctr, key, want in kat:
+        out = rng.philox4x32_10(np.array(ctr, dtype=np.uint64), np.array(key, dtype=np.uint64))
+        assert " ".join(f"{int(x):08x}" for x in out) == want
+
+
+def test_normals_and_uniforms_moments():
+    z = rng.normals3(np.arange(200_000), step=7, tag=rng.TAG_SGLD, seed=1234)
+    assert abs(z.mean()) < 0.01 and abs(z.var() - 1.0) < 0.01
+    assert abs(np.corrcoef(z[:, 0], z[:, 1])[0, 1]) < 0.01
+    u = rng.uniform1(np.arange(200_000), step=3, tag=rng.TAG_RELOC_PICK, seed=99)
+    assert 0.0 < u.min() and u.max() < 1.0
+    assert abs(u.mean() - 0.5) < 0.005
+    # different steps and tags give different streams
+    a = rng.uniform1(np.arange(10), 1, 2, 5)
+    b = rng.uniform1(np.arange(10), 2, 2, 5)
+    c = rng.uniform1(np.arange(10), 1, 3, 5)
+    assert not np.allclose(a, b) and not np.allclose(a, c)
+
+
+def _logit(p):
+    return math.log(p / (1.0 - p))
+
+
+def _scene(G, seed):
+    g = torch.Generator().manual_seed(seed)
+    P = torch.zeros(G, 14, dtype=D)
+    P[:, 0:3] = (torch.rand(G, 3, generator=g, dtype=D) * 2 - 1) * 0.6
+    q = torch.zeros(G, 4, dtype=D)
+    q[:, 0] = 1.0
+    P[:, 3:7] = q + 0.1 * torch.randn(G, 4, generator=g, dtype=D)
+    P[:, 7:10] = math.log(0.08) + 0.1 * torch.randn(G, 3, generator=g, dtype=D)
+    P[:, 10:13] = torch.randn(G, 3, generator=g, dtype=D) * 1.5
+    P[:, 13] = _logit(0.7)
+    return P
+
+
+def _cam(res=24):
+    return geometry.make_camera(res, res, (0.0, 0.0, 3.0))
+
+
+def test_split_preserves_render_exactly():
+    cam = _cam()
+    o0, n = 0.6, 4
+    base = _scene(1, 3)
+    multi = base.repeat(n, 1)
+    multi[:, 13] = _logit(o0 / n)
+    single = base.clone()
+    single[:, 13] = _logit(o0)
+    a = splat.render_dense(single, cam)
+    b = splat.render_dense(multi, cam)
+    assert torch.allclose(a, b, atol=1e-10)
+    multi[:, 13] = _logit(o0)                             # negative control: no split
+    assert (splat.render_dense(multi, cam) - a).abs().max() > 1e-3
+
+
+def test_relocate_with_zero_offset_keeps_render():
+    cam = _cam()
+    P = _scene(40, 5)
+    P[:12, 13] = _logit(1e-4)                             # 12 dead gaussians
+    before = splat.render_dense(P, cam)
+    o, dead, alive = mcmc.classify(P, 0.005)
+    assert dead.numel() == 12
+    u = torch.tensor(rng.uniform1(np.arange(12), 1, rng.TAG_RELOC_PICK, 7))
+    targets = mcmc.pick_targets(o, alive, u)
+    m, v = torch.ones_like(P), torch.ones_like(P)
+    touched = mcmc.relocate(P, m, v, dead, targets, torch.zeros(12, 3, dtype=D))
+    after = splat.render_dense(P, cam)
+    assert (before - after).abs().max() < 2e-2
+    assert torch.equal(torch.sort(touched).values, torch.unique(torch.cat([dead, targets])))
+    assert float(m[touched].abs().max()) == 0.0 and float(v[touched].abs().max()) == 0.0
+    untouched = torch.ones(40, dtype=torch.bool)
+    untouched[touched] = False
+    assert float(m[untouched].min()) == 1.0
+    # every opacity sum over a target and its copies is the target's old opacity
+    o_new = torch.sigmoid(P[:, 13])
+    for t in torch.unique(targets):
+        grp = torch.cat([t[None], dead[targets == t]])
+        assert abs(float(o_new[grp].sum() - o[t])) < 1e-9
+
+
+def test_sgld_noise_is_opacity_gated():
+    P = _scene(2, 1)
+    P[0, 13] = _logit(0.99)
+    P[1, 13] = _logit(1e-3)
+    eps = torch.tensor(rng.normals3(np.arange(2), 1, rng.TAG_SGLD, 3), dtype=D)
+    d = mcmc.sgld_noise(P, 5e-3, 100.0, eps).norm(dim=1)
+    assert float(d[0]) < 1e-6
+    assert float(d[1]) > float(d[0])
+
+
+def test_reg_grad_closed_form():
+    P = _scene(30, 2)
+    lo, ls = 0.01, 0.02
+    g = mcmc.reg_grad(P, lo, ls)
+    o = torch.sigmoid(P[:, 13])
+    assert torch.allclose(g[:, 13], lo / 30 * o * (1 - o))
+    assert torch.allclose(g[:, 7:10], ls / 90 * torch.exp(P[:, 7:10]))
+    assert float(g[:, :7].abs().max()) == 0.0 and float(g[:, 10:13].abs().max()) == 0.0
+
+
+def test_pick_targets_frequencies_follow_opacity():
+    o = torch.tensor([0.001, 0.5, 0.2, 0.0, 0.3, 0.9, 0.004], dtype=D)
+    alive = torch.tensor([1, 2, 4, 5])
+    u = torch.tensor(rng.uniform1(np.arange(200_000), 1, rng.TAG_RELOC_PICK, 11))
+    t = mcmc.pick_targets(o, alive, u)
+    freq = torch.bincount(t, minlength=7).double() / len(u)
+    want = torch.zeros(7, dtype=D)
+    want[alive] = o[alive] / o[alive].sum()
+    assert torch.allclose(freq, want, atol=0.005)

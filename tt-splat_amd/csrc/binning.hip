@@ -965,7 +965,6 @@ inline int far_border_cells(int G, int ntx, int nty) {
   return (NB <= kMaxBorder && nblk * NB <= (1ll << 26)) ? NB : 0;
 }
 
-inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 inline size_t bin_ws_layout(int G, int ntx, int nty, char* base, BinWorkspace* ws) {
   const int T = ntx * nty;

@@ -160,6 +160,43 @@ __device__ __forceinline__ void sh_apply(const float* __restrict__ p, const floa
 
 // Chain rule of geo_forward.  gin = (ga, gb, gc, gmux, gmuy, gcol_o r,g,b, go_col);
 // gout = the 14 parameter gradients in [G,14] column order.
+// ---- MCMC pieces (spike/mcmc.py) -----------------------------------------------------------
+// Rotation of the normalised quaternion (w, x, y, z) (spike/geometry.py:10-19).
+__device__ __forceinline__ void quat_rot(const float* q, float R[3][3]) {
+  const float n = fmaxf(sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]), 1e-12f);
+  const float w = q[0] / n, x = q[1] / n, y = q[2] / n, z = q[3] / n;
+  R[0][0] = 1.f - 2.f * (y * y + z * z); R[0][1] = 2.f * (x * y - w * z); R[0][2] = 2.f * (x * z + w * y);
+  R[1][0] = 2.f * (x * y + w * z); R[1][1] = 1.f - 2.f * (x * x + z * z); R[1][2] = 2.f * (y * z - w * x);
+  R[2][0] = 2.f * (x * z - w * y); R[2][1] = 2.f * (y * z + w * x); R[2][2] = 1.f - 2.f * (x * x + y * y);
+}
+
+// SGLD step on the means (spike/mcmc.py:25-34): p[0..3) += (R(q) diag(exp(ls)) eps) * w,
+// w = sigmoid(100 ((1 - o) - 0.995)) * noise_scale (noise_scale = noise_lr * means lr),
+// eps the gaussian's three Philox normals for (g, step).
+__device__ __forceinline__ void sgld_apply(float* p, int g, uint32_t step, uint32_t seed,
+                                           float noise_scale) {
+  float R[3][3], z[3];
+  quat_rot(p + 3, R);
+  normals3(philox4x32_10((uint32_t)g, step, kTagSgld, 0u, seed, 0u), z);
+  const float o = sigmoidf_(p[13]);
+  const float w = sigmoidf_(100.0f * ((1.0f - o) - 0.995f)) * noise_scale;
+  float se[3];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) se[j] = expf(p[7 + j]) * z[j];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) p[i] += (R[i][0] * se[0] + R[i][1] * se[1] + R[i][2] * se[2]) * w;
+}
+
+// Gradient of reg_loss = lambda_o mean(sigmoid(op)) + lambda_s mean(exp(log_scales))
+// (spike/mcmc.py:18-22) added to a [14] gradient row; reg_o = lambda_o / G,
+// reg_s = lambda_s / (3 G) (tools/resident_traced.py:732-738).
+__device__ __forceinline__ void reg_add(const float* p, float reg_o, float reg_s, float* gout) {
+  const float o = sigmoidf_(p[13]);
+  gout[13] += reg_o * (o * (1.0f - o));
+#pragma unroll
+  for (int j = 0; j < 3; ++j) gout[7 + j] += reg_s * expf(p[7 + j]);
+}
+
 // gcolor (optional): dL/dcolour through the clamp gate, the factor of every colour coefficient's
 // gradient (the DC one is gcolor * C0, the SH rest ones gcolor * b_l).
 __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const Camera& cam,
@@ -420,14 +457,20 @@ __global__ __launch_bounds__(256) void k_slot_scatter(const float* __restrict__ 
 
 // SH: the rest coefficients (and their moments sh_m, sh_v, same layout) take the same Adam step
 // with the scalar learning rate lr_sh[0]; rows l >= n_rest are not touched.
-template <bool SH>
+// MC: the MCMC regulariser gradient is added before Adam (reg_o, reg_s) and, when
+// noise_lr > 0, the SGLD step is applied to the updated means (noise scale noise_lr * lr[0]).
+struct McmcArgs {
+  float reg_o, reg_s, noise_lr;
+  uint32_t seed;
+};
+template <bool SH, bool MC>
 __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     float* __restrict__ params, int G, float* __restrict__ rest, float* __restrict__ sh_m,
     float* __restrict__ sh_v, int n_rest, const float* __restrict__ camera, float near_z,
     float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv,
     float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
     const float* __restrict__ lr, const float* __restrict__ lr_sh,
-    const int32_t* __restrict__ step, float b1, float b2, float eps) {
+    const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   float* p = params + (int64_t)g * 14;
@@ -454,13 +497,20 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     sh_apply(pl, b, rv, n_rest, s);
   }
   geo_backward(pl, cam, s, gin, gout, gcol);
+  if (MC) reg_add(pl, mc.reg_o, mc.reg_s, gout);
   const float* f = reinterpret_cast<const float*>(step);
   const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
+  float pn[14];
 #pragma unroll
   for (int i = 0; i < 14; ++i) {
-    float pi = pl[i];
-    adam_update(pi, mm[i], vv[i], gout[i], lr[i], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
-    p[i] = pi;
+    pn[i] = pl[i];
+    adam_update(pn[i], mm[i], vv[i], gout[i], lr[i], inv_bc1, inv_sqrt_bc2, b1, b2, eps);
+  }
+  if (MC && mc.noise_lr > 0.0f)
+    sgld_apply(pn, g, (uint32_t)step[0], mc.seed, mc.noise_lr * lr[0]);
+#pragma unroll
+  for (int i = 0; i < 14; ++i) {
+    p[i] = pn[i];
     mg[i] = mm[i];
     vg[i] = vv[i];
     if (gparams) gparams[(int64_t)g * 14 + i] = gout[i];
@@ -541,6 +591,38 @@ __global__ __launch_bounds__(256) void k_adam_flat(float* __restrict__ params,
   params[i] = pp;
   m[i] = mm;
   v[i] = vv;
+}
+
+// Batch-mode MCMC pieces: the regulariser gradient into a [G,14] gradient block, and the SGLD
+// step on the means after the Adam update.
+__global__ __launch_bounds__(256) void k_mcmc_reg_grad(const float* __restrict__ params, int G,
+                                                       float reg_o, float reg_s,
+                                                       float* __restrict__ grad) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  float p[14], gr[14];
+#pragma unroll
+  for (int i = 0; i < 14; ++i) {
+    p[i] = params[(int64_t)g * 14 + i];
+    gr[i] = 0.0f;
+  }
+  reg_add(p, reg_o, reg_s, gr);
+  grad[(int64_t)g * 14 + 13] += gr[13];
+#pragma unroll
+  for (int j = 0; j < 3; ++j) grad[(int64_t)g * 14 + 7 + j] += gr[7 + j];
+}
+
+__global__ __launch_bounds__(256) void k_sgld(float* __restrict__ params, int G,
+                                              const float* __restrict__ lr, float noise_lr,
+                                              uint32_t seed, const int32_t* __restrict__ step) {
+  const int g = blockIdx.x * blockDim.x + threadIdx.x;
+  if (g >= G) return;
+  float p[14];
+#pragma unroll
+  for (int i = 0; i < 14; ++i) p[i] = params[(int64_t)g * 14 + i];
+  sgld_apply(p, g, (uint32_t)step[0], seed, noise_lr * lr[0]);
+#pragma unroll
+  for (int i = 0; i < 3; ++i) params[(int64_t)g * 14 + i] = p[i];
 }
 
 __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
@@ -686,26 +768,62 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
     return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_adam<false><<<grid1d(G, 256), 256, 0, stream>>>(
+  k_geom_bwd_adam<false, false><<<grid1d(G, 256), 256, 0, stream>>>(
       params, G, nullptr, nullptr, nullptr, 0, camera, near_z, blur, gslot, inv, gparams, m, v,
-      lr, nullptr, step, beta1, beta2, eps);
+      lr, nullptr, step, beta1, beta2, eps, McmcArgs{0.0f, 0.0f, 0.0f, 0u});
   return launch_status();
 }
 
-int tts_geom_bwd_adam_sh(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
+int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
                          int G, const float* camera, float near_z, float blur, const float* gslot,
                          const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
                          const float* lr_sh, const int32_t* step, float beta1, float beta2,
-                         float eps, hipStream_t stream) {
+                         float eps, float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
+                         hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !m || !v || !lr || !step)))
     return TTS_EINVAL;
   if (const int e = sh_args(sh_degree, sh_rest)) return e;
   if (sh_degree > 0 && (!sh_m || !sh_v || !lr_sh)) return TTS_EINVAL;
+  if (lambda_o < 0.0f || lambda_s < 0.0f || noise_lr < 0.0f) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_adam<true><<<grid1d(G, 256), 256, 0, stream>>>(
-      params, G, sh_rest, sh_m, sh_v, sh_rest_count(sh_degree), camera, near_z, blur, gslot, inv,
-      gparams, m, v, lr, lr_sh, step, beta1, beta2, eps);
+  const McmcArgs mc{lambda_o / (float)G, lambda_s / (3.0f * (float)G), noise_lr, seed};
+  const bool use_mc = lambda_o > 0.0f || lambda_s > 0.0f || noise_lr > 0.0f;
+  const int n_rest = sh_rest_count(sh_degree);
+  const dim3 grid = grid1d(G, 256);
+#define TTS_LAUNCH_BWD_ADAM(SH, MC)                                                          \
+  k_geom_bwd_adam<SH, MC><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_m, sh_v, n_rest,   \
+                                                    camera, near_z, blur, gslot, inv, gparams, \
+                                                    m, v, lr, lr_sh, step, beta1, beta2, eps, mc)
+  if (sh_degree > 0) {
+    if (use_mc) TTS_LAUNCH_BWD_ADAM(true, true);
+    else TTS_LAUNCH_BWD_ADAM(true, false);
+  } else {
+    if (use_mc) TTS_LAUNCH_BWD_ADAM(false, true);
+    else TTS_LAUNCH_BWD_ADAM(false, false);
+  }
+#undef TTS_LAUNCH_BWD_ADAM
+  return launch_status();
+}
+
+int tts_mcmc_reg_grad(const float* params, int G, float lambda_o, float lambda_s, float* grad,
+                      hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !grad))) return TTS_EINVAL;
+  if (lambda_o < 0.0f || lambda_s < 0.0f) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0) return TTS_OK;
+  k_mcmc_reg_grad<<<grid1d(G, 256), 256, 0, stream>>>(params, G, lambda_o / (float)G,
+                                                      lambda_s / (3.0f * (float)G), grad);
+  return launch_status();
+}
+
+int tts_sgld_noise(float* params, int G, const float* lr, float noise_lr, uint32_t seed,
+                   const int32_t* step, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !lr || !step))) return TTS_EINVAL;
+  if (noise_lr < 0.0f) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (G == 0 || noise_lr == 0.0f) return TTS_OK;
+  k_sgld<<<grid1d(G, 256), 256, 0, stream>>>(params, G, lr, noise_lr, seed, step);
   return launch_status();
 }
 

@@ -19,6 +19,9 @@ inline int launch_status() {
 
 inline int grid1d(int64_t n, int block) { return static_cast<int>((n + block - 1) / block); }
 
+// Workspace sub-buffers start on 256-byte boundaries.
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
 // float -> int64 with x86 cvttss2si semantics: NaN and |f| >= 2^63 give INT64_MIN.
 // (PyTorch-CPU's Tensor.long() behaves so; the binning keys depend on it for saturated and
 // non-finite distances.)
@@ -77,6 +80,51 @@ __device__ __forceinline__ int xcd_item(int p, int n) {
   const int per = n / kNumXcd, extra = n % kNumXcd;
   const int x = p % kNumXcd, k = p / kNumXcd;
   return x * per + min(x, extra) + k;
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, SC'11): a counter-based generator, four 32-bit
+// words per (counter, key), no state to carry between calls or graph replays.
+struct Philox4 {
+  uint32_t w[4];
+};
+__device__ __forceinline__ Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint32_t c2,
+                                                 uint32_t c3, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += 0x9E3779B9u;
+      k1 += 0xBB67AE85u;
+    }
+    const uint32_t lo0 = 0xD2511F53u * c0, hi0 = __umulhi(0xD2511F53u, c0);
+    const uint32_t lo1 = 0xCD9E8D57u * c2, hi1 = __umulhi(0xCD9E8D57u, c2);
+    const uint32_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    c0 = n0;
+    c1 = lo1;
+    c2 = n2;
+    c3 = lo0;
+  }
+  return {{c0, c1, c2, c3}};
+}
+
+// Stream tags (counter word 2) of the MCMC draws; counter = (index, step, tag, 0), key = (seed, 0).
+constexpr uint32_t kTagSgld = 1, kTagRelocPick = 2, kTagRelocOffset = 3;
+
+// Uniform in (0, 1) from the top 24 bits: ((x >> 8) + 0.5) * 2^-24 (exact in double).
+__device__ __forceinline__ double u01d(uint32_t x) {
+  return ((double)(x >> 8) + 0.5) * 5.9604644775390625e-08;
+}
+
+// Three standard normals (Box-Muller on words 0,1 and 2,3; the fourth value is unused).
+__device__ __forceinline__ void normals3(const Philox4& p, float* z) {
+  const float u0 = (float)u01d(p.w[0]), u1 = (float)u01d(p.w[1]);
+  const float u2 = (float)u01d(p.w[2]), u3 = (float)u01d(p.w[3]);
+  const float r0 = sqrtf(-2.0f * logf(u0)), r1 = sqrtf(-2.0f * logf(u2));
+  float s0, c0, s1, c1;
+  sincosf(6.283185307179586f * u1, &s0, &c0);
+  sincosf(6.283185307179586f * u3, &s1, &c1);
+  z[0] = r0 * c0;
+  z[1] = r0 * s0;
+  z[2] = r1 * c1;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {

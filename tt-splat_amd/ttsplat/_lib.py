@@ -12,7 +12,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libttsplat.so")
 
 _c_int, _c_float, _vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
-_c_size, _c_i64 = ctypes.c_size_t, ctypes.c_int64
+_c_size, _c_i64, _c_u32 = ctypes.c_size_t, ctypes.c_int64, ctypes.c_uint32
 
 # name -> (restype, argtypes); must match include/ttsplat.h
 SIGNATURES = {
@@ -55,9 +55,14 @@ SIGNATURES = {
     "tts_geom_fwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp]),
     "tts_geom_bwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp,
                                  _vp]),
-    "tts_geom_bwd_adam_sh": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
+    "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_float, _c_float,
-                                      _c_float, _vp]),
+                                      _c_float, _c_float, _c_float, _c_float, _c_u32, _vp]),
+    "tts_mcmc_reg_grad": (_c_int, [_vp, _c_int, _c_float, _c_float, _vp, _vp]),
+    "tts_sgld_noise": (_c_int, [_vp, _c_int, _vp, _c_float, _c_u32, _vp, _vp]),
+    "tts_relocate_workspace_bytes": (_c_size, [_c_int]),
+    "tts_relocate": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_float, _c_float, _c_u32,
+                              _vp, _vp, _vp, _c_size, _vp]),
     "tts_geom_bwd_accum_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp,
                                        _c_float, _vp, _vp, _vp]),
     "tts_adam_flat": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_float, _c_float, _c_float,

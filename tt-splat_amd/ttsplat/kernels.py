@@ -424,10 +424,12 @@ def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=
 
 def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
                   b1=BETA1, b2=BETA2, eps=EPS, sh_rest=None, sh_m=None, sh_v=None, lr_sh=None,
-                  sh_degree=0):
+                  sh_degree=0, lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, seed=0):
     """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel.
     With sh_degree > 0 the rest coefficients sh_rest (moments sh_m, sh_v, all [15,3,G]) take
-    the same Adam step at learning rate lr_sh[1] (device scalar)."""
+    the same Adam step at learning rate lr_sh[1] (device scalar).  lambda_o / lambda_s add the
+    MCMC regulariser's gradient; noise_lr > 0 applies the SGLD step to the updated means
+    (Philox draws keyed by seed and the device step number)."""
     G = params.shape[0]
     dev = params.device
     for t, n in ((params, "params"), (m, "m"), (v, "v")):
@@ -442,16 +444,69 @@ def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BL
     if gparams is not None:
         require(gparams, "gparams", F32, (G, 14), dev)
     _sh_check(sh_rest, sh_degree, G, dev)
+    if min(lambda_o, lambda_s, noise_lr) < 0:
+        raise ValueError("lambda_o, lambda_s and noise_lr must be >= 0")
     if sh_degree > 0:
         require(sh_m, "sh_m", F32, (SH_REST, 3, G), dev)
         require(sh_v, "sh_v", F32, (SH_REST, 3, G), dev)
         require(lr_sh, "lr_sh", F32, (1,), dev)
-        call("tts_geom_bwd_adam_sh", ptr(params), ptr(sh_rest), ptr(sh_m), ptr(sh_v),
+    if sh_degree > 0 or lambda_o or lambda_s or noise_lr:
+        call("tts_geom_bwd_adam_ex", ptr(params), ptr(sh_rest), ptr(sh_m), ptr(sh_v),
              int(sh_degree), G, ptr(camera), near, blur, ptr(gslot), ptr(inv), ptr(gparams),
-             ptr(m), ptr(v), ptr(lr), ptr(lr_sh), ptr(step), b1, b2, eps, stream())
+             ptr(m), ptr(v), ptr(lr), ptr(lr_sh), ptr(step), b1, b2, eps, float(lambda_o),
+             float(lambda_s), float(noise_lr), int(seed) & 0xFFFFFFFF, stream())
         return
     call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
          ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
+
+
+# ----------------------------------------------------------------------------- MCMC --
+def mcmc_reg_grad(params, grad, lambda_o, lambda_s):
+    """grad[G,14] += gradient of the MCMC regulariser (spike/mcmc.py:18-22)."""
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(grad, "grad", F32, (G, 14), dev)
+    call("tts_mcmc_reg_grad", ptr(params), G, float(lambda_o), float(lambda_s), ptr(grad),
+         stream())
+
+
+def sgld_noise(params, lr, noise_lr, step, seed=0):
+    """SGLD step on the means (spike/mcmc.py:25-34), noise scale noise_lr * lr[0]."""
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(lr, "lr", F32, (14,), dev)
+    require(step, "step", I32, (4,), dev)
+    call("tts_sgld_noise", ptr(params), G, ptr(lr), float(noise_lr), int(seed) & 0xFFFFFFFF,
+         ptr(step), stream())
+
+
+def relocate_workspace(G, device):
+    n = _lib.load().tts_relocate_workspace_bytes(G)
+    return torch.empty(max(n, 1), device=device, dtype=U8)
+
+
+def relocate(params, m, v, step, dead_thr=0.005, offset=0.005, seed=0, workspace=None,
+             moved=None, sh_rest=None, sh_m=None, sh_v=None):
+    """MCMC relocation of dead slots onto live gaussians (spike/mcmc.py:41-93), on the device.
+    Returns the device int32 [1] holding the number of relocated slots."""
+    G = params.shape[0]
+    dev = params.device
+    for t, n in ((params, "params"), (m, "m"), (v, "v")):
+        require(t, n, F32, (G, 14), dev)
+    require(step, "step", I32, (4,), dev)
+    if sh_rest is not None:
+        for t, n in ((sh_rest, "sh_rest"), (sh_m, "sh_m"), (sh_v, "sh_v")):
+            require(t, n, F32, (SH_REST, 3, G), dev)
+    ws = relocate_workspace(G, dev) if workspace is None else workspace
+    require(ws, "workspace", U8, None, dev)
+    moved = torch.zeros(1, device=dev, dtype=I32) if moved is None else moved
+    require(moved, "moved", I32, (1,), dev)
+    call("tts_relocate", ptr(params), ptr(m), ptr(v), ptr(sh_rest), ptr(sh_m), ptr(sh_v), G,
+         float(dead_thr), float(offset), int(seed) & 0xFFFFFFFF, ptr(step), ptr(moved), ptr(ws),
+         ws.numel(), stream())
+    return moved
 
 
 def zero_(buf):

@@ -45,11 +45,21 @@ class TrainStep:
     sh_degree = 1..3: view-dependent colour (the SHD > 0 mode of tools/resident_traced.py:237-264):
     sh_rest is spike's color_rest [G,15,3] (zeros if omitted), trained with Adam at lr_sh
     (default: the colour learning rate / 20, as the reference); the direction is constant in
-    the backward, as there."""
+    the backward, as there.
+    mcmc = dict(...): fixed-count MCMC density control (spike/mcmc.py; the reference's device
+    step flags --lambda-o, --lambda-s, --noise-lr, --relocate-every, --dead-thr,
+    tools/resident_traced.py:124-130): the regulariser gradient and the SGLD step run inside the
+    step's geometry backward + Adam kernel; every `relocate_every` steps (after step i > 0 with
+    i % relocate_every == 0, counted by step()) a captured relocation graph moves dead slots
+    onto live gaussians.  Random draws come from Philox keyed by `seed` and the device step
+    number, so replays are reproducible."""
+
+    MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
+                         dead_thr=0.005, offset=0.005, seed=0)
 
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
-                 dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None):
+                 dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -82,6 +92,16 @@ class TrainStep:
             self.lr_sh = torch.tensor([lrs], dtype=F32, device=dev)
         else:
             self.sh = self.sh_m = self.sh_v = self.lr_sh = None
+        unknown = set(mcmc or {}) - set(self.MCMC_DEFAULTS)
+        if unknown:
+            raise ValueError(f"unknown mcmc options {sorted(unknown)}")
+        self.mc = {**self.MCMC_DEFAULTS, **(mcmc or {})}
+        self._it = 0
+        if self.mc["relocate_every"]:
+            self.reloc_ws = kernels.relocate_workspace(G, dev)
+            self.moved = torch.zeros(1, device=dev, dtype=I32)
+            self.relocations = torch.zeros(1, device=dev, dtype=torch.int64)
+        self.reloc_graph = None
         w_b = torch.nn.functional.softplus(torch.tensor(float(w_b_raw)))
         self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
         # per-view inputs
@@ -154,12 +174,15 @@ class TrainStep:
     def enqueue(self, i=0):
         """Enqueue training step i (camera i, or batch i) on the current stream."""
         sh = dict(sh_rest=self.sh, sh_degree=self.sh_degree)
+        mc = self.mc
         if self.batch == 1:
             self._view_backward(i)
             kernels.adam_advance(self.step_block)
             kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
                                   self.lr, self.step_block, sh_m=self.sh_m, sh_v=self.sh_v,
-                                  lr_sh=self.lr_sh, **sh)
+                                  lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
+                                  lambda_s=mc["lambda_s"], noise_lr=mc["noise_lr"],
+                                  seed=mc["seed"], **sh)
             return
         scale = 1.0 / self.batch
         for ci in range(i * self.batch, (i + 1) * self.batch):
@@ -167,12 +190,23 @@ class TrainStep:
             kernels.geom_bwd_accum(self.P, self.cams[ci], self.gslot, self.inv, self.gacc, scale,
                                    gacc_sh=self.gacc_sh, **sh)
         kernels.adam_advance(self.step_block)
+        if mc["lambda_o"] or mc["lambda_s"]:
+            kernels.mcmc_reg_grad(self.P, self.gacc, mc["lambda_o"], mc["lambda_s"])
         kernels.adam(self.P, self.m, self.v, self.gacc, self.lr, self.step_block)
+        if mc["noise_lr"]:
+            kernels.sgld_noise(self.P, self.lr, mc["noise_lr"], self.step_block, mc["seed"])
         kernels.zero_(self.gacc)
         if self.sh_degree > 0:
             kernels.adam_flat(self.sh, self.sh_m, self.sh_v, self.gacc_sh, self.lr_sh,
                               self.step_block)
             kernels.zero_(self.gacc_sh)
+
+    def enqueue_relocate(self):
+        """Enqueue one MCMC relocation (dead slots onto live gaussians, moments reset)."""
+        mc = self.mc
+        kernels.relocate(self.P, self.m, self.v, self.step_block, mc["dead_thr"], mc["offset"],
+                         mc["seed"], self.reloc_ws, self.moved, self.sh, self.sh_m, self.sh_v)
+        self.relocations += self.moved
 
     def capture(self, cams=None):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
@@ -187,15 +221,24 @@ class TrainStep:
         with torch.cuda.stream(side):
             for ci in cams:
                 self.enqueue(ci)
+            if self.mc["relocate_every"]:
+                self.enqueue_relocate()
         torch.cuda.current_stream(self.dev).wait_stream(side)
         for dst, src in zip(live, state):
             dst.copy_(src)
+        if self.mc["relocate_every"]:
+            self.relocations.zero_()
         torch.cuda.synchronize(self.dev)
         for ci in cams:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 self.enqueue(ci)
             self.graphs[ci] = g
+        if self.mc["relocate_every"]:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.enqueue_relocate()
+            self.reloc_graph = g
         torch.cuda.synchronize(self.dev)
 
     def step(self, ci=0):
@@ -205,6 +248,13 @@ class TrainStep:
             g.replay()
         else:
             self.enqueue(ci)
+        every = self.mc["relocate_every"]
+        if every and self._it > 0 and self._it % every == 0:
+            if self.reloc_graph is not None:
+                self.reloc_graph.replay()
+            else:
+                self.enqueue_relocate()
+        self._it += 1
 
     def loss(self):
         """Loss of the last step (a device scalar; reading it synchronises)."""
