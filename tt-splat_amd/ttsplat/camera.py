@@ -1,4 +1,4 @@
-"""Pinhole cameras in the OpenCV convention (spike/camera.py:36-70).
+"""Pinhole cameras in the OpenCV convention (spike/camera.py:14-70).
 
 `Camera` keeps the reference's fields (R_v, t_v, fx, fy, cx, cy, H, W).  `device_block()`
 packs them into the 16-float camera block the HIP kernels read
@@ -39,6 +39,24 @@ class Camera:
     def as_dict(self):
         return dict(R_v=self.R_v, t_v=self.t_v, fx=self.fx, fy=self.fy, cx=self.cx, cy=self.cy,
                     H=self.H, W=self.W)
+
+
+def opengl_c2w_to_opencv_w2c(c2w):
+    """OpenGL camera-to-world [4,4] (camera looks down -z, +y up; NeRF-synthetic's
+    transform_matrix) -> OpenCV world-to-camera (R_v[3,3], t_v[3]) (spike/camera.py:16-24):
+    R_v = (R_c diag(1,-1,-1))^T, t_v = -R_v cam_pos.  Computed in the input's dtype."""
+    c2w = torch.as_tensor(c2w)
+    R_c, cam_pos = c2w[:3, :3], c2w[:3, 3]
+    flip = torch.diag(torch.tensor([1.0, -1.0, -1.0], dtype=c2w.dtype))
+    R_v = (R_c @ flip).transpose(-1, -2)
+    return R_v, -R_v @ cam_pos
+
+
+def project_point(p_world, R_v, t_v, fx, fy, cx, cy):
+    """Pixel and depth of one world point (spike/camera.py:27-33); z > 0 is in front."""
+    p_cam = R_v @ p_world + t_v
+    z = p_cam[2]
+    return torch.stack([fx * p_cam[0] / z + cx, fy * p_cam[1] / z + cy]), z
 
 
 def look_at_opencv(eye, target=(0.0, 0.0, 0.0), up=(0.0, 1.0, 0.0)):

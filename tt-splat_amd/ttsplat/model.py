@@ -5,7 +5,11 @@ The reference model (spike/model.py:16-95) keeps separate tensors; the device tr
 (tools/resident_traced.py:91, :233-235).  `GaussianModel` holds that block and exposes the
 reference attribute names as views, so code written against spike.model reads it unchanged.
 """
+import math
+
 import torch
+
+C0 = 0.28209479177387814   # SH degree-0 constant (spike/sh.py:9)
 
 PN = ("mx", "my", "mz", "qw", "qx", "qy", "qz", "lx", "ly", "lz", "cr", "cg", "cb", "op")
 
@@ -49,3 +53,37 @@ class GaussianModel:
     @property
     def opacity_raw(self):
         return self.params[:, 13]
+
+
+@torch.no_grad()
+def init_from_points(xyz, rgb, G, seed=0, base=None):
+    """[G,14] parameters initialised from a sparse point cloud (spike/model.py:53-80): G points
+    drawn without replacement (or all points plus jittered copies when there are fewer), a
+    common log-scale from the median nearest-neighbour distance over up to 4000 of them, and
+    colour_dc the inverse DC SH of the point colours.  Quaternions and opacity come from
+    `base` [G,14] when given, else the identity rotation and opacity 0.1."""
+    xyz = torch.as_tensor(xyz, dtype=torch.float32)
+    rgb = torch.as_tensor(rgb, dtype=torch.float32)
+    g = torch.Generator().manual_seed(seed)
+    n = xyz.shape[0]
+    if n >= G:
+        sel = torch.randperm(n, generator=g)[:G]
+        pts, cols = xyz[sel], rgb[sel]
+    else:
+        extra = G - n
+        j = torch.randint(0, n, (extra,), generator=g)
+        span = (xyz.max(0).values - xyz.min(0).values).norm() * 0.01
+        pts = torch.cat([xyz, xyz[j] + torch.randn(extra, 3, generator=g) * span], 0)
+        cols = torch.cat([rgb, rgb[j]], 0)
+    sub = pts[torch.randperm(G, generator=g)[:min(G, 4000)]]
+    d = torch.cdist(sub, sub)
+    d.fill_diagonal_(float("inf"))
+    nn = d.min(1).values.median().clamp(min=1e-4)
+    P = torch.zeros(G, 14) if base is None else torch.as_tensor(base, dtype=torch.float32).clone()
+    if base is None:
+        P[:, 3] = 1.0
+        P[:, 13] = math.log(0.1 / 0.9)
+    P[:, 0:3] = pts
+    P[:, 7:10] = float(torch.log(nn))
+    P[:, 10:13] = (cols - 0.5) / C0
+    return P
