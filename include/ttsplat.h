@@ -228,32 +228,44 @@ int tts_geom_bwd_accum(const float* params, int G, const float* camera, float ne
                        float blur, const float* gslot, const int32_t* inv, float scale,
                        float* gacc, hipStream_t stream);
 
-/* ---- view-dependent colour: real spherical harmonics, degree sh_degree in [0, 3] ----
+/* ---- extended geometry: view-dependent SH colour and the depth weight ----
  *
- * sh_rest holds the rest coefficients (SH indices 1..15) coefficient-major:
+ * SH colour, degree sh_degree in [0, 3].  sh_rest holds the rest coefficients (SH indices
+ * 1..15) coefficient-major:
  *   sh_rest[(l * 3 + c) * G + g], l = 0..14, channel c   (spike's color_rest[G,15,3] permuted)
  * Only the first (sh_degree+1)^2 - 1 rows are read.  colour = max(0.5 + C0*dc + sum_l b_l(dir)
  * rest_l, 0) with dir = means3d - camera centre (spike/sh.py:54-72 as used by the device step,
  * tools/resident_traced.py:246-264,339-341).  In the backward the direction is a constant
- * (tools/resident_traced.py:405-410): dL/drest_l = b_l(dir) * dL/dcolour through the clamp gate. */
+ * (tools/resident_traced.py:405-410): dL/drest_l = b_l(dir) * dL/dcolour through the clamp gate.
+ *
+ * Depth weight (arm B's occlusion lever, spike/arms.py:34-37; device step
+ * tools/resident_traced.py:333-337,418-426): depth_bt = device (beta, tau) or NULL;
+ * keo = keep * sigmoid(op) * sigmoid(beta (tau - z_cam)).  gdepth [G,2] receives each gaussian's
+ * dL/d(beta, tau); tts_depth_weight_adam reduces it and updates (beta, tau).  As in the device
+ * step no gradient reaches the means through z_cam, unless depth_zgrad (tts_geom_bwd_ex only) asks
+ * for it (the dense arm-B autograd of spike/render.py). */
 
-/* Geometry forward with SH colour.  Replaces the SHD > 0 branch of
- * tools/resident_traced.py:339-341 (sh_color_dev). */
-int tts_geom_fwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                    const float* camera, float near_z, float blur, float* proj, uint8_t* keep,
-                    hipStream_t stream);
+/* Geometry forward with SH colour and/or the depth weight.  Replaces the SHD > 0 and
+ * --depth-weight branches of tools/resident_traced.py:327-346 (geom_fwd). */
+int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
+                    const float* depth_bt, int G, const float* camera, float near_z, float blur,
+                    float* proj, uint8_t* keep, hipStream_t stream);
 
-/* Geometry backward with SH colour: grad9 -> gparams[G,14] and gsh_rest (rest layout; rows
- * beyond the degree written as zero).  Replaces the SHD > 0 branch of
- * tools/resident_traced.py:405-410. */
-int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                    const float* camera, float near_z, float blur, const float* grad9,
-                    float* gparams, float* gsh_rest, hipStream_t stream);
+/* Geometry backward with SH colour and/or the depth weight: grad9 -> gparams[G,14], gsh_rest
+ * (rest layout; rows beyond the degree written as zero; needed when sh_degree > 0), gdepth [G,2]
+ * (optional).  Replaces tools/resident_traced.py:397-427 (geom_bwd) with its SH and depth-weight
+ * branches. */
+int tts_geom_bwd_ex(const float* params, const float* sh_rest, int sh_degree,
+                    const float* depth_bt, int depth_zgrad, int G, const float* camera,
+                    float near_z, float blur, const float* grad9, float* gparams,
+                    float* gsh_rest, float* gdepth, hipStream_t stream);
 
 /* tts_geom_bwd_adam with the optional extensions of the device step, in one kernel:
  *  - SH colour (sh_degree > 0): the rest coefficients and their Adam moments sh_m, sh_v (rest
  *    layout) take the same Adam step with learning rate lr_sh[0] (device scalar; the reference
  *    uses the colour rate / 20).  Replaces adam_crest, tools/resident_traced.py:492-501.
+ *  - depth weight (depth_bt): rho in keo, per-gaussian dL/d(beta, tau) into gdepth [G,2]
+ *    (then tts_depth_weight_adam).
  *  - MCMC regulariser (lambda_o, lambda_s > 0): the gradient of lambda_o mean(sigmoid(op)) +
  *    lambda_s mean(exp(log_scales)) is added before Adam (spike/mcmc.py:18-22; device form
  *    tools/resident_traced.py:732-738).
@@ -261,18 +273,32 @@ int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, in
  *    0.995)) * noise_lr * lr[0] with eps three Philox4x32-10 normals for counter (g, step[0],
  *    1, 0) and key (seed, 0) (spike/mcmc.py:25-34; the reference draws eps on the host,
  *    tools/resident_traced.py:620-629).
- * sh_rest, sh_m, sh_v, lr_sh may be NULL when sh_degree is 0. */
+ * sh_rest, sh_m, sh_v, lr_sh may be NULL when sh_degree is 0; depth_bt and gdepth may be NULL. */
 int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
-                         int G, const float* camera, float near_z, float blur, const float* gslot,
-                         const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
-                         const float* lr_sh, const int32_t* step, float beta1, float beta2,
-                         float eps, float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
+                         const float* depth_bt, float* gdepth, int G, const float* camera,
+                         float near_z, float blur, const float* gslot, const int32_t* inv,
+                         float* gparams, float* m, float* v, const float* lr, const float* lr_sh,
+                         const int32_t* step, float beta1, float beta2, float eps,
+                         float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
                          hipStream_t stream);
 
-/* tts_geom_bwd_accum with SH colour: also gacc_sh += scale * dL/drest (rest layout). */
-int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                          const float* camera, float near_z, float blur, const float* gslot,
-                          const int32_t* inv, float scale, float* gacc, float* gacc_sh,
+/* tts_geom_bwd_accum with the extensions: also gacc_sh += scale * dL/drest (rest layout, when
+ * sh_degree > 0) and gacc_depth[G,2] += scale * dL/d(beta, tau) (when depth_bt). */
+int tts_geom_bwd_accum_ex(const float* params, const float* sh_rest, int sh_degree,
+                          const float* depth_bt, int G, const float* camera, float near_z,
+                          float blur, const float* gslot, const int32_t* inv, float scale,
+                          float* gacc, float* gacc_sh, float* gacc_depth, hipStream_t stream);
+
+/* Workspace of tts_depth_weight_adam for G gaussians. */
+size_t tts_depth_weight_workspace_bytes(int G);
+
+/* Sum of gdepth[G,2] over the gaussians (deterministic, fixed order) and one Adam step on the
+ * device scalars depth_bt = (beta, tau) with bt_state = (m_beta, m_tau, v_beta, v_tau) and
+ * learning rate lr1[0], bias factors from `step`.  Replaces adam_bt,
+ * tools/resident_traced.py:503-512 (host sum + host Adam). */
+int tts_depth_weight_adam(const float* gdepth, int G, float* depth_bt, float* bt_state,
+                          const float* lr1, const int32_t* step, float beta1, float beta2,
+                          float eps, void* workspace, size_t workspace_bytes,
                           hipStream_t stream);
 
 /* Adam over n values with one learning rate lr1[0] (device scalar), bias factors from `step`

@@ -99,13 +99,17 @@ def softplus(x):
     return torch.nn.functional.softplus(torch.as_tensor(x))
 
 
-def project_params(P, cam, blur_eps=0.3, near=0.2, rest=None, sh_degree=0):
+def project_params(P, cam, blur_eps=0.3, near=0.2, rest=None, sh_degree=0, depth_bt=None,
+                   depth_zgrad=False):
     """Geometry + activations of the binned trainer (tools/m4_train_binned.py:194-202).
 
     `cam` is a dict with R_v[3,3], t_v[3], fx, fy, cx, cy.  Returns a dict with
-    mu2d, conic, depth, keep, color_o[G,3], o_col[G] -- differentiable w.r.t. P (and `rest`).
-    With sh_degree > 0 and rest [G,15,3] the colour is the device step's view-dependent SH
-    colour (oracle/sh.py: view_color); otherwise the DC colour."""
+    mu2d, conic, depth, keep, color_o[G,3], o_col[G] -- differentiable w.r.t. P (and `rest`,
+    `depth_bt`).  With sh_degree > 0 and rest [G,15,3] the colour is the device step's
+    view-dependent SH colour (oracle/sh.py: view_color); otherwise the DC colour.
+    depth_bt = (beta, tau): the depth weight rho = sigmoid(beta (tau - depth)) multiplies the
+    opacity (spike/arms.py:34-37; device step tools/resident_traced.py:333-337), with depth a
+    constant of the gradient as in that step unless depth_zgrad (spike's dense autograd)."""
     means, quats, log_scales, color_dc, op = split_params(P)
     R = quat_to_rotmat(quats)
     cov = cov3d(torch.exp(log_scales), R)
@@ -120,6 +124,9 @@ def project_params(P, cam, blur_eps=0.3, near=0.2, rest=None, sh_degree=0):
     else:
         color = color_from_dc(color_dc)
     keo = keep.to(dt) * torch.sigmoid(op)
+    if depth_bt is not None:
+        z = depth if depth_zgrad else depth.detach()
+        keo = keo * torch.sigmoid(depth_bt[0] * (depth_bt[1] - z))
     return dict(mu2d=mu2d, conic=conic, depth=depth, keep=keep,
                 color_o=keo[:, None] * color, o_col=keo)
 

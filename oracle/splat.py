@@ -10,7 +10,7 @@ Restates
   spike/forward.py:61-66    poly_splat_wgeo = max(0, 1-Q/k)^2 (* keep)
   spike/arms.py:22-31       WSR blend, arm A: C = (sum w c + w_b c_b) / (sum w + w_b), w = o*w_geo
   spike/backward.py:11-20   wsr_polysplat_ref
-  spike/render.py:14-49     dense render, arm A, SH degree 0
+  spike/render.py:14-49     dense render, arms A and B (spike/arms.py:34-37), SH degree 0
   tools/m4_train_binned.py:130-143  theta_u_gathered (per-tile origin fold, [T,6,K])
   tools/m4_train_binned.py:189-212  _operands (returns the 5-tuple it is meant to)
   tools/bh_views.py:65-71   binned forward: w = relu(einsum(Phi, theta))^2,
@@ -75,9 +75,10 @@ def wsr_polysplat_ref(theta_u, o, color, w_b, Phi, c_b, keep=None):
     return (w @ color + w_b * c_b[None, :]) / (w.sum(1, keepdim=True) + w_b)
 
 
-def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None):
-    """Dense arm-A render of the [G,14] parameter set (spike/render.py:14-49, SH degree 0).
-    O(H*W*G) memory: small images only."""
+def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None, depth_bt=None):
+    """Dense arm-A render of the [G,14] parameter set (spike/render.py:14-49, SH degree 0);
+    with depth_bt = (depth_beta, depth_tau) arm B (spike/arms.py:34-37), the depth
+    differentiable as in spike's autograd.  O(H*W*G) memory: small images only."""
     pr = geometry.project_params(P, cam, blur_eps, near)
     dt = P.dtype
     px, py = geometry.pixel_grid(cam["H"], cam["W"], dtype=dt)
@@ -85,6 +86,8 @@ def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None):
     w_geo = poly_splat_wgeo(Q, k, pr["keep"])
     color = geometry.color_from_dc(P[:, 10:13])
     o = torch.sigmoid(P[:, 13])
+    if depth_bt is not None:
+        o = o * torch.sigmoid(depth_bt[0] * (depth_bt[1] - pr["depth"]))
     w_b = geometry.softplus(torch.tensor(w_b_raw, dtype=dt))
     c_b = torch.ones(3, dtype=dt) if c_b is None else c_b.to(dt)
     img = wsr(o[None, :] * w_geo, color, w_b, c_b)
@@ -106,12 +109,12 @@ def theta_u_gathered(conic_t, mu_t, origins, k):
 
 
 def operands(P, cam, tmap, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2, bins=None, span=2048,
-             stable=False, rest=None, sh_degree=0):
+             stable=False, rest=None, sh_degree=0, depth_bt=None):
     """Geometry, binning and per-tile gather (tools/m4_train_binned.py:189-212).
 
     Returns (theta_u[T,6,K], color_o_t[T,K,3], o_col_t[T,K,1], proj, (idx, valid));
     differentiable w.r.t. P except through the bin indices."""
-    pr = geometry.project_params(P, cam, blur_eps, near, rest, sh_degree)
+    pr = geometry.project_params(P, cam, blur_eps, near, rest, sh_degree, depth_bt)
     if bins is None:
         bins = binning.assign_bins(pr["mu2d"], pr["keep"], tmap, R, K, span=span, stable=stable)
     idx, valid = bins
@@ -140,12 +143,12 @@ def tiles_to_image(C, tmap):
 
 def render_binned(P, cam, tmap, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0,
                   c_b=None, bins=None, span=2048, stable=False, return_all=False, rest=None,
-                  sh_degree=0):
+                  sh_degree=0, depth_bt=None):
     """Binned arm-A render (tools/bh_views.py:65-71 on _operands).  Differentiable w.r.t. P
     (and the SH rest coefficients `rest` [G,15,3] when sh_degree > 0)."""
     dt = P.dtype
     theta, col, oc, pr, bins = operands(P, cam, tmap, R, K, k, blur_eps, near, bins, span, stable,
-                                        rest, sh_degree)
+                                        rest, sh_degree, depth_bt)
     w_b = geometry.softplus(torch.tensor(w_b_raw, dtype=dt))
     c_b = torch.ones(3, dtype=dt) if c_b is None else c_b.to(dt)
     C, den = splat_tiles(theta, col, oc, tmap.Phi.to(dt), w_b, c_b)

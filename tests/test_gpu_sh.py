@@ -50,8 +50,8 @@ def test_geom_fwd_sh_degree0_and_zero_rest_equal_dc():
     # kernel instances may contract multiply-adds differently)
     p0 = torch.empty_like(base)
     k0 = torch.empty(cfg.G, device="cuda", dtype=torch.uint8)
-    _lib.call("tts_geom_fwd_sh", _lib.ptr(Pc), _lib.ptr(zero), 0, cfg.G, _lib.ptr(camb), 0.2,
-              0.3, _lib.ptr(p0), _lib.ptr(k0), _lib.stream())
+    _lib.call("tts_geom_fwd_ex", _lib.ptr(Pc), _lib.ptr(zero), 0, None, cfg.G, _lib.ptr(camb),
+              0.2, 0.3, _lib.ptr(p0), _lib.ptr(k0), _lib.stream())
     assert torch.equal(k0, _lib_keep(Pc, camb))
     assert float(((p0 - base).abs() / base.abs().clamp(min=1.0)).max()) <= 1e-6
     # zero rest at degree 3: the colour is the DC colour (up to the summation order)
@@ -65,7 +65,7 @@ def test_geom_bwd_sh(deg):
     rest = rest_for(cfg.G)
     g = torch.Generator().manual_seed(11)
     grad9 = torch.randn(cfg.G, 9, generator=g)
-    gP, gsh = kernels.geom_bwd(P.cuda(), cam.device_block("cuda"), grad9.cuda(),
+    gP, gsh, _ = kernels.geom_bwd(P.cuda(), cam.device_block("cuda"), grad9.cuda(),
                                sh_rest=kernels.sh_rest_layout(rest.cuda()), sh_degree=deg)
     Pr = P.double().clone().requires_grad_(True)
     rr = rest.double().clone().requires_grad_(True)
@@ -92,8 +92,8 @@ def test_bad_sh_arguments_raise():
     proj = torch.empty(cfg.G, 12, device="cuda")
     keep = torch.empty(cfg.G, device="cuda", dtype=torch.uint8)
     with pytest.raises(_lib.TTSError, match="SH degree"):   # the C ABI's own check
-        _lib.call("tts_geom_fwd_sh", _lib.ptr(Pc), None, 2, cfg.G, _lib.ptr(camb), 0.2, 0.3,
-                  _lib.ptr(proj), _lib.ptr(keep), _lib.stream())
+        _lib.call("tts_geom_fwd_ex", _lib.ptr(Pc), None, 2, None, cfg.G, _lib.ptr(camb), 0.2,
+                  0.3, _lib.ptr(proj), _lib.ptr(keep), _lib.stream())
 
 
 def target_for(cfg, cam, rest=None, deg=0):

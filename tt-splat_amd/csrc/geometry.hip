@@ -10,6 +10,13 @@
 // every load and store of a wave is coalesced.  Their gradient is b_{l+1}(dir) * dL/dcolour
 // through the clamp gate; the direction is a constant of the backward, as in
 // tools/resident_traced.py:405-410 (no gradient reaches the means through it).
+//
+// Depth weight (the occlusion lever of spike/arms.py:34-37 on the device step,
+// tools/resident_traced.py:333-337,418-426): keo = keep * sigmoid(op) * rho with
+// rho = sigmoid(beta (tau - z_cam)), beta and tau two global device scalars.  The backward gives
+// per-gaussian dL/dbeta = g (tau - z_cam), dL/dtau = g beta with g = dL/dkeo keep o rho (1 - rho);
+// like the reference's device step, no gradient reaches the means through z_cam unless asked
+// (DepthW::zgrad, the dense arm-B autograd of spike/render.py).
 
 #include <math.h>
 
@@ -37,7 +44,30 @@ struct GeoState {
   float craw[3];     // colour before the clamp: 0.5 + C0*dc (+ the SH rest terms)
   float color[3];    // max(craw, 0)
   float o;           // sigmoid(op)
+  float rho;         // depth weight sigmoid(beta (tau - z_cam)), 1 without one
+  float dw_beta, dw_tau;
+  bool dw;
 };
+
+// Depth-weight arguments of the geometry kernels.
+struct DepthW {
+  const float* bt;   // device (beta, tau), or null: no depth weight
+  float* grad;       // [G,2] per-gaussian dL/d(beta, tau), or null
+  float scale;       // grad (+)= scale * value
+  int accumulate;    // 1: grad += ..., 0: grad = ...
+  int zgrad;         // 1: dL/dz_cam through rho reaches the means
+};
+__device__ __forceinline__ void depthw_store(const DepthW& d, int g, const float* v) {
+  if (!d.bt || !d.grad) return;
+  float* o = d.grad + (int64_t)g * 2;
+  if (d.accumulate) {
+    o[0] += d.scale * v[0];
+    o[1] += d.scale * v[1];
+  } else {
+    o[0] = d.scale * v[0];
+    o[1] = d.scale * v[1];
+  }
+}
 
 // SH constants (spike/sh.py:9-19,43-51): normalisation of the real SH basis, inria/gsplat signs.
 constexpr float kSC1 = 0.4886025119029199f;
@@ -50,7 +80,8 @@ constexpr int kShRest = 15;  // rest coefficients per channel at degree 3
 __host__ __device__ __forceinline__ int sh_rest_count(int deg) { return (deg + 1) * (deg + 1) - 1; }
 
 __device__ __forceinline__ void geo_forward(const float* __restrict__ p, const Camera& cam,
-                                            float near_z, float blur, GeoState& s) {
+                                            float near_z, float blur, GeoState& s,
+                                            const float* __restrict__ dw = nullptr) {
   const float qw = p[3], qx = p[4], qy = p[5], qz = p[6];
   s.qnorm = sqrtf(qw * qw + qx * qx + qy * qy + qz * qz);
   s.qdiv = fmaxf(s.qnorm, 1e-12f);
@@ -106,6 +137,15 @@ __device__ __forceinline__ void geo_forward(const float* __restrict__ p, const C
     s.color[i] = fmaxf(s.craw[i], 0.0f);
   }
   s.o = sigmoidf_(p[13]);
+  s.dw = dw != nullptr;
+  if (dw) {
+    s.dw_beta = dw[0];
+    s.dw_tau = dw[1];
+    s.rho = sigmoidf_(s.dw_beta * (s.dw_tau - depth));
+  } else {
+    s.dw_beta = s.dw_tau = 0.0f;
+    s.rho = 1.0f;
+  }
 }
 
 // Basis b[1..15] of the rest coefficients in the direction mean - camera centre
@@ -198,10 +238,22 @@ __device__ __forceinline__ void reg_add(const float* p, float reg_o, float reg_s
 }
 
 // gcolor (optional): dL/dcolour through the clamp gate, the factor of every colour coefficient's
-// gradient (the DC one is gcolor * C0, the SH rest ones gcolor * b_l).
+// gradient (the DC one is gcolor * C0, the SH rest ones gcolor * b_l).  gdw (optional, with a
+// depth weight): this gaussian's dL/d(beta, tau); dw_zgrad adds dL/dz_cam through rho to the
+// mean gradient.
 __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const Camera& cam,
                                              const GeoState& s, const float* gin, float* gout,
-                                             float* gcolor = nullptr) {
+                                             float* gcolor = nullptr, float* gdw = nullptr,
+                                             bool dw_zgrad = false) {
+  // activations: color_o = keo * color, o_col = keo, keo = keep * sigmoid(op) * rho
+  const float keo = s.keep ? s.o * s.rho : 0.0f;
+  const float gkeo = gin[5] * s.color[0] + gin[6] * s.color[1] + gin[7] * s.color[2] + gin[8];
+  // depth weight: g = dL/drho * drho/dpre, pre = beta (tau - z_cam)
+  const float gpre = (s.dw && s.keep) ? gkeo * s.o * s.rho * (1.0f - s.rho) : 0.0f;
+  if (gdw) {
+    gdw[0] = gpre * (s.dw_tau - s.mc[2]);
+    gdw[1] = gpre * s.dw_beta;
+  }
   // conic = (s11, -s01, s00) / det
   const float di = s.det_inv;
   float gs11 = gin[0] * di, gs01 = -gin[1] * di, gs00 = gin[2] * di;
@@ -259,7 +311,7 @@ __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const 
   const float gmcy = gmy2 * fy * zi - gJ12 * fy * zi2;
   float gz = -gJ00 * fx * zi2 - gJ11 * fy * zi2 + 2.f * gJ02 * fx * s.mc[0] * zi3 +
              2.f * gJ12 * fy * s.mc[1] * zi3 - gmx2 * fx * s.mc[0] * zi2 - gmy2 * fy * s.mc[1] * zi2;
-  const float gmcz = s.zmask ? gz : 0.0f;
+  const float gmcz = (s.zmask ? gz : 0.0f) - (dw_zgrad ? gpre * s.dw_beta : 0.0f);
 #pragma unroll
   for (int j = 0; j < 3; ++j) gout[j] = cam.R[0 * 3 + j] * gmcx + cam.R[1 * 3 + j] * gmcy + cam.R[2 * 3 + j] * gmcz;
   // rotation from the normalised quaternion
@@ -281,16 +333,13 @@ __device__ __forceinline__ void geo_backward(const float* __restrict__ p, const 
   // s2 = exp(2 log_scale)
 #pragma unroll
   for (int m = 0; m < 3; ++m) gout[7 + m] = gs2[m] * 2.f * s.s2[m];
-  // activations: color_o = keo * color, o_col = keo, keo = keep * sigmoid(op)
-  const float keo = s.keep ? s.o : 0.0f;
-  const float gkeo = gin[5] * s.color[0] + gin[6] * s.color[1] + gin[7] * s.color[2] + gin[8];
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
     const float gc = s.craw[c] >= 0.0f ? gin[5 + c] * keo : 0.0f;
     gout[10 + c] = gc * kC0;
     if (gcolor) gcolor[c] = gc;
   }
-  gout[13] = s.keep ? gkeo * s.o * (1.0f - s.o) : 0.0f;
+  gout[13] = s.keep ? gkeo * s.o * (1.0f - s.o) * s.rho : 0.0f;
 }
 
 __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
@@ -307,6 +356,7 @@ __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
                                                   const float* __restrict__ rest, int n_rest,
+                                                  const float* __restrict__ dw,
                                                   const float* __restrict__ camera, float near_z,
                                                   float blur, float* __restrict__ proj,
                                                   uint8_t* __restrict__ keep) {
@@ -317,13 +367,13 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
   float rv[SH ? 3 * kShRest : 1];
   if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
-  geo_forward(p, cam, near_z, blur, s);
+  geo_forward(p, cam, near_z, blur, s, dw);
   if (SH) {
     float b[16];
     sh_basis(p, cam, b);
     sh_apply(p, b, rv, n_rest, s);
   }
-  const float keo = s.keep ? s.o : 0.0f;
+  const float keo = s.keep ? s.o * s.rho : 0.0f;
   float4* out = reinterpret_cast<float4*>(proj + (int64_t)g * 12);
   out[0] = make_float4(s.mux, s.muy, s.a, s.b);
   out[1] = make_float4(s.c, s.mc[2], keo * s.color[0], keo * s.color[1]);
@@ -335,8 +385,9 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ params, int G,
                                                   const float* __restrict__ rest, int n_rest,
-                                                  const float* __restrict__ camera, float near_z,
-                                                  float blur, const float* __restrict__ grad9,
+                                                  DepthW dwa, const float* __restrict__ camera,
+                                                  float near_z, float blur,
+                                                  const float* __restrict__ grad9,
                                                   float* __restrict__ gparams,
                                                   float* __restrict__ gsh) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
@@ -346,18 +397,19 @@ __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ para
   float rv[SH ? 3 * kShRest : 1];
   if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
-  geo_forward(p, cam, near_z, blur, s);
+  geo_forward(p, cam, near_z, blur, s, dwa.bt);
   float b[16];
   if (SH) {
     sh_basis(p, cam, b);
     sh_apply(p, b, rv, n_rest, s);
   }
-  float gin[9], gout[14], gcol[3];
+  float gin[9], gout[14], gcol[3], gdw[2];
 #pragma unroll
   for (int i = 0; i < 9; ++i) gin[i] = grad9[(int64_t)g * 9 + i];
-  geo_backward(p, cam, s, gin, gout, gcol);
+  geo_backward(p, cam, s, gin, gout, gcol, gdw, dwa.zgrad != 0);
 #pragma unroll
   for (int i = 0; i < 14; ++i) gparams[(int64_t)g * 14 + i] = gout[i];
+  depthw_store(dwa, g, gdw);
   if (SH) {
 #pragma unroll
     for (int l = 0; l < kShRest; ++l)
@@ -470,7 +522,7 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv,
     float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
     const float* __restrict__ lr, const float* __restrict__ lr_sh,
-    const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc) {
+    const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc, DepthW dwa) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   float* p = params + (int64_t)g * 14;
@@ -490,13 +542,15 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
   gather_slot_grads(gslot, inv, g, gin);
   const Camera cam = load_camera(camera);
   GeoState s;
-  geo_forward(pl, cam, near_z, blur, s);
+  geo_forward(pl, cam, near_z, blur, s, dwa.bt);
   float b[16];
   if (SH) {
     sh_basis(pl, cam, b);
     sh_apply(pl, b, rv, n_rest, s);
   }
-  geo_backward(pl, cam, s, gin, gout, gcol);
+  float gdw[2];
+  geo_backward(pl, cam, s, gin, gout, gcol, gdw, dwa.zgrad != 0);
+  depthw_store(dwa, g, gdw);
   if (MC) reg_add(pl, mc.reg_o, mc.reg_s, gout);
   const float* f = reinterpret_cast<const float*>(step);
   const float inv_bc1 = f[1], inv_sqrt_bc2 = f[2];
@@ -539,9 +593,9 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd_accum(
     const float* __restrict__ params, int G, const float* __restrict__ rest, int n_rest,
-    const float* __restrict__ camera, float near_z, float blur, const float* __restrict__ gslot,
-    const int32_t* __restrict__ inv, float scale, float* __restrict__ gacc,
-    float* __restrict__ gacc_sh) {
+    DepthW dwa, const float* __restrict__ camera, float near_z, float blur,
+    const float* __restrict__ gslot, const int32_t* __restrict__ inv, float scale,
+    float* __restrict__ gacc, float* __restrict__ gacc_sh) {
   const int g = blockIdx.x * blockDim.x + threadIdx.x;
   if (g >= G) return;
   const Camera cam = load_camera(camera);
@@ -552,15 +606,16 @@ __global__ __launch_bounds__(256) void k_geom_bwd_accum(
   float rv[SH ? 3 * kShRest : 1];
   if (SH) sh_load(rest, G, g, n_rest, rv);
   GeoState s;
-  geo_forward(pl, cam, near_z, blur, s);
+  geo_forward(pl, cam, near_z, blur, s, dwa.bt);
   float b[16];
   if (SH) {
     sh_basis(pl, cam, b);
     sh_apply(pl, b, rv, n_rest, s);
   }
-  float gin[9], gout[14], gcol[3];
+  float gin[9], gout[14], gcol[3], gdw[2];
   gather_slot_grads(gslot, inv, g, gin);
-  geo_backward(pl, cam, s, gin, gout, gcol);
+  geo_backward(pl, cam, s, gin, gout, gcol, gdw, dwa.zgrad != 0);
+  depthw_store(dwa, g, gdw);
   float* a = gacc + (int64_t)g * 14;
 #pragma unroll
   for (int i = 0; i < 14; ++i) a[i] += scale * gout[i];
@@ -625,6 +680,59 @@ __global__ __launch_bounds__(256) void k_sgld(float* __restrict__ params, int G,
   for (int i = 0; i < 3; ++i) params[(int64_t)g * 14 + i] = p[i];
 }
 
+// Depth weight: per-gaussian dL/d(beta, tau) [G,2] -> block partial sums (fixed order) -> one
+// block sums the partials and applies Adam to the two device scalars (the reference sums on the
+// host and runs a host Adam, tools/resident_traced.py:503-512).
+constexpr int kDwPer = 8;  // gaussians per thread in the partial pass
+__global__ __launch_bounds__(256) void k_dw_partial(const float* __restrict__ gdw, int G,
+                                                    float* __restrict__ part) {
+  __shared__ float tmp[4];
+  const int64_t base = (int64_t)blockIdx.x * 256 * kDwPer;
+  float sb = 0.0f, st = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kDwPer; ++k) {
+    const int64_t g = base + k * 256 + threadIdx.x;
+    if (g < G) {
+      sb += gdw[g * 2 + 0];
+      st += gdw[g * 2 + 1];
+    }
+  }
+  sb = block_sum256(sb, tmp);
+  st = block_sum256(st, tmp);
+  if (threadIdx.x == 0) {
+    part[blockIdx.x * 2 + 0] = sb;
+    part[blockIdx.x * 2 + 1] = st;
+  }
+}
+
+// bt = (beta, tau); state = (m_beta, m_tau, v_beta, v_tau); lr1[0] the learning rate.
+__global__ __launch_bounds__(256) void k_dw_adam(const float* __restrict__ part, int nb,
+                                                 float* __restrict__ bt, float* __restrict__ state,
+                                                 const float* __restrict__ lr1,
+                                                 const int32_t* __restrict__ step, float b1,
+                                                 float b2, float eps) {
+  __shared__ float tmp[4];
+  float sb = 0.0f, st = 0.0f;
+  for (int i = threadIdx.x; i < nb; i += 256) {
+    sb += part[i * 2 + 0];
+    st += part[i * 2 + 1];
+  }
+  sb = block_sum256(sb, tmp);
+  st = block_sum256(st, tmp);
+  if (threadIdx.x == 0) {
+    const float* f = reinterpret_cast<const float*>(step);
+    const float g[2] = {sb, st};
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float p = bt[k], m = state[k], v = state[2 + k];
+      adam_update(p, m, v, g[k], lr1[0], f[1], f[2], b1, b2, eps);
+      bt[k] = p;
+      state[k] = m;
+      state[2 + k] = v;
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) buf[i] = 0.0f;
@@ -658,28 +766,32 @@ int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, 
   if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_fwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera, near_z,
-                                                        blur, proj, keep);
+  k_geom_fwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, nullptr, camera,
+                                                        near_z, blur, proj, keep);
   return launch_status();
 }
 
-// SH degree check shared by the *_sh entry points: 0 <= deg <= 3, rest present when deg > 0.
+// SH degree check shared by the *_ex entry points: 0 <= deg <= 3, rest present when deg > 0.
 static int sh_args(int deg, const void* rest) {
   if (deg < 0 || deg > 3) return TTS_ESH;
   if (deg > 0 && !rest) return TTS_ESH;
   return TTS_OK;
 }
 
-int tts_geom_fwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                    const float* camera, float near_z, float blur, float* proj, uint8_t* keep,
-                    hipStream_t stream) {
+int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
+                    const float* depth_bt, int G, const float* camera, float near_z, float blur,
+                    float* proj, uint8_t* keep, hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
   if (const int e = sh_args(sh_degree, sh_rest)) return e;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_fwd<true><<<grid1d(G, 256), 256, 0, stream>>>(params, G, sh_rest,
-                                                       sh_rest_count(sh_degree), camera, near_z,
-                                                       blur, proj, keep);
+  const dim3 grid = grid1d(G, 256);
+  if (sh_degree > 0)
+    k_geom_fwd<true><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_rest_count(sh_degree),
+                                               depth_bt, camera, near_z, blur, proj, keep);
+  else
+    k_geom_fwd<false><<<grid, 256, 0, stream>>>(params, G, nullptr, 0, depth_bt, camera, near_z,
+                                                blur, proj, keep);
   return launch_status();
 }
 
@@ -688,22 +800,30 @@ int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, 
   if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera, near_z,
-                                                        blur, grad9, gparams, nullptr);
+  k_geom_bwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0,
+                                                        DepthW{nullptr, nullptr, 1.0f, 0, 0},
+                                                        camera, near_z, blur, grad9, gparams,
+                                                        nullptr);
   return launch_status();
 }
 
-int tts_geom_bwd_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                    const float* camera, float near_z, float blur, const float* grad9,
-                    float* gparams, float* gsh_rest, hipStream_t stream) {
-  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams || !gsh_rest)))
-    return TTS_EINVAL;
+int tts_geom_bwd_ex(const float* params, const float* sh_rest, int sh_degree,
+                    const float* depth_bt, int depth_zgrad, int G, const float* camera,
+                    float near_z, float blur, const float* grad9, float* gparams,
+                    float* gsh_rest, float* gdepth, hipStream_t stream) {
+  if (G < 0 || (G > 0 && (!params || !camera || !grad9 || !gparams))) return TTS_EINVAL;
   if (const int e = sh_args(sh_degree, sh_rest)) return e;
+  if (sh_degree > 0 && !gsh_rest) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd<true><<<grid1d(G, 256), 256, 0, stream>>>(params, G, sh_rest,
-                                                       sh_rest_count(sh_degree), camera, near_z,
-                                                       blur, grad9, gparams, gsh_rest);
+  const DepthW dwa{depth_bt, gdepth, 1.0f, 0, depth_zgrad ? 1 : 0};
+  const dim3 grid = grid1d(G, 256);
+  if (sh_degree > 0)
+    k_geom_bwd<true><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_rest_count(sh_degree), dwa,
+                                               camera, near_z, blur, grad9, gparams, gsh_rest);
+  else
+    k_geom_bwd<false><<<grid, 256, 0, stream>>>(params, G, nullptr, 0, dwa, camera, near_z, blur,
+                                                grad9, gparams, nullptr);
   return launch_status();
 }
 
@@ -739,24 +859,31 @@ int tts_geom_bwd_accum(const float* params, int G, const float* camera, float ne
   if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !gacc))) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_accum<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, camera,
-                                                              near_z, blur, gslot, inv, scale,
-                                                              gacc, nullptr);
+  k_geom_bwd_accum<false><<<grid1d(G, 256), 256, 0, stream>>>(
+      params, G, nullptr, 0, DepthW{nullptr, nullptr, 1.0f, 0, 0}, camera, near_z, blur, gslot,
+      inv, scale, gacc, nullptr);
   return launch_status();
 }
 
-int tts_geom_bwd_accum_sh(const float* params, const float* sh_rest, int sh_degree, int G,
-                          const float* camera, float near_z, float blur, const float* gslot,
-                          const int32_t* inv, float scale, float* gacc, float* gacc_sh,
-                          hipStream_t stream) {
+int tts_geom_bwd_accum_ex(const float* params, const float* sh_rest, int sh_degree,
+                          const float* depth_bt, int G, const float* camera, float near_z,
+                          float blur, const float* gslot, const int32_t* inv, float scale,
+                          float* gacc, float* gacc_sh, float* gacc_depth, hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !gacc))) return TTS_EINVAL;
   if (const int e = sh_args(sh_degree, sh_rest)) return e;
   if (sh_degree > 0 && !gacc_sh) return TTS_EINVAL;
+  if (depth_bt && !gacc_depth) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  k_geom_bwd_accum<true><<<grid1d(G, 256), 256, 0, stream>>>(
-      params, G, sh_rest, sh_rest_count(sh_degree), camera, near_z, blur, gslot, inv, scale, gacc,
-      gacc_sh);
+  const DepthW dwa{depth_bt, gacc_depth, scale, 1, 0};
+  const dim3 grid = grid1d(G, 256);
+  if (sh_degree > 0)
+    k_geom_bwd_accum<true><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_rest_count(sh_degree),
+                                                     dwa, camera, near_z, blur, gslot, inv, scale,
+                                                     gacc, gacc_sh);
+  else
+    k_geom_bwd_accum<false><<<grid, 256, 0, stream>>>(params, G, nullptr, 0, dwa, camera, near_z,
+                                                      blur, gslot, inv, scale, gacc, nullptr);
   return launch_status();
 }
 
@@ -770,15 +897,17 @@ int tts_geom_bwd_adam(float* params, int G, const float* camera, float near_z, f
   if (G == 0) return TTS_OK;
   k_geom_bwd_adam<false, false><<<grid1d(G, 256), 256, 0, stream>>>(
       params, G, nullptr, nullptr, nullptr, 0, camera, near_z, blur, gslot, inv, gparams, m, v,
-      lr, nullptr, step, beta1, beta2, eps, McmcArgs{0.0f, 0.0f, 0.0f, 0u});
+      lr, nullptr, step, beta1, beta2, eps, McmcArgs{0.0f, 0.0f, 0.0f, 0u},
+      DepthW{nullptr, nullptr, 1.0f, 0, 0});
   return launch_status();
 }
 
 int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v, int sh_degree,
-                         int G, const float* camera, float near_z, float blur, const float* gslot,
-                         const int32_t* inv, float* gparams, float* m, float* v, const float* lr,
-                         const float* lr_sh, const int32_t* step, float beta1, float beta2,
-                         float eps, float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
+                         const float* depth_bt, float* gdepth, int G, const float* camera,
+                         float near_z, float blur, const float* gslot, const int32_t* inv,
+                         float* gparams, float* m, float* v, const float* lr, const float* lr_sh,
+                         const int32_t* step, float beta1, float beta2, float eps,
+                         float lambda_o, float lambda_s, float noise_lr, uint32_t seed,
                          hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !gslot || !inv || !m || !v || !lr || !step)))
     return TTS_EINVAL;
@@ -788,13 +917,15 @@ int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
   const McmcArgs mc{lambda_o / (float)G, lambda_s / (3.0f * (float)G), noise_lr, seed};
+  const DepthW dwa{depth_bt, gdepth, 1.0f, 0, 0};
   const bool use_mc = lambda_o > 0.0f || lambda_s > 0.0f || noise_lr > 0.0f;
   const int n_rest = sh_rest_count(sh_degree);
   const dim3 grid = grid1d(G, 256);
 #define TTS_LAUNCH_BWD_ADAM(SH, MC)                                                          \
   k_geom_bwd_adam<SH, MC><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_m, sh_v, n_rest,   \
                                                     camera, near_z, blur, gslot, inv, gparams, \
-                                                    m, v, lr, lr_sh, step, beta1, beta2, eps, mc)
+                                                    m, v, lr, lr_sh, step, beta1, beta2, eps,  \
+                                                    mc, dwa)
   if (sh_degree > 0) {
     if (use_mc) TTS_LAUNCH_BWD_ADAM(true, true);
     else TTS_LAUNCH_BWD_ADAM(true, false);
@@ -803,6 +934,26 @@ int tts_geom_bwd_adam_ex(float* params, float* sh_rest, float* sh_m, float* sh_v
     else TTS_LAUNCH_BWD_ADAM(false, false);
   }
 #undef TTS_LAUNCH_BWD_ADAM
+  return launch_status();
+}
+
+size_t tts_depth_weight_workspace_bytes(int G) {
+  if (G < 0) return 0;
+  const int nb = (G + 256 * kDwPer - 1) / (256 * kDwPer);
+  return sizeof(float) * 2 * (size_t)(nb > 0 ? nb : 1);
+}
+
+int tts_depth_weight_adam(const float* gdepth, int G, float* depth_bt, float* bt_state,
+                          const float* lr1, const int32_t* step, float beta1, float beta2,
+                          float eps, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream) {
+  if (G < 0 || !depth_bt || !bt_state || !lr1 || !step || (G > 0 && !gdepth)) return TTS_EINVAL;
+  if (G >= (1 << 30)) return TTS_EG;
+  if (!workspace || workspace_bytes < tts_depth_weight_workspace_bytes(G)) return TTS_EWORKSPACE;
+  const int nb = (G + 256 * kDwPer - 1) / (256 * kDwPer);
+  float* part = static_cast<float*>(workspace);
+  if (nb > 0) k_dw_partial<<<nb, 256, 0, stream>>>(gdepth, G, part);
+  k_dw_adam<<<1, 256, 0, stream>>>(part, nb, depth_bt, bt_state, lr1, step, beta1, beta2, eps);
   return launch_status();
 }
 

@@ -52,19 +52,24 @@ SIGNATURES = {
     "tts_zero": (_c_int, [_vp, _c_i64, _vp]),
     "tts_geom_bwd_accum": (_c_int, [_vp, _c_int, _vp, _c_float, _c_float, _vp, _vp, _c_float,
                                     _vp, _vp]),
-    "tts_geom_fwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp]),
-    "tts_geom_bwd_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp,
+    "tts_geom_fwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_float, _c_float, _vp, _vp,
                                  _vp]),
-    "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
-                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_float, _c_float,
-                                      _c_float, _c_float, _c_float, _c_float, _c_u32, _vp]),
+    "tts_geom_bwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
+                                 _vp, _vp, _vp, _vp, _vp]),
+    "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_float,
+                                      _c_float, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_float,
+                                      _c_float, _c_float, _c_float, _c_float, _c_float, _c_u32,
+                                      _vp]),
+    "tts_geom_bwd_accum_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_float, _c_float, _vp,
+                                       _vp, _c_float, _vp, _vp, _vp, _vp]),
+    "tts_depth_weight_workspace_bytes": (_c_size, [_c_int]),
+    "tts_depth_weight_adam": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_float, _c_float,
+                                       _c_float, _vp, _c_size, _vp]),
     "tts_mcmc_reg_grad": (_c_int, [_vp, _c_int, _c_float, _c_float, _vp, _vp]),
     "tts_sgld_noise": (_c_int, [_vp, _c_int, _vp, _c_float, _c_u32, _vp, _vp]),
     "tts_relocate_workspace_bytes": (_c_size, [_c_int]),
     "tts_relocate": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_float, _c_float, _c_u32,
                               _vp, _vp, _vp, _c_size, _vp]),
-    "tts_geom_bwd_accum_sh": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _c_float, _c_float, _vp, _vp,
-                                       _c_float, _vp, _vp, _vp]),
     "tts_adam_flat": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_float, _c_float, _c_float,
                                _vp]),
     "tts_dense_workspace_bytes": (_c_size, [_c_int, _c_int]),

@@ -54,22 +54,29 @@ def _sh_check(sh_rest, sh_degree, G, dev):
         require(sh_rest, "sh_rest", F32, (SH_REST, 3, G), dev)
 
 
+def _dw_check(depth_bt, dev):
+    if depth_bt is not None:
+        require(depth_bt, "depth_bt", F32, (2,), dev)
+
+
 def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest=None,
-             sh_degree=0):
+             sh_degree=0, depth_bt=None):
     """Projection + activations -> proj[G,12], keep[G].  sh_degree > 0: view-dependent colour
-    from the rest coefficients sh_rest [15,3,G] (sh_rest_layout of spike's color_rest)."""
+    from the rest coefficients sh_rest [15,3,G] (sh_rest_layout of spike's color_rest).
+    depth_bt (device (beta, tau)): the depth weight sigmoid(beta (tau - z_cam)) on the opacity."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
     require(camera, "camera", F32, (16,), dev)
     _sh_check(sh_rest, sh_degree, G, dev)
+    _dw_check(depth_bt, dev)
     proj = torch.empty(G, 12, device=dev, dtype=F32) if proj is None else proj
     keep = torch.empty(G, device=dev, dtype=U8) if keep is None else keep
     _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
     require(keep, "keep", U8, (G,), dev)
-    if sh_degree > 0:
-        call("tts_geom_fwd_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera), near,
-             blur, ptr(proj), ptr(keep), stream())
+    if sh_degree > 0 or depth_bt is not None:
+        call("tts_geom_fwd_ex", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt), G,
+             ptr(camera), near, blur, ptr(proj), ptr(keep), stream())
     else:
         call("tts_geom_fwd", ptr(params), G, ptr(camera), near, blur, ptr(proj), ptr(keep),
              stream())
@@ -77,22 +84,33 @@ def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest
 
 
 def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None, sh_rest=None, sh_degree=0,
-             gsh_out=None):
-    """grad9[G,9] -> dL/dparams[G,14]; with sh_degree > 0 returns (gparams, dL/dsh_rest)."""
+             gsh_out=None, depth_bt=None, depth_zgrad=False, gdepth=None):
+    """grad9[G,9] -> dL/dparams[G,14].  With sh_degree > 0 also dL/dsh_rest [15,3,G]; with
+    depth_bt also dL/d(beta, tau) per gaussian [G,2] (depth_zgrad: plus the gradient through
+    z_cam into the means).  Returns gparams, or a tuple (gparams, gsh, gdepth) when either
+    extension is on (absent parts None)."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
     require(camera, "camera", F32, (16,), dev)
     require(grad9, "grad9", F32, (G, 9), dev)
     _sh_check(sh_rest, sh_degree, G, dev)
+    _dw_check(depth_bt, dev)
     out = torch.empty(G, 14, device=dev, dtype=F32) if out is None else out
     require(out, "gparams", F32, (G, 14), dev)
-    if sh_degree > 0:
-        gsh = torch.empty(SH_REST, 3, G, device=dev, dtype=F32) if gsh_out is None else gsh_out
-        require(gsh, "gsh_out", F32, (SH_REST, 3, G), dev)
-        call("tts_geom_bwd_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera), near,
-             blur, ptr(grad9), ptr(out), ptr(gsh), stream())
-        return out, gsh
+    if sh_degree > 0 or depth_bt is not None:
+        gsh = None
+        if sh_degree > 0:
+            gsh = torch.empty(SH_REST, 3, G, device=dev, dtype=F32) if gsh_out is None else gsh_out
+            require(gsh, "gsh_out", F32, (SH_REST, 3, G), dev)
+        gdw = None
+        if depth_bt is not None:
+            gdw = torch.empty(G, 2, device=dev, dtype=F32) if gdepth is None else gdepth
+            require(gdw, "gdepth", F32, (G, 2), dev)
+        call("tts_geom_bwd_ex", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt),
+             int(bool(depth_zgrad)), G, ptr(camera), near, blur, ptr(grad9), ptr(out), ptr(gsh),
+             ptr(gdw), stream())
+        return out, gsh, gdw
     call("tts_geom_bwd", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(out), stream())
     return out
 
@@ -401,9 +419,10 @@ def adam_flat(params, m, v, grad, lr1, step, b1=BETA1, b2=BETA2, eps=EPS):
 
 
 def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=BLUR,
-                   sh_rest=None, sh_degree=0, gacc_sh=None):
+                   sh_rest=None, sh_degree=0, gacc_sh=None, depth_bt=None, gacc_depth=None):
     """gacc[G,14] += scale * dL/dparams for one view (slot gradients gathered through inv);
-    with sh_degree > 0 also gacc_sh[15,3,G] += scale * dL/dsh_rest."""
+    with sh_degree > 0 also gacc_sh[15,3,G] += scale * dL/dsh_rest, with depth_bt also
+    gacc_depth[G,2] += scale * dL/d(beta, tau)."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
@@ -412,10 +431,15 @@ def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=
     require(inv, "inv", I32, (G, 9), dev)
     require(gacc, "gacc", F32, (G, 14), dev)
     _sh_check(sh_rest, sh_degree, G, dev)
-    if sh_degree > 0:
-        require(gacc_sh, "gacc_sh", F32, (SH_REST, 3, G), dev)
-        call("tts_geom_bwd_accum_sh", ptr(params), ptr(sh_rest), int(sh_degree), G, ptr(camera),
-             near, blur, ptr(gslot), ptr(inv), float(scale), ptr(gacc), ptr(gacc_sh), stream())
+    _dw_check(depth_bt, dev)
+    if sh_degree > 0 or depth_bt is not None:
+        if sh_degree > 0:
+            require(gacc_sh, "gacc_sh", F32, (SH_REST, 3, G), dev)
+        if depth_bt is not None:
+            require(gacc_depth, "gacc_depth", F32, (G, 2), dev)
+        call("tts_geom_bwd_accum_ex", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt), G,
+             ptr(camera), near, blur, ptr(gslot), ptr(inv), float(scale), ptr(gacc),
+             ptr(gacc_sh), ptr(gacc_depth), stream())
         return gacc
     call("tts_geom_bwd_accum", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
          float(scale), ptr(gacc), stream())
@@ -424,12 +448,14 @@ def geom_bwd_accum(params, camera, gslot, inv, gacc, scale=1.0, near=NEAR, blur=
 
 def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BLUR, gparams=None,
                   b1=BETA1, b2=BETA2, eps=EPS, sh_rest=None, sh_m=None, sh_v=None, lr_sh=None,
-                  sh_degree=0, lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, seed=0):
+                  sh_degree=0, lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, seed=0, depth_bt=None,
+                  gdepth=None):
     """Slot gradients (gathered through inv) -> geometry backward -> Adam, in one kernel.
     With sh_degree > 0 the rest coefficients sh_rest (moments sh_m, sh_v, all [15,3,G]) take
     the same Adam step at learning rate lr_sh[1] (device scalar).  lambda_o / lambda_s add the
     MCMC regulariser's gradient; noise_lr > 0 applies the SGLD step to the updated means
-    (Philox draws keyed by seed and the device step number)."""
+    (Philox draws keyed by seed and the device step number).  depth_bt: the depth weight, each
+    gaussian's dL/d(beta, tau) into gdepth [G,2] (then depth_weight_adam)."""
     G = params.shape[0]
     dev = params.device
     for t, n in ((params, "params"), (m, "m"), (v, "v")):
@@ -450,14 +476,39 @@ def geom_bwd_adam(params, camera, gslot, inv, m, v, lr, step, near=NEAR, blur=BL
         require(sh_m, "sh_m", F32, (SH_REST, 3, G), dev)
         require(sh_v, "sh_v", F32, (SH_REST, 3, G), dev)
         require(lr_sh, "lr_sh", F32, (1,), dev)
-    if sh_degree > 0 or lambda_o or lambda_s or noise_lr:
+    _dw_check(depth_bt, dev)
+    if gdepth is not None:
+        require(gdepth, "gdepth", F32, (G, 2), dev)
+    if sh_degree > 0 or lambda_o or lambda_s or noise_lr or depth_bt is not None:
         call("tts_geom_bwd_adam_ex", ptr(params), ptr(sh_rest), ptr(sh_m), ptr(sh_v),
-             int(sh_degree), G, ptr(camera), near, blur, ptr(gslot), ptr(inv), ptr(gparams),
-             ptr(m), ptr(v), ptr(lr), ptr(lr_sh), ptr(step), b1, b2, eps, float(lambda_o),
-             float(lambda_s), float(noise_lr), int(seed) & 0xFFFFFFFF, stream())
+             int(sh_degree), ptr(depth_bt), ptr(gdepth), G, ptr(camera), near, blur, ptr(gslot),
+             ptr(inv), ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(lr_sh), ptr(step), b1, b2, eps,
+             float(lambda_o), float(lambda_s), float(noise_lr), int(seed) & 0xFFFFFFFF, stream())
         return
     call("tts_geom_bwd_adam", ptr(params), G, ptr(camera), near, blur, ptr(gslot), ptr(inv),
          ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2, eps, stream())
+
+
+def depth_weight_workspace(G, device):
+    n = _lib.load().tts_depth_weight_workspace_bytes(G)
+    return torch.empty(max(n, 1), device=device, dtype=U8)
+
+
+def depth_weight_adam(gdepth, depth_bt, bt_state, lr1, step, workspace=None, b1=BETA1, b2=BETA2,
+                      eps=EPS):
+    """Sum gdepth [G,2] over the gaussians and take one Adam step on depth_bt = (beta, tau)
+    (state (m_beta, m_tau, v_beta, v_tau), learning rate lr1[1])."""
+    G = gdepth.shape[0]
+    dev = gdepth.device
+    require(gdepth, "gdepth", F32, (G, 2))
+    require(depth_bt, "depth_bt", F32, (2,), dev)
+    require(bt_state, "bt_state", F32, (4,), dev)
+    require(lr1, "lr1", F32, (1,), dev)
+    require(step, "step", I32, (4,), dev)
+    ws = depth_weight_workspace(G, dev) if workspace is None else workspace
+    require(ws, "workspace", U8, None, dev)
+    call("tts_depth_weight_adam", ptr(gdepth), G, ptr(depth_bt), ptr(bt_state), ptr(lr1),
+         ptr(step), b1, b2, eps, ptr(ws), ws.numel(), stream())
 
 
 # ----------------------------------------------------------------------------- MCMC --

@@ -5,9 +5,11 @@ whole render is one differentiable op of the [G,14] parameter block (and w_b_raw
 geometry forward (tts_geom_fwd) -> every gaussian against every pixel (tts_render_dense);
 backward: tts_render_dense_bwd -> tts_geom_bwd.  O(H*W*G) work, no O(H*W*G) memory.
 
-Only arm "A" (depth-free WSR, the hot path's blend) and SH degree 0 are provided; the
-reference's other arms (B, C0, C, SZ, RV, D) raise.  c_b is a constant (a registered buffer in
-the reference model, spike/model.py:51), so its gradient is zero.
+Arms "A" (depth-free WSR, the hot path's blend) and "B" (A with the per-gaussian depth weight
+rho = sigmoid(depth_beta (depth_tau - z_cam)) on the opacity, spike/arms.py:34-37; gradients to
+depth_beta, depth_tau and, as spike's autograd gives them, to the means through z_cam) with SH
+degree 0 are provided; the reference's other arms (C0, C, SZ, RV, D) raise.  c_b is a constant
+(a registered buffer in the reference model, spike/model.py:51), so its gradient is zero.
 """
 import torch
 
@@ -15,35 +17,44 @@ from . import kernels
 from .binned import background, params_of
 
 F32 = torch.float32
-ARMS = ("A",)
+ARMS = ("A", "B")
 
 
 def _check_arm(arm, sh_degree=0):
-    if arm != "A":
-        raise NotImplementedError(f"arm {arm!r}: only the WSR arm 'A' is on the HIP path")
+    if arm not in ARMS:
+        raise NotImplementedError(f"arm {arm!r}: only the WSR arms 'A' and 'B' are on the HIP path")
     if sh_degree:
         raise NotImplementedError("view-dependent colour (sh_degree > 0) is not on the HIP path")
 
 
 class DenseRender(torch.autograd.Function):
+    """bt: (depth_beta, depth_tau) [2] for arm B, or None."""
+
     @staticmethod
-    def forward(ctx, P, camera, bg, H, W, k, blur, near):
+    def forward(ctx, P, camera, bg, bt, H, W, k, blur, near):
         Pc = P.detach().contiguous()
-        proj, _ = kernels.geom_fwd(Pc, camera, near=near, blur=blur)
+        btc = None if bt is None else bt.detach().float().contiguous()
+        proj, _ = kernels.geom_fwd(Pc, camera, near=near, blur=blur, depth_bt=btc)
         img, den = kernels.render_dense(proj, H, W, k, bg.detach().contiguous())
-        ctx.save_for_backward(Pc, camera, bg, proj, img, den)
+        ctx.save_for_backward(Pc, camera, bg, proj, img, den, btc)
         ctx.meta = (H, W, k, blur, near)
         return img
 
     @staticmethod
     def backward(ctx, gimg):
-        Pc, camera, bg, proj, img, den = ctx.saved_tensors
+        Pc, camera, bg, proj, img, den, btc = ctx.saved_tensors
         H, W, k, blur, near = ctx.meta
         grad9, gwb = kernels.render_dense_bwd(proj, H, W, k, bg.detach().contiguous(), img, den,
                                               gimg.float().contiguous())
-        gP = kernels.geom_bwd(Pc, camera, grad9, near=near, blur=blur)
+        gbt = None
+        if btc is None:
+            gP = kernels.geom_bwd(Pc, camera, grad9, near=near, blur=blur)
+        else:
+            gP, _, gdw = kernels.geom_bwd(Pc, camera, grad9, near=near, blur=blur, depth_bt=btc,
+                                          depth_zgrad=True)
+            gbt = gdw.sum(0)
         gbg = torch.cat([gwb, torch.zeros(3, device=gwb.device, dtype=F32)])
-        return gP, None, gbg, None, None, None, None, None
+        return gP, None, gbg, gbt, None, None, None, None, None
 
 
 def render(model, cam, arm, k=4.0, blur_eps=0.3, near=0.2, sh_degree=0):
@@ -51,5 +62,9 @@ def render(model, cam, arm, k=4.0, blur_eps=0.3, near=0.2, sh_degree=0):
     _check_arm(arm, sh_degree)
     P = params_of(model)
     dev = P.device
-    return DenseRender.apply(P, cam.device_block(dev), background(model, dev), cam.H, cam.W,
+    bt = None
+    if arm == "B":
+        bt = torch.stack([torch.as_tensor(model.depth_beta, dtype=F32, device=dev).reshape(()),
+                          torch.as_tensor(model.depth_tau, dtype=F32, device=dev).reshape(())])
+    return DenseRender.apply(P, cam.device_block(dev), background(model, dev), bt, cam.H, cam.W,
                              float(k), float(blur_eps), float(near))

@@ -52,14 +52,22 @@ class TrainStep:
     step's geometry backward + Adam kernel; every `relocate_every` steps (after step i > 0 with
     i % relocate_every == 0, counted by step()) a captured relocation graph moves dead slots
     onto live gaussians.  Random draws come from Philox keyed by `seed` and the device step
-    number, so replays are reproducible."""
+    number, so replays are reproducible.
+
+    depth_weight = dict(beta0=1.0, tau0=None, lr_bt=0.02): the depth-weight occlusion lever
+    (tools/resident_traced.py --depth-weight, :138-140,333-337,418-426,503-512): the opacity is
+    multiplied by sigmoid(beta (tau - z_cam)); beta and tau live on the device and take an Adam
+    step (learning rate lr_bt) after every step; tau0 = None uses the median camera depth of
+    the gaussians camera 0 keeps, as the reference refines it at warm-up."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
+    DEPTH_DEFAULTS = dict(beta0=1.0, tau0=None, lr_bt=0.02)
 
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
-                 dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None):
+                 dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None,
+                 depth_weight=None):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -103,6 +111,22 @@ class TrainStep:
             self.relocations = torch.zeros(1, device=dev, dtype=torch.int64)
         self.reloc_graph = None
         w_b = torch.nn.functional.softplus(torch.tensor(float(w_b_raw)))
+        self.dw = self.dw_state = self.lr_bt = self.gdw = None
+        if depth_weight is not None:
+            unknown = set(depth_weight) - set(self.DEPTH_DEFAULTS)
+            if unknown:
+                raise ValueError(f"unknown depth_weight options {sorted(unknown)}")
+            dwo = {**self.DEPTH_DEFAULTS, **depth_weight}
+            tau0 = dwo["tau0"]
+            if tau0 is None:                 # median camera depth of the kept gaussians
+                pr, kp = kernels.geom_fwd(self.P, cameras[0].device_block(dev))
+                z = pr[:, 5][kp.bool()]
+                tau0 = float(z.median()) if z.numel() else float(pr[:, 5].median())
+            self.dw = torch.tensor([float(dwo["beta0"]), tau0], dtype=F32, device=dev)
+            self.dw_state = torch.zeros(4, dtype=F32, device=dev)
+            self.lr_bt = torch.tensor([float(dwo["lr_bt"])], dtype=F32, device=dev)
+            self.gdw = torch.zeros(G, 2, dtype=F32, device=dev)
+            self.dw_ws = kernels.depth_weight_workspace(G, dev)
         self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
         # per-view inputs
         self.cams = [c.device_block(dev) for c in cameras]
@@ -144,7 +168,7 @@ class TrainStep:
     def forward(self, ci=0):
         """Geometry + binning + fused splat for camera ci into self.image (no training)."""
         kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep, sh_rest=self.sh,
-                         sh_degree=self.sh_degree)
+                         sh_degree=self.sh_degree, depth_bt=self.dw)
         kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
                             self.ncand, self.inv)
@@ -182,13 +206,17 @@ class TrainStep:
                                   self.lr, self.step_block, sh_m=self.sh_m, sh_v=self.sh_v,
                                   lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
                                   lambda_s=mc["lambda_s"], noise_lr=mc["noise_lr"],
-                                  seed=mc["seed"], **sh)
+                                  seed=mc["seed"], depth_bt=self.dw, gdepth=self.gdw, **sh)
+            if self.dw is not None:
+                kernels.depth_weight_adam(self.gdw, self.dw, self.dw_state, self.lr_bt,
+                                          self.step_block, self.dw_ws)
             return
         scale = 1.0 / self.batch
         for ci in range(i * self.batch, (i + 1) * self.batch):
             self._view_backward(ci)
             kernels.geom_bwd_accum(self.P, self.cams[ci], self.gslot, self.inv, self.gacc, scale,
-                                   gacc_sh=self.gacc_sh, **sh)
+                                   gacc_sh=self.gacc_sh, depth_bt=self.dw, gacc_depth=self.gdw,
+                                   **sh)
         kernels.adam_advance(self.step_block)
         if mc["lambda_o"] or mc["lambda_s"]:
             kernels.mcmc_reg_grad(self.P, self.gacc, mc["lambda_o"], mc["lambda_s"])
@@ -200,6 +228,10 @@ class TrainStep:
             kernels.adam_flat(self.sh, self.sh_m, self.sh_v, self.gacc_sh, self.lr_sh,
                               self.step_block)
             kernels.zero_(self.gacc_sh)
+        if self.dw is not None:
+            kernels.depth_weight_adam(self.gdw, self.dw, self.dw_state, self.lr_bt,
+                                      self.step_block, self.dw_ws)
+            kernels.zero_(self.gdw)
 
     def enqueue_relocate(self):
         """Enqueue one MCMC relocation (dead slots onto live gaussians, moments reset)."""
@@ -215,6 +247,8 @@ class TrainStep:
         live = [self.P, self.m, self.v, self.step_block]
         if self.sh is not None:
             live += [self.sh, self.sh_m, self.sh_v]
+        if self.dw is not None:
+            live += [self.dw, self.dw_state, self.gdw]
         state = [t.clone() for t in live]
         side = torch.cuda.Stream(device=self.dev)
         side.wait_stream(torch.cuda.current_stream(self.dev))

@@ -36,6 +36,11 @@ class _Fitted:
         self.params = P
         self.w_b_raw = torch.as_tensor(model.w_b_raw, dtype=F32).detach().to(P.device).reshape(())
         self.c_b = torch.as_tensor(model.c_b, dtype=F32).detach().to(P.device)
+        # arm B's global depth-weight scalars (spike/model.py:48-49)
+        self.depth_beta = torch.as_tensor(getattr(model, "depth_beta", 1.0),
+                                          dtype=F32).detach().to(P.device).reshape(())
+        self.depth_tau = torch.as_tensor(getattr(model, "depth_tau", 3.0),
+                                         dtype=F32).detach().to(P.device).reshape(())
 
 
 def _write_back(model, st):
@@ -53,6 +58,10 @@ def _write_back(model, st):
             model.w_b_raw.copy_(st.w_b_raw.reshape(model.w_b_raw.shape))
         else:
             model.w_b_raw = float(st.w_b_raw)
+        for name in ("depth_beta", "depth_tau"):
+            cur = getattr(model, name, None)
+            if torch.is_tensor(cur):
+                cur.copy_(getattr(st, name).reshape(cur.shape))
 
 
 def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4.0, blur_eps=0.3,
@@ -69,8 +78,10 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
     lrv = lrv.to(dev)
     lrw = torch.zeros(14, dtype=F32)
     lrw[0] = float(lr["wb"])
+    lrw[1:3] = float(lr["depth"])
     lrw = lrw.to(dev)
-    # Adam state: [G,14] moments, plus w_b_raw carried as column 0 of a one-row block
+    # Adam state: [G,14] moments, plus w_b_raw (column 0) and, for arm B, depth_beta and
+    # depth_tau (columns 1, 2) carried in a one-row block
     m, v = torch.zeros(G, 14, device=dev, dtype=F32), torch.zeros(G, 14, device=dev, dtype=F32)
     wrow = torch.zeros(1, 14, device=dev, dtype=F32)
     mw, vw = torch.zeros_like(wrow), torch.zeros_like(wrow)
@@ -86,19 +97,29 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
         wl = st.w_b_raw.clone().requires_grad_(True)
         view = _View()
         view.params, view.w_b_raw, view.c_b = Pl, wl, st.c_b
+        leaves = [Pl, wl]
+        if arm == "B":
+            view.depth_beta = st.depth_beta.clone().requires_grad_(True)
+            view.depth_tau = st.depth_tau.clone().requires_grad_(True)
+            leaves += [view.depth_beta, view.depth_tau]
         total = 0.0
         for cam, gt in zip(cameras, gts):
             img = render(view, cam, arm, k=k, blur_eps=blur_eps, near=near)
             total = total + loss_fn(img, gt, lambda_ssim)
         total = total / len(cameras)
-        gP, gw = torch.autograd.grad(total, (Pl, wl))
+        grads = torch.autograd.grad(total, leaves)
         kernels.adam_advance(step)
-        kernels.adam(st.params, m, v, gP.contiguous(), lrv, step)
+        kernels.adam(st.params, m, v, grads[0].contiguous(), lrv, step)
         wrow[0, 0] = st.w_b_raw
         gwrow = torch.zeros_like(wrow)
-        gwrow[0, 0] = gw
+        gwrow[0, 0] = grads[1]
+        if arm == "B":
+            wrow[0, 1], wrow[0, 2] = st.depth_beta, st.depth_tau
+            gwrow[0, 1], gwrow[0, 2] = grads[2], grads[3]
         kernels.adam(wrow, mw, vw, gwrow, lrw, step)
         st.w_b_raw = wrow[0, 0].clone()
+        if arm == "B":
+            st.depth_beta, st.depth_tau = wrow[0, 1].clone(), wrow[0, 2].clone()
         history.append(float(total.detach()))
         if log_every and (it % log_every == 0 or it == iters - 1):
             print(f"    iter {it:4d}  loss {history[-1]:.5f}")
