@@ -341,7 +341,12 @@ int tts_zero(float* buf, int64_t n, hipStream_t stream);
 
 /* ---- dense (unbinned) forms, O(H*W*G): every gaussian against every pixel ---- */
 
-/* Workspace for the two dense backward entry points (G gaussians, P pixels). */
+/* Dense blend arms of tts_render_dense_arm (spike/arms.py). */
+#define TTS_ARM_A 0   /* depth-free WSR (:22-31); arm B = A with the depth weight of tts_geom_fwd_ex */
+#define TTS_ARM_SZ 1  /* soft-Z visibility prepass (:50-68) */
+#define TTS_ARM_RV 2  /* revealage compositing (:71-83) */
+
+/* Workspace for the dense backward entry points (G gaussians, P pixels). */
 size_t tts_dense_workspace_bytes(int G, int P);
 
 /* Dense arm-A render from proj[G,12]: Q = a dx^2 + 2b dx dy + c dy^2 at pixel centres
@@ -357,6 +362,27 @@ int tts_render_dense(const float* proj, int G, int H, int W, float k, const floa
 int tts_render_dense_bwd(const float* proj, int G, int H, int W, float k, const float* bg,
                          const float* image, const float* den, const float* gimage, float* grad9,
                          float* gwb, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Dense render with the per-pixel occlusion arms (arm = TTS_ARM_*): SZ computes the visible
+ * front depth z* = sum W0 z / (sum W0 + 1e-6) per pixel (W0 = o w_geo, z = camera depth proj[5])
+ * and blends W0 sigmoid(-softz_beta (z - z*)) by WSR (spike/arms.py:50-68); RV blends
+ * C_avg (1 - R) + c_b R with revealage R = exp(sum log(1 - min(W0, 1 - 1e-4))) and no w_b
+ * (:71-83).  aux [P,4] receives the per-pixel state the backward needs (SZ: z*, den0; RV: R,
+ * C_avg); softz_beta is a device scalar (SZ only).  den: the WSR denominator (RV: sum W0 + 1e-6).
+ * TTS_ARM_A behaves as tts_render_dense. */
+int tts_render_dense_arm(const float* proj, int G, int H, int W, float k, const float* bg,
+                         int arm, const float* softz_beta, float* image, float* den, float* aux,
+                         hipStream_t stream);
+
+/* Backward of tts_render_dense_arm: grad10 [G,10] = the 9 per-gaussian gradients of
+ * tts_render_dense_bwd, plus (SZ) column 9 = this gaussian's share of dL/dsoftz_beta (sum over
+ * the gaussians for the scalar's gradient; row stride 10 for SZ, 9 otherwise).  z enters as a
+ * constant, z* does not (its gradient is a pixel pre-pass).  gwb = dL/dw_b (0 for RV). */
+int tts_render_dense_arm_bwd(const float* proj, int G, int H, int W, float k, const float* bg,
+                             int arm, const float* softz_beta, const float* image,
+                             const float* den, const float* aux, const float* gimage,
+                             float* grad10, float* gwb, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
 
 /* WSR poly-splat over an explicit basis: u[p,g] = phi[p,:6] . theta[g,:6],
  * w = o[g]*keep[g]*max(u,0)^2, C [P,3] = (w@color + w_b c_b)/(sum w + w_b); den [P] may be NULL;

@@ -10,7 +10,7 @@ Restates
   spike/forward.py:61-66    poly_splat_wgeo = max(0, 1-Q/k)^2 (* keep)
   spike/arms.py:22-31       WSR blend, arm A: C = (sum w c + w_b c_b) / (sum w + w_b), w = o*w_geo
   spike/backward.py:11-20   wsr_polysplat_ref
-  spike/render.py:14-49     dense render, arms A and B (spike/arms.py:34-37), SH degree 0
+  spike/render.py:14-49     dense render, arms A, B, SZ, RV (spike/arms.py:34-83), SH degree 0
   tools/m4_train_binned.py:130-143  theta_u_gathered (per-tile origin fold, [T,6,K])
   tools/m4_train_binned.py:189-212  _operands (returns the 5-tuple it is meant to)
   tools/bh_views.py:65-71   binned forward: w = relu(einsum(Phi, theta))^2,
@@ -75,10 +75,32 @@ def wsr_polysplat_ref(theta_u, o, color, w_b, Phi, c_b, keep=None):
     return (w @ color + w_b * c_b[None, :]) / (w.sum(1, keepdim=True) + w_b)
 
 
-def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None, depth_bt=None):
-    """Dense arm-A render of the [G,14] parameter set (spike/render.py:14-49, SH degree 0);
+def blend_sz(W0, z, softz_beta, color, w_b, c_b, eps=1e-6):
+    """Soft-Z visibility prepass (spike/arms.py:50-68): z* = sum W0 z / (sum W0 + eps) per pixel,
+    h = sigmoid(-beta (z - z*)), WSR of W0 h; z a constant of the gradient."""
+    z = z.detach()
+    den0 = W0.sum(dim=1, keepdim=True) + eps
+    zstar = (W0 @ z[:, None]) / den0
+    h = torch.sigmoid(-softz_beta * (z[None, :] - zstar))
+    return wsr(W0 * h, color, w_b, c_b)
+
+
+def blend_rv(W, color, c_b, eps=1e-6):
+    """Revealage compositing (spike/arms.py:71-83): C_avg (1 - R) + c_b R,
+    R = exp(sum log1p(-clamp(W, 0, 1 - 1e-4)))."""
+    den = W.sum(dim=1, keepdim=True) + eps
+    C_avg = (W @ color) / den
+    a = W.clamp(0.0, 1.0 - 1e-4)
+    R = torch.exp(torch.log1p(-a).sum(dim=1, keepdim=True))
+    return C_avg * (1.0 - R) + c_b[None, :] * R
+
+
+def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None, depth_bt=None,
+                 arm="A", softz_beta=None):
+    """Dense render of the [G,14] parameter set (spike/render.py:14-49, SH degree 0): arm "A";
     with depth_bt = (depth_beta, depth_tau) arm B (spike/arms.py:34-37), the depth
-    differentiable as in spike's autograd.  O(H*W*G) memory: small images only."""
+    differentiable as in spike's autograd; arm "SZ" (softz_beta) and "RV".  O(H*W*G) memory:
+    small images only."""
     pr = geometry.project_params(P, cam, blur_eps, near)
     dt = P.dtype
     px, py = geometry.pixel_grid(cam["H"], cam["W"], dtype=dt)
@@ -88,9 +110,14 @@ def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None, 
     o = torch.sigmoid(P[:, 13])
     if depth_bt is not None:
         o = o * torch.sigmoid(depth_bt[0] * (depth_bt[1] - pr["depth"]))
-    w_b = geometry.softplus(torch.tensor(w_b_raw, dtype=dt))
+    w_b = geometry.softplus(torch.as_tensor(w_b_raw, dtype=dt))
     c_b = torch.ones(3, dtype=dt) if c_b is None else c_b.to(dt)
-    img = wsr(o[None, :] * w_geo, color, w_b, c_b)
+    if arm == "SZ":
+        img = blend_sz(o[None, :] * w_geo, pr["depth"], softz_beta, color, w_b, c_b)
+    elif arm == "RV":
+        img = blend_rv(o[None, :] * w_geo, color, c_b)
+    else:
+        img = wsr(o[None, :] * w_geo, color, w_b, c_b)
     return img.reshape(cam["H"], cam["W"], 3)
 
 
@@ -149,7 +176,7 @@ def render_binned(P, cam, tmap, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2, w_b_r
     dt = P.dtype
     theta, col, oc, pr, bins = operands(P, cam, tmap, R, K, k, blur_eps, near, bins, span, stable,
                                         rest, sh_degree, depth_bt)
-    w_b = geometry.softplus(torch.tensor(w_b_raw, dtype=dt))
+    w_b = geometry.softplus(torch.as_tensor(w_b_raw, dtype=dt))
     c_b = torch.ones(3, dtype=dt) if c_b is None else c_b.to(dt)
     C, den = splat_tiles(theta, col, oc, tmap.Phi.to(dt), w_b, c_b)
     img = tiles_to_image(C, tmap)

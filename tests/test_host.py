@@ -70,10 +70,10 @@ def test_model_views():
 def test_render_rejects_arms_off_the_hip_path():
     import pytest
     from ttsplat import render, train
-    for arm in ("C0", "C", "SZ", "RV", "D"):
+    for arm in ("C0", "C", "D"):
         with pytest.raises(NotImplementedError):
             render.render(None, None, arm)
-    assert render.ARMS == ("A", "B")
+    assert render.ARMS == ("A", "B", "SZ", "RV")
     with pytest.raises(NotImplementedError):
         render.render(None, None, "A", sh_degree=1)
     assert train.DEFAULT_LR["means"] == 5e-3 and train.DEFAULT_LR["wb"] == 1e-2

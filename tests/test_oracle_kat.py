@@ -331,3 +331,28 @@ def test_training_step_reduces_loss():
     lr = torch.full((14,), 1e-2)
     losses = [float(opipe.train_step(P, m, v, t, cam, tmap, tgt, lr, K=128)[1]) for t in range(1, 31)]
     assert losses[-1] < 0.9 * losses[0]
+
+
+def test_soft_z_and_revealage_arms_limits():
+    """spike/arms.py:50-83 restated: soft-Z with beta = 0 halves every weight (h = 1/2), which the
+    WSR ratio ignores except against w_b; a fully transparent set shows c_b through revealage; an
+    opaque front gaussian hides one behind it in SZ for large beta."""
+    from oracle import splat as osp
+    D = torch.float64
+    W0 = torch.rand(5, 4, dtype=D) * 0.5
+    color = torch.rand(4, 3, dtype=D)
+    z = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=D)
+    w_b, c_b = torch.tensor(0.05, dtype=D), torch.ones(3, dtype=D)
+    a = osp.blend_sz(W0, z, torch.tensor(0.0, dtype=D), color, w_b, c_b)
+    assert torch.allclose(a, osp.wsr(0.5 * W0, color, w_b, c_b))
+    assert torch.allclose(osp.blend_rv(torch.zeros(3, 4, dtype=D), color, c_b),
+                          torch.ones(3, 3, dtype=D))
+    W = torch.tensor([[10.0, 10.0]], dtype=D)                # two equal gaussians at z = 1 and 5
+    col = torch.tensor([[1.0, 0.0, 0.0], [0.0, 0.0, 1.0]], dtype=D)
+    out = osp.blend_sz(W, torch.tensor([1.0, 5.0], dtype=D), torch.tensor(50.0, dtype=D), col,
+                       torch.tensor(1e-6, dtype=D), c_b)
+    # z* = 3: the front one passes (h ~ 1), the back one is gated (h ~ 0)
+    assert float(out[0, 0]) > 0.99 and float(out[0, 2]) < 0.01
+    # revealage: an opaque pixel (W >= 1) shows the average colour, no background
+    rv = osp.blend_rv(torch.tensor([[2.0, 0.0]], dtype=D), col, c_b)
+    assert torch.allclose(rv, torch.tensor([[1.0, 0.0, 0.0]], dtype=D), atol=1e-3)

@@ -15,12 +15,22 @@
 // block stages its band's per-pixel WSR gradients (gnum = gC/den, gden = -(gC.C)/den) in LDS and
 // accumulates the gaussian's sums over the band.  Band partials go to a workspace and are summed
 // in band order by a second kernel, so the result is deterministic and there are no atomics.
+//
+// The quad form also renders the two per-pixel occlusion arms of spike/arms.py (ARM template):
+//   SZ (soft-Z, :50-68):  W0 = o w_geo, z* = sum W0 z / (sum W0 + 1e-6) per pixel (pass 1),
+//        h = sigmoid(-beta (z - z*)), C = WSR(W0 h) (pass 2); z is a constant of the gradient,
+//        z* is not: its gradient Z = sum_g dL/dh h (1 - h) beta is a pixel pre-pass of the
+//        backward, and dL/dW0 += Z (z - z*) / den0.  beta (softz_beta) gets a gradient too.
+//   RV (revealage, :71-83): C = C_avg (1 - R) + c_b R, C_avg = sum W color / (sum W + 1e-6),
+//        R = exp(sum log(1 - min(W, 1 - 1e-4))) (no w_b); dL/dW gains -dL/dlogR / (1 - a).
+// aux [P,4] carries the per-pixel forward state to the backward (SZ: z*, den0; RV: R, C_avg).
 
 #include "tts_common.h"
 
 namespace tts {
 
 constexpr int kDenseChunk = 256;
+constexpr int kArmA = 0, kArmSZ = 1, kArmRV = 2;   // TTS_ARM_* values
 constexpr int kQuadComp = 9;    // a, b, c, mu_x, mu_y, col_o r, g, b, o_col
 constexpr int kThetaComp = 10;  // theta 0..5, o, color r, g, b
 constexpr int kDenseTargetBlocks = 2048;
@@ -39,57 +49,91 @@ inline int dense_band_pixels(int G, int P) {
   return pb;
 }
 
-// Workspace layout: [align to 256][gwb partials, nb floats, padded to 256][partials nb*G*ncomp].
+// Workspace layout: [align to 256][gwb partials, nb floats, padded to 256]
+// [per-pixel scratch, P floats, padded to 256][partials nb*G*ncomp].
 inline size_t dense_ws_bytes(int G, int P, int ncomp) {
   if (G <= 0 || P <= 0) return 0;
   const int pb = dense_band_pixels(G, P);
   const size_t nb = (size_t)((P + pb - 1) / pb);
-  return 256 + ((nb * 4 + 255) & ~size_t(255)) + nb * (size_t)G * ncomp * 4;
+  return 256 + ((nb * 4 + 255) & ~size_t(255)) + (((size_t)P * 4 + 255) & ~size_t(255)) +
+         nb * (size_t)G * ncomp * 4;
 }
 
 // ---------------------------------------------------------------- forward
 
+template <int ARM>
 __global__ __launch_bounds__(256) void k_render_dense(const float* __restrict__ proj, int G,
                                                       int W, int P, float inv_k,
                                                       const float* __restrict__ bg,
+                                                      const float* __restrict__ szb,
                                                       float* __restrict__ image,
-                                                      float* __restrict__ den_out) {
+                                                      float* __restrict__ den_out,
+                                                      float4* __restrict__ aux) {
   __shared__ float4 s_a[kDenseChunk];  // mu_x, mu_y, a, 2b
   __shared__ float4 s_b[kDenseChunk];  // c, col_o r, g, b
-  __shared__ float s_o[kDenseChunk];   // o_col
+  __shared__ float2 s_o[kDenseChunk];  // o_col, depth
   const int p = blockIdx.x * 256 + threadIdx.x;
   const float px = (float)(p % W) + 0.5f, py = (float)(p / W) + 0.5f;
-  float nr = 0.f, ng = 0.f, nb = 0.f, nd = 0.f;
-  for (int g0 = 0; g0 < G; g0 += kDenseChunk) {
-    const int n = min(kDenseChunk, G - g0);
-    __syncthreads();
-    if ((int)threadIdx.x < n) {
-      const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)(g0 + threadIdx.x) * 12);
-      const float4 r0 = r[0], r1 = r[1], r2 = r[2];
-      s_a[threadIdx.x] = make_float4(r0.x, r0.y, r0.z, 2.0f * r0.w);
-      s_b[threadIdx.x] = make_float4(r1.x, r1.z, r1.w, r2.x);
-      s_o[threadIdx.x] = r2.y;
+  const float beta = ARM == kArmSZ ? szb[0] : 0.0f;
+  float zstar = 0.0f, den0 = 0.0f;
+  // SZ runs the gaussian loop twice: pass 0 finds z*, pass 1 blends
+  for (int pass = (ARM == kArmSZ ? 0 : 1); pass < 2; ++pass) {
+    float nr = 0.f, ng = 0.f, nb = 0.f, nd = 0.f, lr = 0.f;
+    for (int g0 = 0; g0 < G; g0 += kDenseChunk) {
+      const int n = min(kDenseChunk, G - g0);
+      __syncthreads();
+      if ((int)threadIdx.x < n) {
+        const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)(g0 + threadIdx.x) * 12);
+        const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+        s_a[threadIdx.x] = make_float4(r0.x, r0.y, r0.z, 2.0f * r0.w);
+        s_b[threadIdx.x] = make_float4(r1.x, r1.z, r1.w, r2.x);
+        s_o[threadIdx.x] = make_float2(r2.y, r1.y);
+      }
+      __syncthreads();
+      for (int j = 0; j < n; ++j) {
+        const float4 A = s_a[j], B = s_b[j];
+        const float2 O = s_o[j];
+        const float dx = px - A.x, dy = py - A.y;
+        const float Q = (A.z * dx + A.w * dy) * dx + (B.x * dy) * dy;
+        const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
+        float w = r * r;
+        if (ARM == kArmSZ && pass == 0) {
+          nd += w * O.x;
+          nr += w * O.x * O.y;
+          continue;
+        }
+        if (ARM == kArmSZ) w *= sigmoidf_(-beta * (O.y - zstar));
+        if (ARM == kArmRV) lr += log1pf(-fminf(w * O.x, 1.0f - 1e-4f));
+        nr += w * B.y;
+        ng += w * B.z;
+        nb += w * B.w;
+        nd += w * O.x;
+      }
     }
-    __syncthreads();
-    for (int j = 0; j < n; ++j) {
-      const float4 A = s_a[j], B = s_b[j];
-      const float dx = px - A.x, dy = py - A.y;
-      const float Q = (A.z * dx + A.w * dy) * dx + (B.x * dy) * dy;
-      const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
-      const float w = r * r;
-      nr += w * B.y;
-      ng += w * B.z;
-      nb += w * B.w;
-      nd += w * s_o[j];
+    if (ARM == kArmSZ && pass == 0) {
+      den0 = nd + 1e-6f;
+      zstar = nr / den0;
+      continue;
     }
-  }
-  if (p < P) {
-    const float wb = bg[0];
-    const float d = nd + wb;
-    image[(int64_t)p * 3 + 0] = (nr + wb * bg[1]) / d;
-    image[(int64_t)p * 3 + 1] = (ng + wb * bg[2]) / d;
-    image[(int64_t)p * 3 + 2] = (nb + wb * bg[3]) / d;
-    if (den_out) den_out[p] = d;
+    if (p < P) {
+      if (ARM == kArmRV) {
+        const float d = nd + 1e-6f, R = expf(lr);
+        const float a0 = nr / d, a1 = ng / d, a2 = nb / d;
+        image[(int64_t)p * 3 + 0] = a0 * (1.0f - R) + bg[1] * R;
+        image[(int64_t)p * 3 + 1] = a1 * (1.0f - R) + bg[2] * R;
+        image[(int64_t)p * 3 + 2] = a2 * (1.0f - R) + bg[3] * R;
+        if (den_out) den_out[p] = d;
+        aux[p] = make_float4(R, a0, a1, a2);
+      } else {
+        const float wb = bg[0];
+        const float d = nd + wb;
+        image[(int64_t)p * 3 + 0] = (nr + wb * bg[1]) / d;
+        image[(int64_t)p * 3 + 1] = (ng + wb * bg[2]) / d;
+        image[(int64_t)p * 3 + 2] = (nb + wb * bg[3]) / d;
+        if (den_out) den_out[p] = d;
+        if (ARM == kArmSZ) aux[p] = make_float4(zstar, den0, 0.0f, 0.0f);
+      }
+    }
   }
 }
 
@@ -167,32 +211,126 @@ __device__ __forceinline__ float stage_pixel_grads(const float* __restrict__ ima
   return q.x * bg[1] + q.y * bg[2] + q.z * bg[3] + q.w;
 }
 
+// Per-pixel WSR gradients of the quad form, staged in LDS: (gnum r,g,b, gden) and the arm's
+// pair-independent extras (SZ: z*, Z/den0; RV: dL/dlogR).  Returns this thread's share of
+// dL/dw_b (zero for RV, which has no w_b).
+template <int ARM>
+__device__ __forceinline__ float stage_arm_grads(const float* __restrict__ image,
+                                                 const float* __restrict__ den,
+                                                 const float4* __restrict__ aux,
+                                                 const float* __restrict__ zk,
+                                                 const float* __restrict__ gimage, int p, bool in,
+                                                 const float* __restrict__ bg, float4* s_px,
+                                                 float2* s_ex) {
+  if (ARM != kArmRV) {
+    const float wpart = stage_pixel_grads(image, den, gimage, p, in, bg, s_px);
+    if (ARM == kArmSZ) s_ex[threadIdx.x] = in ? make_float2(aux[p].x, zk[p]) : make_float2(0.f, 0.f);
+    return wpart;
+  }
+  float4 q = make_float4(0.f, 0.f, 0.f, 0.f);
+  float gs = 0.0f;
+  if (in) {
+    const float4 x = aux[p];  // R, C_avg
+    const float R = x.x, inv = 1.0f / den[p];
+    const float g0 = gimage[(int64_t)p * 3 + 0], g1 = gimage[(int64_t)p * 3 + 1],
+                g2 = gimage[(int64_t)p * 3 + 2];
+    const float k = (1.0f - R) * inv;  // dC/dC_avg / den
+    q = make_float4(g0 * k, g1 * k, g2 * k, -(g0 * x.y + g1 * x.z + g2 * x.w) * k);
+    // dL/dR * R = dL/dlogR
+    gs = (g0 * (bg[1] - x.y) + g1 * (bg[2] - x.z) + g2 * (bg[3] - x.w)) * R;
+  }
+  s_px[threadIdx.x] = q;
+  s_ex[threadIdx.x] = make_float2(gs, 0.0f);
+  return 0.0f;
+}
+
+// Soft-Z backward pre-pass, one thread per pixel: Z/den0 with Z = dL/dz* =
+// beta sum_g w_geo (gnum . col_o + gden o_col) h (1 - h).
+__global__ __launch_bounds__(256) void k_softz_pre(const float* __restrict__ proj, int G, int W,
+                                                   int P, float inv_k,
+                                                   const float* __restrict__ szb,
+                                                   const float* __restrict__ image,
+                                                   const float* __restrict__ den,
+                                                   const float4* __restrict__ aux,
+                                                   const float* __restrict__ gimage,
+                                                   float* __restrict__ zk) {
+  __shared__ float4 s_a[kDenseChunk];
+  __shared__ float4 s_b[kDenseChunk];
+  __shared__ float2 s_o[kDenseChunk];
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  const bool in = p < P;
+  const float px = (float)(p % W) + 0.5f, py = (float)(p / W) + 0.5f;
+  const float beta = szb[0];
+  float q0 = 0.f, q1 = 0.f, q2 = 0.f, q3 = 0.f, zs = 0.f, d0 = 1.f;
+  if (in) {
+    const float inv = 1.0f / den[p];
+    const float g0 = gimage[(int64_t)p * 3 + 0], g1 = gimage[(int64_t)p * 3 + 1],
+                g2 = gimage[(int64_t)p * 3 + 2];
+    q0 = g0 * inv; q1 = g1 * inv; q2 = g2 * inv;
+    q3 = -(g0 * image[(int64_t)p * 3 + 0] + g1 * image[(int64_t)p * 3 + 1] +
+           g2 * image[(int64_t)p * 3 + 2]) * inv;
+    zs = aux[p].x;
+    d0 = aux[p].y;
+  }
+  float Z = 0.0f;
+  for (int g0 = 0; g0 < G; g0 += kDenseChunk) {
+    const int n = min(kDenseChunk, G - g0);
+    __syncthreads();
+    if ((int)threadIdx.x < n) {
+      const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)(g0 + threadIdx.x) * 12);
+      const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+      s_a[threadIdx.x] = make_float4(r0.x, r0.y, r0.z, 2.0f * r0.w);
+      s_b[threadIdx.x] = make_float4(r1.x, r1.z, r1.w, r2.x);
+      s_o[threadIdx.x] = make_float2(r2.y, r1.y);
+    }
+    __syncthreads();
+    for (int j = 0; j < n; ++j) {
+      const float4 A = s_a[j], B = s_b[j];
+      const float2 O = s_o[j];
+      const float dx = px - A.x, dy = py - A.y;
+      const float Q = (A.z * dx + A.w * dy) * dx + (B.x * dy) * dy;
+      const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
+      const float h = sigmoidf_(-beta * (O.y - zs));
+      Z += r * r * (q0 * B.y + q1 * B.z + q2 * B.w + q3 * O.x) * h * (1.0f - h);
+    }
+  }
+  if (in) zk[p] = beta * Z / d0;
+}
+
+// ncomp = 9 (a, b, c, mu_x, mu_y, col_o rgb, o_col), 10 for SZ (+ this gaussian's dL/dbeta).
+template <int ARM>
 __global__ __launch_bounds__(256) void k_render_dense_bwd(
     const float* __restrict__ proj, int G, int W, int P, int PB, float inv_k,
-    const float* __restrict__ bg, const float* __restrict__ image, const float* __restrict__ den,
+    const float* __restrict__ bg, const float* __restrict__ szb, const float* __restrict__ image,
+    const float* __restrict__ den, const float4* __restrict__ aux, const float* __restrict__ zk,
     const float* __restrict__ gimage, float* __restrict__ part, float* __restrict__ gwb_part) {
+  constexpr int NC = ARM == kArmSZ ? kQuadComp + 1 : kQuadComp;
   __shared__ float4 s_px[256];
   __shared__ float2 s_xy[256];
+  __shared__ float2 s_ex[256];
   __shared__ float s_ftmp[4];
   const int band = blockIdx.y;
   const int g = blockIdx.x * 256 + threadIdx.x;
   const bool act = g < G;
   float mx = 0.f, my = 0.f, a = 0.f, b = 0.f, c = 0.f, cr = 0.f, cg = 0.f, cb = 0.f, oc = 0.f;
+  float zg = 0.f;
   if (act) {
     const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
     const float4 r0 = r[0], r1 = r[1], r2 = r[2];
     mx = r0.x; my = r0.y; a = r0.z; b = r0.w; c = r1.x;
     cr = r1.z; cg = r1.w; cb = r2.x; oc = r2.y;
+    zg = r1.y;
   }
+  const float beta = ARM == kArmSZ ? szb[0] : 0.0f;
   const float b2 = 2.0f * b;
   float sxx = 0.f, sxy = 0.f, syy = 0.f, sx = 0.f, sy = 0.f;
-  float gr = 0.f, gg = 0.f, gbl = 0.f, go = 0.f;
+  float gr = 0.f, gg = 0.f, gbl = 0.f, go = 0.f, gbeta = 0.f;
   float wpart = 0.f;
   const int pend = min(P, (band + 1) * PB);
   for (int p0 = band * PB; p0 < pend; p0 += 256) {
     __syncthreads();
     const int pp = p0 + threadIdx.x;
-    wpart += stage_pixel_grads(image, den, gimage, pp, pp < pend, bg, s_px);
+    wpart += stage_arm_grads<ARM>(image, den, aux, zk, gimage, pp, pp < pend, bg, s_px, s_ex);
     s_xy[threadIdx.x] = make_float2((float)(pp % W) + 0.5f, (float)(pp / W) + 0.5f);
     __syncthreads();
     const int n = min(256, pend - p0);
@@ -203,11 +341,34 @@ __global__ __launch_bounds__(256) void k_render_dense_bwd(
       const float Q = (a * dx + b2 * dy) * dx + (c * dy) * dy;
       const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
       const float w = r * r;
-      gr += w * q.x;
-      gg += w * q.y;
-      gbl += w * q.z;
-      go += w * q.w;
-      const float gu = r * (q.x * cr + q.y * cg + q.z * cb + q.w * oc);  // half of dL/du
+      const float gw = q.x * cr + q.y * cg + q.z * cb + q.w * oc;  // dL/dw_geo of arm A
+      float dw;                                                   // dL/dw_geo of this arm
+      if (ARM == kArmSZ) {
+        const float2 ex = s_ex[j];  // z*, Z/den0
+        const float h = sigmoidf_(-beta * (zg - ex.x));
+        const float e = ex.y * (zg - ex.x);  // dL/dW0 through z*
+        gr += w * h * q.x;
+        gg += w * h * q.y;
+        gbl += w * h * q.z;
+        go += w * (h * q.w + e);
+        gbeta -= w * gw * h * (1.0f - h) * (zg - ex.x);
+        dw = h * gw + oc * e;
+      } else if (ARM == kArmRV) {
+        const float W0 = w * oc;
+        const float e = W0 <= 1.0f - 1e-4f ? -s_ex[j].x / (1.0f - W0) : 0.0f;  // clamp gate
+        gr += w * q.x;
+        gg += w * q.y;
+        gbl += w * q.z;
+        go += w * (q.w + e);
+        dw = gw + oc * e;
+      } else {
+        gr += w * q.x;
+        gg += w * q.y;
+        gbl += w * q.z;
+        go += w * q.w;
+        dw = gw;
+      }
+      const float gu = r * dw;  // half of dL/du
       const float tx = gu * dx, ty = gu * dy;
       sxx += tx * dx;
       sxy += tx * dy;
@@ -224,7 +385,7 @@ __global__ __launch_bounds__(256) void k_render_dense_bwd(
     // dL/dQ = dL/du * (-1/k) = -2 gu / k
     const float s = -2.0f * inv_k;
     const float mxx = s * sxx, mxy = s * sxy, myy = s * syy, m_x = s * sx, m_y = s * sy;
-    float* dst = part + ((int64_t)band * G + g) * kQuadComp;
+    float* dst = part + ((int64_t)band * G + g) * NC;
     dst[0] = mxx;                          // dQ/da = dx^2
     dst[1] = 2.0f * mxy;                   // dQ/db = 2 dx dy
     dst[2] = myy;                          // dQ/dc = dy^2
@@ -234,6 +395,7 @@ __global__ __launch_bounds__(256) void k_render_dense_bwd(
     dst[6] = gg;
     dst[7] = gbl;
     dst[8] = go;
+    if (ARM == kArmSZ) dst[9] = gbeta;
   }
 }
 
@@ -338,16 +500,20 @@ __global__ __launch_bounds__(256) void k_dense_reduce(const float* __restrict__ 
   }
 }
 
-// Unpacks the workspace into (partials, gwb partials); returns the band count or an error.
+// Unpacks the workspace into (partials, gwb partials, per-pixel scratch); returns the band
+// count or an error.
 inline int dense_ws(void* ws, size_t ws_bytes, int G, int P, int ncomp, float** part,
-                    float** gwbp, int* PB) {
+                    float** gwbp, int* PB, float** pix = nullptr) {
   if (!ws) return TTS_EWORKSPACE;
   if (ws_bytes < dense_ws_bytes(G, P, ncomp)) return TTS_EWORKSPACE;
   *PB = dense_band_pixels(G, P);
   const int nb = (P + *PB - 1) / *PB;
   uintptr_t base = (reinterpret_cast<uintptr_t>(ws) + 255) & ~uintptr_t(255);
   *gwbp = reinterpret_cast<float*>(base);
-  *part = reinterpret_cast<float*>(base + (((size_t)nb * 4 + 255) & ~size_t(255)));
+  base += ((size_t)nb * 4 + 255) & ~size_t(255);
+  if (pix) *pix = reinterpret_cast<float*>(base);
+  base += ((size_t)P * 4 + 255) & ~size_t(255);
+  *part = reinterpret_cast<float*>(base);
   return nb;
 }
 
@@ -369,8 +535,34 @@ int tts_render_dense(const float* proj, int G, int H, int W, float k, const floa
   if (G > (1 << 30)) return TTS_EG;
   if ((int64_t)H * W > (int64_t(1) << 30)) return TTS_EINVAL;
   const int P = H * W;
-  k_render_dense<<<grid1d(P, 256), 256, 0, stream>>>(proj, G, W, P, (float)(1.0 / (double)k), bg,
-                                                     image, den);
+  k_render_dense<kArmA><<<grid1d(P, 256), 256, 0, stream>>>(
+      proj, G, W, P, (float)(1.0 / (double)k), bg, nullptr, image, den, nullptr);
+  return launch_status();
+}
+
+int tts_render_dense_arm(const float* proj, int G, int H, int W, float k, const float* bg,
+                         int arm, const float* softz_beta, float* image, float* den, float* aux,
+                         hipStream_t stream) {
+  if ((G > 0 && !proj) || !bg || !image || H <= 0 || W <= 0 || G < 0 || !(k > 0.0f))
+    return TTS_EINVAL;
+  if (arm != kArmA && arm != kArmSZ && arm != kArmRV) return TTS_EINVAL;
+  if (arm != kArmA && !aux) return TTS_EINVAL;
+  if (arm == kArmSZ && !softz_beta) return TTS_EINVAL;
+  if (G > (1 << 30)) return TTS_EG;
+  if ((int64_t)H * W > (int64_t(1) << 30)) return TTS_EINVAL;
+  const int P = H * W;
+  const float ik = (float)(1.0 / (double)k);
+  float4* ax = reinterpret_cast<float4*>(aux);
+  const dim3 grid = grid1d(P, 256);
+  if (arm == kArmSZ)
+    k_render_dense<kArmSZ><<<grid, 256, 0, stream>>>(proj, G, W, P, ik, bg, softz_beta, image,
+                                                     den, ax);
+  else if (arm == kArmRV)
+    k_render_dense<kArmRV><<<grid, 256, 0, stream>>>(proj, G, W, P, ik, bg, nullptr, image, den,
+                                                     ax);
+  else
+    k_render_dense<kArmA><<<grid, 256, 0, stream>>>(proj, G, W, P, ik, bg, nullptr, image, den,
+                                                    nullptr);
   return launch_status();
 }
 
@@ -389,10 +581,50 @@ int tts_render_dense_bwd(const float* proj, int G, int H, int W, float k, const 
   const int nb = dense_ws(workspace, workspace_bytes, G, P, kQuadComp, &part, &gwbp, &PB);
   if (nb < 0) return nb;
   dim3 grid(grid1d(G, 256), nb);
-  k_render_dense_bwd<<<grid, 256, 0, stream>>>(proj, G, W, P, PB, (float)(1.0 / (double)k), bg,
-                                               image, den, gimage, part, gwbp);
+  k_render_dense_bwd<kArmA><<<grid, 256, 0, stream>>>(proj, G, W, P, PB, (float)(1.0 / (double)k),
+                                                      bg, nullptr, image, den, nullptr, nullptr,
+                                                      gimage, part, gwbp);
   k_dense_reduce<<<grid1d((int64_t)G * kQuadComp, 256), 256, 0, stream>>>(part, nb, G, kQuadComp,
                                                                          gwbp, grad9, gwb);
+  return launch_status();
+}
+
+int tts_render_dense_arm_bwd(const float* proj, int G, int H, int W, float k, const float* bg,
+                             int arm, const float* softz_beta, const float* image,
+                             const float* den, const float* aux, const float* gimage,
+                             float* grad10, float* gwb, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
+  if (!proj || !bg || !image || !den || !gimage || !grad10 || H <= 0 || W <= 0 || G <= 0 ||
+      !(k > 0.0f))
+    return TTS_EINVAL;
+  if (arm != kArmA && arm != kArmSZ && arm != kArmRV) return TTS_EINVAL;
+  if (arm != kArmA && !aux) return TTS_EINVAL;
+  if (arm == kArmSZ && !softz_beta) return TTS_EINVAL;
+  if (G > (1 << 30)) return TTS_EG;
+  if ((int64_t)H * W > (int64_t(1) << 30)) return TTS_EINVAL;
+  const int P = H * W;
+  const int nc = arm == kArmSZ ? kQuadComp + 1 : kQuadComp;
+  float *part, *gwbp, *zk;
+  int PB;
+  const int nb = dense_ws(workspace, workspace_bytes, G, P, nc, &part, &gwbp, &PB, &zk);
+  if (nb < 0) return nb;
+  const float ik = (float)(1.0 / (double)k);
+  const float4* ax = reinterpret_cast<const float4*>(aux);
+  dim3 grid(grid1d(G, 256), nb);
+  if (arm == kArmSZ) {
+    k_softz_pre<<<grid1d(P, 256), 256, 0, stream>>>(proj, G, W, P, ik, softz_beta, image, den,
+                                                    ax, gimage, zk);
+    k_render_dense_bwd<kArmSZ><<<grid, 256, 0, stream>>>(proj, G, W, P, PB, ik, bg, softz_beta,
+                                                         image, den, ax, zk, gimage, part, gwbp);
+  } else if (arm == kArmRV) {
+    k_render_dense_bwd<kArmRV><<<grid, 256, 0, stream>>>(proj, G, W, P, PB, ik, bg, nullptr, image,
+                                                         den, ax, nullptr, gimage, part, gwbp);
+  } else {
+    k_render_dense_bwd<kArmA><<<grid, 256, 0, stream>>>(proj, G, W, P, PB, ik, bg, nullptr, image,
+                                                        den, nullptr, nullptr, gimage, part, gwbp);
+  }
+  k_dense_reduce<<<grid1d((int64_t)G * nc, 256), 256, 0, stream>>>(part, nb, G, nc, gwbp, grad10,
+                                                                  gwb);
   return launch_status();
 }
 

@@ -76,6 +76,10 @@ SIGNATURES = {
     "tts_render_dense": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _vp, _vp, _vp]),
     "tts_render_dense_bwd": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _vp, _vp, _vp,
                                       _vp, _vp, _vp, _c_size, _vp]),
+    "tts_render_dense_arm": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _c_int, _vp, _vp,
+                                      _vp, _vp, _vp]),
+    "tts_render_dense_arm_bwd": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_float, _vp, _c_int, _vp,
+                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "tts_wsr_dense": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp]),
     "tts_wsr_dense_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _vp,
                                    _vp, _vp, _vp, _c_size, _vp]),

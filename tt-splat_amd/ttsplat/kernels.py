@@ -606,6 +606,55 @@ def render_dense_bwd(proj, H, W, k, bg, image, den, gimage, grad9=None, gwb=None
     return grad9, gwb
 
 
+ARM_CODES = {"A": 0, "SZ": 1, "RV": 2}
+
+
+def render_dense_arm(proj, H, W, k, bg, arm, softz_beta=None, image=None, den=None, aux=None):
+    """Dense render with a per-pixel occlusion arm ("A", "SZ" soft-Z, "RV" revealage;
+    spike/arms.py).  Returns image, den, aux [H,W,4] (the per-pixel state the backward reads).
+    softz_beta: device scalar [1] (SZ)."""
+    G = proj.shape[0]
+    dev = proj.device
+    code = ARM_CODES[arm]
+    _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
+    require(bg, "bg", F32, (4,), dev)
+    if arm == "SZ":
+        require(softz_beta, "softz_beta", F32, (1,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    aux = torch.zeros(H, W, 4, device=dev, dtype=F32) if aux is None else aux
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    require(aux, "aux", F32, (H, W, 4), dev)
+    call("tts_render_dense_arm", ptr(proj), G, H, W, float(k), ptr(bg), code, ptr(softz_beta),
+         ptr(image), ptr(den), ptr(aux), stream())
+    return image, den, aux
+
+
+def render_dense_arm_bwd(proj, H, W, k, bg, arm, image, den, aux, gimage, softz_beta=None,
+                         workspace=None):
+    """Backward of render_dense_arm: grad [G,9] (or [G,10] for SZ, column 9 = each gaussian's
+    dL/dsoftz_beta) and gwb [1]."""
+    G = proj.shape[0]
+    dev = proj.device
+    code = ARM_CODES[arm]
+    _aligned16(require(proj, "proj", F32, (G, 12)), "proj")
+    require(bg, "bg", F32, (4,), dev)
+    for t, n, sh in ((image, "image", (H, W, 3)), (den, "den", (H, W)), (aux, "aux", (H, W, 4)),
+                     (gimage, "gimage", (H, W, 3))):
+        require(t, n, F32, sh, dev)
+    if arm == "SZ":
+        require(softz_beta, "softz_beta", F32, (1,), dev)
+    nc = 10 if arm == "SZ" else 9
+    grad = torch.empty(G, nc, device=dev, dtype=F32)
+    gwb = torch.empty(1, device=dev, dtype=F32)
+    workspace = dense_workspace(G, H * W, dev) if workspace is None else workspace
+    call("tts_render_dense_arm_bwd", ptr(proj), G, H, W, float(k), ptr(bg), code,
+         ptr(softz_beta), ptr(image), ptr(den), ptr(aux), ptr(gimage), ptr(grad), ptr(gwb),
+         ptr(workspace), workspace.numel(), stream())
+    return grad, gwb
+
+
 def _wsr_operands(theta, o, color, keep, phi):
     G, P = theta.shape[0], phi.shape[0]
     dev = theta.device

@@ -15,10 +15,11 @@ PN = ("mx", "my", "mz", "qw", "qx", "qy", "qz", "lx", "ly", "lz", "cr", "cg", "c
 
 
 class GaussianModel:
-    """depth_beta, depth_tau: the global depth-weight scalars of arm B (spike/model.py:48-49
-    defaults 1.0 and 3.0)."""
+    """depth_beta, depth_tau: the global depth-weight scalars of arm B; softz_beta: the gate
+    sharpness of arm SZ (spike/model.py:48-50 defaults 1.0, 3.0 and 4.0)."""
 
-    def __init__(self, params, w_b_raw=-3.0, c_b=(1.0, 1.0, 1.0), depth_beta=1.0, depth_tau=3.0):
+    def __init__(self, params, w_b_raw=-3.0, c_b=(1.0, 1.0, 1.0), depth_beta=1.0, depth_tau=3.0,
+                 softz_beta=4.0):
         if params.dim() != 2 or params.shape[1] != 14:
             raise ValueError(f"params must be [G,14], got {tuple(params.shape)}")
         self.params = params.float().contiguous()
@@ -27,6 +28,7 @@ class GaussianModel:
         self.c_b = torch.as_tensor(c_b, dtype=torch.float32, device=dev)
         self.depth_beta = torch.tensor(float(depth_beta), device=dev)
         self.depth_tau = torch.tensor(float(depth_tau), device=dev)
+        self.softz_beta = torch.tensor(float(softz_beta), device=dev)
 
     @classmethod
     def from_reference(cls, model, device="cuda"):

@@ -5,11 +5,16 @@ whole render is one differentiable op of the [G,14] parameter block (and w_b_raw
 geometry forward (tts_geom_fwd) -> every gaussian against every pixel (tts_render_dense);
 backward: tts_render_dense_bwd -> tts_geom_bwd.  O(H*W*G) work, no O(H*W*G) memory.
 
-Arms "A" (depth-free WSR, the hot path's blend) and "B" (A with the per-gaussian depth weight
-rho = sigmoid(depth_beta (depth_tau - z_cam)) on the opacity, spike/arms.py:34-37; gradients to
-depth_beta, depth_tau and, as spike's autograd gives them, to the means through z_cam) with SH
-degree 0 are provided; the reference's other arms (C0, C, SZ, RV, D) raise.  c_b is a constant
-(a registered buffer in the reference model, spike/model.py:51), so its gradient is zero.
+Arms, with SH degree 0:
+  "A"   depth-free WSR, the hot path's blend (spike/arms.py:22-31);
+  "B"   A with the per-gaussian depth weight rho = sigmoid(depth_beta (depth_tau - z_cam)) on the
+        opacity (:34-37); gradients to depth_beta, depth_tau and, as spike's autograd gives them,
+        to the means through z_cam;
+  "SZ"  soft-Z visibility prepass (:50-68), trainable model.softz_beta, z_cam a constant of the
+        gradient as in the reference;
+  "RV"  revealage compositing (:71-83).
+The reference's arms C0, C (view-dependent opacity) and D (sorted alpha) raise.  c_b is a
+constant (a registered buffer in the reference model, spike/model.py:51): its gradient is zero.
 """
 import torch
 
@@ -17,35 +22,51 @@ from . import kernels
 from .binned import background, params_of
 
 F32 = torch.float32
-ARMS = ("A", "B")
+ARMS = ("A", "B", "SZ", "RV")
 
 
 def _check_arm(arm, sh_degree=0):
     if arm not in ARMS:
-        raise NotImplementedError(f"arm {arm!r}: only the WSR arms 'A' and 'B' are on the HIP path")
+        raise NotImplementedError(f"arm {arm!r}: only the arms {ARMS} are on the HIP path")
     if sh_degree:
         raise NotImplementedError("view-dependent colour (sh_degree > 0) is not on the HIP path")
 
 
 class DenseRender(torch.autograd.Function):
-    """bt: (depth_beta, depth_tau) [2] for arm B, or None."""
+    """bt: (depth_beta, depth_tau) [2] for arm B, or None; szb: softz_beta [1] for arm SZ, or
+    None; blend: "A", "SZ" or "RV" (arm B blends as A)."""
 
     @staticmethod
-    def forward(ctx, P, camera, bg, bt, H, W, k, blur, near):
+    def forward(ctx, P, camera, bg, bt, szb, blend, H, W, k, blur, near):
         Pc = P.detach().contiguous()
         btc = None if bt is None else bt.detach().float().contiguous()
+        szc = None if szb is None else szb.detach().float().reshape(1).contiguous()
         proj, _ = kernels.geom_fwd(Pc, camera, near=near, blur=blur, depth_bt=btc)
-        img, den = kernels.render_dense(proj, H, W, k, bg.detach().contiguous())
-        ctx.save_for_backward(Pc, camera, bg, proj, img, den, btc)
-        ctx.meta = (H, W, k, blur, near)
+        bgc = bg.detach().contiguous()
+        if blend == "A":
+            img, den = kernels.render_dense(proj, H, W, k, bgc)
+            aux = None
+        else:
+            img, den, aux = kernels.render_dense_arm(proj, H, W, k, bgc, blend, szc)
+        ctx.save_for_backward(Pc, camera, bg, proj, img, den, btc, szc, aux)
+        ctx.meta = (H, W, k, blur, near, blend)
         return img
 
     @staticmethod
     def backward(ctx, gimg):
-        Pc, camera, bg, proj, img, den, btc = ctx.saved_tensors
-        H, W, k, blur, near = ctx.meta
-        grad9, gwb = kernels.render_dense_bwd(proj, H, W, k, bg.detach().contiguous(), img, den,
-                                              gimg.float().contiguous())
+        Pc, camera, bg, proj, img, den, btc, szc, aux = ctx.saved_tensors
+        H, W, k, blur, near, blend = ctx.meta
+        bgc = bg.detach().contiguous()
+        gi = gimg.float().contiguous()
+        gszb = None
+        if blend == "A":
+            grad9, gwb = kernels.render_dense_bwd(proj, H, W, k, bgc, img, den, gi)
+        else:
+            g, gwb = kernels.render_dense_arm_bwd(proj, H, W, k, bgc, blend, img, den, aux, gi,
+                                                  szc)
+            grad9 = g[:, :9].contiguous()
+            if blend == "SZ":
+                gszb = g[:, 9].sum().reshape(1)
         gbt = None
         if btc is None:
             gP = kernels.geom_bwd(Pc, camera, grad9, near=near, blur=blur)
@@ -54,7 +75,7 @@ class DenseRender(torch.autograd.Function):
                                           depth_zgrad=True)
             gbt = gdw.sum(0)
         gbg = torch.cat([gwb, torch.zeros(3, device=gwb.device, dtype=F32)])
-        return gP, None, gbg, gbt, None, None, None, None, None
+        return gP, None, gbg, gbt, gszb, None, None, None, None, None, None
 
 
 def render(model, cam, arm, k=4.0, blur_eps=0.3, near=0.2, sh_degree=0):
@@ -62,9 +83,12 @@ def render(model, cam, arm, k=4.0, blur_eps=0.3, near=0.2, sh_degree=0):
     _check_arm(arm, sh_degree)
     P = params_of(model)
     dev = P.device
-    bt = None
+    bt = szb = None
     if arm == "B":
         bt = torch.stack([torch.as_tensor(model.depth_beta, dtype=F32, device=dev).reshape(()),
                           torch.as_tensor(model.depth_tau, dtype=F32, device=dev).reshape(())])
-    return DenseRender.apply(P, cam.device_block(dev), background(model, dev), bt, cam.H, cam.W,
-                             float(k), float(blur_eps), float(near))
+    if arm == "SZ":
+        szb = torch.as_tensor(model.softz_beta, dtype=F32, device=dev).reshape(1)
+    blend = "A" if arm == "B" else arm
+    return DenseRender.apply(P, cam.device_block(dev), background(model, dev), bt, szb, blend,
+                             cam.H, cam.W, float(k), float(blur_eps), float(near))

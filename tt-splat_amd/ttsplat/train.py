@@ -41,6 +41,8 @@ class _Fitted:
                                           dtype=F32).detach().to(P.device).reshape(())
         self.depth_tau = torch.as_tensor(getattr(model, "depth_tau", 3.0),
                                          dtype=F32).detach().to(P.device).reshape(())
+        self.softz_beta = torch.as_tensor(getattr(model, "softz_beta", 4.0),
+                                          dtype=F32).detach().to(P.device).reshape(())
 
 
 def _write_back(model, st):
@@ -58,7 +60,7 @@ def _write_back(model, st):
             model.w_b_raw.copy_(st.w_b_raw.reshape(model.w_b_raw.shape))
         else:
             model.w_b_raw = float(st.w_b_raw)
-        for name in ("depth_beta", "depth_tau"):
+        for name in ("depth_beta", "depth_tau", "softz_beta"):
             cur = getattr(model, name, None)
             if torch.is_tensor(cur):
                 cur.copy_(getattr(st, name).reshape(cur.shape))
@@ -78,10 +80,10 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
     lrv = lrv.to(dev)
     lrw = torch.zeros(14, dtype=F32)
     lrw[0] = float(lr["wb"])
-    lrw[1:3] = float(lr["depth"])
+    lrw[1:4] = float(lr["depth"])
     lrw = lrw.to(dev)
     # Adam state: [G,14] moments, plus w_b_raw (column 0) and, for arm B, depth_beta and
-    # depth_tau (columns 1, 2) carried in a one-row block
+    # depth_tau (columns 1, 2), for arm SZ softz_beta (column 3), carried in a one-row block
     m, v = torch.zeros(G, 14, device=dev, dtype=F32), torch.zeros(G, 14, device=dev, dtype=F32)
     wrow = torch.zeros(1, 14, device=dev, dtype=F32)
     mw, vw = torch.zeros_like(wrow), torch.zeros_like(wrow)
@@ -102,6 +104,9 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
             view.depth_beta = st.depth_beta.clone().requires_grad_(True)
             view.depth_tau = st.depth_tau.clone().requires_grad_(True)
             leaves += [view.depth_beta, view.depth_tau]
+        if arm == "SZ":
+            view.softz_beta = st.softz_beta.clone().requires_grad_(True)
+            leaves += [view.softz_beta]
         total = 0.0
         for cam, gt in zip(cameras, gts):
             img = render(view, cam, arm, k=k, blur_eps=blur_eps, near=near)
@@ -116,10 +121,15 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
         if arm == "B":
             wrow[0, 1], wrow[0, 2] = st.depth_beta, st.depth_tau
             gwrow[0, 1], gwrow[0, 2] = grads[2], grads[3]
+        if arm == "SZ":
+            wrow[0, 3] = st.softz_beta
+            gwrow[0, 3] = grads[2]
         kernels.adam(wrow, mw, vw, gwrow, lrw, step)
         st.w_b_raw = wrow[0, 0].clone()
         if arm == "B":
             st.depth_beta, st.depth_tau = wrow[0, 1].clone(), wrow[0, 2].clone()
+        if arm == "SZ":
+            st.softz_beta = wrow[0, 3].clone()
         history.append(float(total.detach()))
         if log_every and (it % log_every == 0 or it == iters - 1):
             print(f"    iter {it:4d}  loss {history[-1]:.5f}")
