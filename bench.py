@@ -137,8 +137,7 @@ def time_kernels(ts, reps, torch, kernels):
         "geom_fwd": lambda: kernels.geom_fwd(ts.P, cam, proj=ts.proj, keep=ts.keep, **sh),
         "binning": lambda: kernels.assign_bins(ts.proj[:, 0:2], ts.keep, ts.H, ts.W, ts.S, ts.K,
                                                ts.span, 1, ts.bin_ws, ts.idx, ts.valid,
-                                               ts.count, ts.ncand, ts.inv),
-        "tile_order": lambda: kernels.tile_order(ts.count, ts.K, ts.order),
+                                               ts.count, ts.ncand, ts.inv, ts.order),
         "splat_fwd": (lambda: kernels.splat_fwd_mx(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
                                                    ts.S, ts.k, ts.image, ts.den, ts.order,
                                                    bf16=True))

@@ -88,11 +88,14 @@ size_t tts_bin_workspace_bytes(int G, int H, int W, int S);
  * keep[g*keep_stride].  Order inside a tile is by (clamp(int64(dist2), 0, span-1), stencil
  * index j, gaussian id), i.e. the reference's sort key with ties in its concatenation order;
  * span = 2048 at S = 16.  Writes idx[T,K], valid[T,K]; count[T] (kept per tile), ncand[T]
- * (candidates per tile) and inv[G,9] are optional (may be NULL). */
+ * (candidates per tile), inv[G,9] and order[T] are optional (may be NULL).  order receives the
+ * tile ids sorted by kept count, heaviest first (what tts_tile_order computes; for grids of up
+ * to 8192 tiles it comes out of the offset scan at no extra pass, beyond that count[T] is
+ * required). */
 int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                     int G, int H, int W, int S, int R, int K, int span,
                     int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
-                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+                    int32_t* order, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Tile ids ordered by kept count, heaviest first (counting sort of count[T], values in [0,K]).
  * Handing it to tts_splat_fwd / tts_splat_bwd makes the expensive tiles start first.  No

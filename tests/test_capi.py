@@ -72,8 +72,8 @@ def test_host_only_entry_points(lib):
 def test_assign_bins_rejects_before_launch(lib, S, H, W, K, span, code):
     buf = ctypes.create_string_buffer(64)
     p = ctypes.cast(buf, ctypes.c_void_p)
-    rc = lib.tts_assign_bins(p, 2, p, 1, 4, H, W, S, 1, K, span, p, p, None, None, None, p,
-                             1 << 20, None)
+    rc = lib.tts_assign_bins(p, 2, p, 1, 4, H, W, S, 1, K, span, p, p, None, None, None, None,
+                             p, 1 << 20, None)
     assert rc == code
 
 

@@ -14,7 +14,8 @@ import torch
 
 from helpers import bins_equal_report, config_inputs
 from oracle import binning as obin
-from ttsplat import kernels
+from ttsplat import kernels, scenes
+from ttsplat.camera import pinhole
 
 pytestmark = pytest.mark.gpu
 
@@ -191,3 +192,36 @@ def test_bins_workspace_reused_across_sizes():
         ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
         assert ndiff == 0, f"G={G}: {ndiff} tiles differ, first {tiles[:8].tolist()}"
         assert torch.equal(ncand.cpu().long(), rncand)
+
+
+def _check_order(order, count):
+    o = order.cpu().long()
+    c = count.cpu().long()
+    assert torch.equal(torch.sort(o).values, torch.arange(c.numel()))   # a permutation
+    co = c[o]
+    assert bool((co[1:] <= co[:-1]).all())                              # heaviest first
+
+
+@pytest.mark.parametrize("H,W,G", [(832, 1264, 100_000), (2064, 1024, 50_000)])
+def test_bins_tile_order_output(H, W, G):
+    """order[T] from assign_bins: a permutation sorted by kept count, heaviest first, produced
+    by the offset scan when the grid has at most 8192 tiles and by the order pass above that
+    (2064 x 1024 = 8256 tiles, which also takes the separate classification path)."""
+    cfg = scenes.CONFIGS["c4"]
+    P = cfg.params(0)[:G] if G <= cfg.G else cfg.params(0)
+    cam = pinhole(H, W, scenes.orbit_eyes(1)[0])
+    proj, keep = kernels.geom_fwd(P.cuda(), cam.device_block("cuda"))
+    T = (H // 16) * (W // 16)
+    order = torch.full((T,), -1, dtype=torch.int32, device="cuda")
+    idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, H, W, 16, 128, 2048,
+                                                   order=order)
+    _check_order(order, count)
+    assert torch.equal(count.cpu().long(), torch.clamp(ncand.cpu().long(), max=128))
+    ref = kernels.tile_order(count, 128)
+    assert torch.equal(count.cpu()[ref.cpu().long()], count.cpu()[order.cpu().long()])
+    if T > 8192:     # the non-fused path's bins stay bit-exact
+        tmap = obin.TileMap(H, W, 16)
+        ridx, rvalid = obin.assign_bins(proj[:, 0:2].cpu(), keep.cpu().bool(), tmap, 1, 128,
+                                        2048, stable=True)
+        ndiff, tiles = bins_equal_report(idx, valid, ridx, rvalid)
+        assert ndiff == 0, f"{ndiff} tiles differ, first {tiles[:8].tolist()}"

@@ -346,15 +346,27 @@ __global__ __launch_bounds__(256) void k_far_colscan(int* __restrict__ far_blk, 
 // Cell offsets, one block: exclusive scans of the regular and far counts -> cell_start[T+1],
 // far_start[T+1]; both counters are reset to zero for the next call.  Values are staged
 // through LDS so every global access is coalesced.
-constexpr int kScanChunk = 4096;
+//
+// When the whole grid fits one chunk (T <= kScanChunk) the same block also classifies the tiles
+// from the starts still in LDS (what k_tile_classify does otherwise): tiles with more than K
+// candidates go to lists[0..nlist[0]), the others to lists[T-1], lists[T-2], ...; and, when
+// `order` is given, it writes the tiles ordered by kept count min(candidates, K), heaviest first
+// (a counting sort; the splat kernels' block -> tile map), so no separate order pass runs.
+constexpr int kScanChunk = 8192;
 
 __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
                                                    int* __restrict__ far_cnt,
                                                    int* __restrict__ cell_start,
-                                                   int* __restrict__ far_start, int T,
-                                                   int* __restrict__ nlist) {
+                                                   int* __restrict__ far_start, int ntx, int nty,
+                                                   int K, int fuse, int* __restrict__ lists,
+                                                   int* __restrict__ nlist,
+                                                   int32_t* __restrict__ order) {
   __shared__ int s_v[2][kScanChunk];
   __shared__ int s_tmp[2][16];
+  __shared__ int s_n[kScanChunk];     // fused: candidates per tile
+  __shared__ int s_bins[kMaxK + 2];   // fused: counting-sort buckets
+  __shared__ int s_cnt[2];            // fused: heavy / light list lengths
+  const int T = ntx * nty;
   int carry[2] = {0, 0};
   for (int base = 0; base < T; base += kScanChunk) {
     const int n = min(kScanChunk, T - base);
@@ -388,14 +400,57 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
       cell_start[base + i] = s_v[0][i];
       far_start[base + i] = s_v[1][i];
     }
-    __syncthreads();
+    if (!fuse) __syncthreads();
   }
   if (threadIdx.x == 0) {
     cell_start[T] = carry[0];
     far_start[T] = carry[1];
-    nlist[0] = 0;  // tile lists of k_tile_classify
-    nlist[1] = 0;
   }
+  if (!fuse) {
+    if (threadIdx.x == 0) {
+      nlist[0] = 0;  // tile lists of k_tile_classify
+      nlist[1] = 0;
+    }
+    return;
+  }
+  // ---- fused tile classification (T <= kScanChunk: every start is in s_v) ----
+  if (threadIdx.x < 2) s_cnt[threadIdx.x] = 0;
+  for (int c = threadIdx.x; c <= K + 1; c += 1024) s_bins[c] = 0;
+  __syncthreads();
+  auto start = [&](int w, int c) { return c < T ? s_v[w][c] : carry[w]; };
+  for (int t0 = 0; t0 < T; t0 += 1024) {  // uniform trip count: wave-aggregated appends inside
+    const int t = t0 + threadIdx.x;
+    int nc = 0;
+    if (t < T) {
+      const int tx = t % ntx, ty = t / ntx;
+      for (int j = 0; j < 9; ++j) {
+        const int cx = tx - (j % 3 - 1), cy = ty - (j / 3 - 1);
+        if (cx >= 0 && cx < ntx && cy >= 0 && cy < nty) {
+          const int c = cy * ntx + cx;
+          nc += start(0, c + 1) - start(0, c) + start(1, c + 1) - start(1, c);
+        }
+      }
+      s_n[t] = nc;
+    }
+    const int ph = wave_append(&s_cnt[0], t < T && nc > K);
+    if (ph >= 0) lists[ph] = t;
+    const int pl = wave_append(&s_cnt[1], t < T && nc <= K);
+    if (pl >= 0) lists[T - 1 - pl] = t;
+    if (order && t < T) agg_inc(s_bins, K - min(nc, K));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    nlist[0] = s_cnt[0];
+    nlist[1] = s_cnt[1];
+  }
+  if (!order) return;
+  // K + 1 <= 513 buckets: one per thread
+  const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
+  int total;
+  const int ex = block_excl_scan<1024>(v, s_tmp[0], &total);
+  if (threadIdx.x <= K) s_bins[threadIdx.x] = ex;
+  __syncthreads();
+  for (int t = threadIdx.x; t < T; t += 1024) order[agg_inc(s_bins, K - min(s_n[t], K))] = t;
 }
 
 __global__ __launch_bounds__(256) void k_bin_scatter(const float* __restrict__ mu2d, int mu_stride,
@@ -1018,7 +1073,8 @@ size_t tts_bin_workspace_bytes(int G, int H, int W, int S) {
 int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                     int G, int H, int W, int S, int R, int K, int span, int32_t* idx,
                     uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
-                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                    int32_t* order, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
   if (G < 0 || H <= 0 || W <= 0 || !idx || !valid) return TTS_EINVAL;
   if (G > 0 && (!mu2d || !keep || mu_stride < 2 || keep_stride < 1)) return TTS_EINVAL;
   if (G > (1 << 28)) return TTS_EG;  // (j << gbits) | g must fit in 32 bits
@@ -1048,8 +1104,9 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
                                                      nblk, ws.cell_slot);
     if (NB > 0) k_far_colscan<<<NB, 256, 0, stream>>>(ws.far_blk, nblk, ntx, nty, ws.far_cnt);
   }
-  k_bin_scan<<<1, 1024, 0, stream>>>(ws.reg_cnt, ws.far_cnt, ws.cell_start, ws.far_start, T,
-                                     ws.nlist);
+  const int fuse = T <= kScanChunk;
+  k_bin_scan<<<1, 1024, 0, stream>>>(ws.reg_cnt, ws.far_cnt, ws.cell_start, ws.far_start, ntx,
+                                     nty, K, fuse, ws.lists, ws.nlist, order);
   if (G > 0) {
     k_bin_scatter<<<grid1d(G, 256), 256, 0, stream>>>(mu2d, mu_stride, G, ntx, nty, ws.cell_slot,
                                                       ws.cell_start, ws.far_start, ws.far_blk,
@@ -1064,11 +1121,17 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
                            sizeof(unsigned) * (size_t)hist_bins;
   const size_t light_lds = sizeof(unsigned long long) * (size_t)kpow2 * (kSelThreads / 64);
   const size_t lds = heavy_lds > light_lds ? heavy_lds : light_lds;
-  k_tile_classify<<<grid1d(T, 256), 256, 0, stream>>>(ws.cell_start, ws.far_start, ntx, nty, K,
-                                                      ws.lists, ws.nlist);
+  if (!fuse)
+    k_tile_classify<<<grid1d(T, 256), 256, 0, stream>>>(ws.cell_start, ws.far_start, ntx, nty, K,
+                                                        ws.lists, ws.nlist);
   SelectArgs sa{ws.recs, ws.far_g, ws.cell_start, ws.far_start, ntx, nty, Sf, span, K, kpow2,
                 gbits, idx, valid, count, ncand, inv};
   k_bin_select<kSelThreads><<<T, kSelThreads, lds, stream>>>(sa, ws.lists, ws.nlist);
+  // large grids: the order pass runs on the kept counts (the fused scan wrote it otherwise)
+  if (order && !fuse) {
+    if (count) k_tile_order<<<1, 1024, 0, stream>>>(count, T, K, order);
+    else return TTS_EINVAL;
+  }
   return launch_status();
 }
 

@@ -352,6 +352,52 @@ __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
   return c;
 }
 
+// Per-gaussian rows ([G,14] params and moments, [G,12] proj, [G,9] inv) are moved between HBM
+// and the threads through LDS: a block copies its 256 contiguous rows with coalesced accesses
+// (each wave instruction covers 1 KB of consecutive bytes) and each thread then reads its own
+// row from LDS.  Direct row-per-thread accesses would make every wave instruction touch ~28
+// cache lines 56 bytes apart, which the L1 address path, not HBM, turns into the limit.  LDS
+// rows are padded to an odd stride, so the per-thread row reads are free of bank conflicts.
+constexpr int kGeoBlock = 256;
+template <int W, int SW, typename T>
+__device__ __forceinline__ void stage_in(const T* __restrict__ src, int g0, int rows, T* s) {
+  const T* base = src + (int64_t)g0 * W;
+  const int n = rows * W;
+  for (int i = threadIdx.x; i < n; i += kGeoBlock) s[(i / W) * SW + i % W] = base[i];
+}
+template <int W, int SW, typename T>
+__device__ __forceinline__ void stage_out(T* __restrict__ dst, int g0, int rows, const T* s) {
+  T* base = dst + (int64_t)g0 * W;
+  const int n = rows * W;
+  for (int i = threadIdx.x; i < n; i += kGeoBlock) base[i] = s[(i / W) * SW + i % W];
+}
+
+// Slot gradient sum through inverse-table entries e[9] already loaded (see gather_slot_grads):
+// each 36-byte record is read as two 16-byte and one 4-byte load.
+typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ void gather_slots(const float* __restrict__ gslot, const int* e,
+                                             float* gin) {
+  f4u a[9], b[9];
+  float c[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    const float* src = gslot + (int64_t)(e[j] >= 0 ? e[j] : 0) * 9;
+    a[j] = *reinterpret_cast<const f4u*>(src);
+    b[j] = *reinterpret_cast<const f4u*>(src + 4);
+    c[j] = src[8];
+  }
+#pragma unroll
+  for (int k = 0; k < 9; ++k) gin[k] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 9; ++j) {
+    if (e[j] >= 0) {
+      gin[0] += a[j].x; gin[1] += a[j].y; gin[2] += a[j].z; gin[3] += a[j].w;
+      gin[4] += b[j].x; gin[5] += b[j].y; gin[6] += b[j].z; gin[7] += b[j].w;
+      gin[8] += c[j];
+    }
+  }
+}
+
 // SH = true: view-dependent colour from the first n = sh_rest_count(deg) rest coefficients.
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
@@ -360,25 +406,35 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
                                                   const float* __restrict__ camera, float near_z,
                                                   float blur, float* __restrict__ proj,
                                                   uint8_t* __restrict__ keep) {
-  const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= G) return;
-  const Camera cam = load_camera(camera);
-  const float* p = params + (int64_t)g * 14;
-  float rv[SH ? 3 * kShRest : 1];
-  if (SH) sh_load(rest, G, g, n_rest, rv);
-  GeoState s;
-  geo_forward(p, cam, near_z, blur, s, dw);
-  if (SH) {
-    float b[16];
-    sh_basis(p, cam, b);
-    sh_apply(p, b, rv, n_rest, s);
+  __shared__ float s_p[kGeoBlock * 15];
+  __shared__ float s_o[kGeoBlock * 13];
+  const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
+  const int g = g0 + threadIdx.x;
+  stage_in<14, 15>(params, g0, rows, s_p);
+  __syncthreads();
+  if ((int)threadIdx.x < rows) {
+    const Camera cam = load_camera(camera);
+    float p[14];
+#pragma unroll
+    for (int i = 0; i < 14; ++i) p[i] = s_p[threadIdx.x * 15 + i];
+    float rv[SH ? 3 * kShRest : 1];
+    if (SH) sh_load(rest, G, g, n_rest, rv);
+    GeoState s;
+    geo_forward(p, cam, near_z, blur, s, dw);
+    if (SH) {
+      float b[16];
+      sh_basis(p, cam, b);
+      sh_apply(p, b, rv, n_rest, s);
+    }
+    const float keo = s.keep ? s.o * s.rho : 0.0f;
+    const float out[12] = {s.mux, s.muy, s.a, s.b, s.c, s.mc[2], keo * s.color[0],
+                           keo * s.color[1], keo * s.color[2], keo, s.o, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 12; ++i) s_o[threadIdx.x * 13 + i] = out[i];
+    keep[g] = s.keep ? 1 : 0;
   }
-  const float keo = s.keep ? s.o * s.rho : 0.0f;
-  float4* out = reinterpret_cast<float4*>(proj + (int64_t)g * 12);
-  out[0] = make_float4(s.mux, s.muy, s.a, s.b);
-  out[1] = make_float4(s.c, s.mc[2], keo * s.color[0], keo * s.color[1]);
-  out[2] = make_float4(keo * s.color[2], keo, s.o, 0.0f);
-  keep[g] = s.keep ? 1 : 0;
+  __syncthreads();
+  stage_out<12, 13>(proj, g0, rows, s_o);
 }
 
 // gsh (SH only): dL/drest in the rest layout; rows l >= n_rest are written as zero.
@@ -523,23 +579,31 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
     const float* __restrict__ lr, const float* __restrict__ lr_sh,
     const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc, DepthW dwa) {
-  const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= G) return;
-  float* p = params + (int64_t)g * 14;
-  float* mg = m + (int64_t)g * 14;
-  float* vg = v + (int64_t)g * 14;
-  // independent loads first: parameters, Adam moments (their latency overlaps the gathers)
+  __shared__ float s_p[kGeoBlock * 15], s_m[kGeoBlock * 15], s_v[kGeoBlock * 15];
+  __shared__ int s_inv[kGeoBlock * 9];
+  const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
+  const int g = g0 + threadIdx.x;
+  stage_in<9, 9>(inv, g0, rows, s_inv);
+  stage_in<14, 15>(params, g0, rows, s_p);
+  stage_in<14, 15>(m, g0, rows, s_m);
+  stage_in<14, 15>(v, g0, rows, s_v);
+  __syncthreads();
+  if ((int)threadIdx.x < rows) {
+  const int t = threadIdx.x;
+  int e[9];
+#pragma unroll
+  for (int j = 0; j < 9; ++j) e[j] = s_inv[t * 9 + j];
+  float gin[9], gout[14], gcol[3];
+  gather_slots(gslot, e, gin);
   float pl[14], mm[14], vv[14];
 #pragma unroll
   for (int i = 0; i < 14; ++i) {
-    pl[i] = p[i];
-    mm[i] = mg[i];
-    vv[i] = vg[i];
+    pl[i] = s_p[t * 15 + i];
+    mm[i] = s_m[t * 15 + i];
+    vv[i] = s_v[t * 15 + i];
   }
   float rv[SH ? 3 * kShRest : 1];
   if (SH) sh_load(rest, G, g, n_rest, rv);
-  float gin[9], gout[14], gcol[3];
-  gather_slot_grads(gslot, inv, g, gin);
   const Camera cam = load_camera(camera);
   GeoState s;
   geo_forward(pl, cam, near_z, blur, s, dwa.bt);
@@ -564,9 +628,9 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     sgld_apply(pn, g, (uint32_t)step[0], mc.seed, mc.noise_lr * lr[0]);
 #pragma unroll
   for (int i = 0; i < 14; ++i) {
-    p[i] = pn[i];
-    mg[i] = mm[i];
-    vg[i] = vv[i];
+    s_p[t * 15 + i] = pn[i];
+    s_m[t * 15 + i] = mm[i];
+    s_v[t * 15 + i] = vv[i];
     if (gparams) gparams[(int64_t)g * 14 + i] = gout[i];
   }
   if (SH) {
@@ -586,6 +650,11 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
       }
     }
   }
+  }  // active row
+  __syncthreads();
+  stage_out<14, 15>(params, g0, rows, s_p);
+  stage_out<14, 15>(m, g0, rows, s_m);
+  stage_out<14, 15>(v, g0, rows, s_v);
 }
 
 // Batch form: gacc[g] += scale * dL/dparams[g] for one view (one writer per gaussian); with SH

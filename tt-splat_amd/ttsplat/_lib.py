@@ -22,7 +22,7 @@ SIGNATURES = {
     "tts_geom_bwd": (_c_int, [_vp, _c_int, _vp, _c_float, _c_float, _vp, _vp, _vp]),
     "tts_bin_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "tts_assign_bins": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                 _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+                                 _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "tts_theta_u_gathered": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                       _vp, _vp, _vp, _vp]),
     "tts_tile_order": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),

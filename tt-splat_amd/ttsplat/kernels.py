@@ -123,10 +123,11 @@ def bin_workspace(G, H, W, S, device):
 
 
 def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, idx=None,
-                valid=None, count=None, ncand=None, inv=None):
+                valid=None, count=None, ncand=None, inv=None, order=None):
     """mu2d: [G,2] fp32 (or any [G,>=2] row-contiguous view, e.g. the proj record),
     keep: [G] uint8 or bool.  Returns idx[T,K] int32, valid[T,K] uint8, count[T], ncand[T];
-    the inverse table inv[G,9] is written when a buffer is passed."""
+    the inverse table inv[G,9] and the heaviest-first tile order[T] are written when buffers are
+    passed."""
     G = mu2d.shape[0]
     dev = mu2d.device
     if not mu2d.is_cuda or mu2d.dtype != F32 or mu2d.dim() != 2 or mu2d.shape[1] < 2 \
@@ -148,9 +149,11 @@ def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, i
     require(ncand, "ncand", I32, (T,), dev)
     if inv is not None:
         require(inv, "inv", I32, (G, 9), dev)
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
     workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
     call("tts_assign_bins", ptr(mu2d), mu2d.stride(0), ptr(keep), 1, G, H, W, S, R, K, span,
-         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(workspace),
+         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(order), ptr(workspace),
          workspace.numel(), stream())
     return idx, valid, count, ncand
 

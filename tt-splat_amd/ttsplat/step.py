@@ -5,7 +5,7 @@ captures the step as ttnn traces (:551-567) and replays them per iteration (:667
 host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
 host round trip:
 
-    geom_fwd -> assign_bins (4 kernels, + inverse table) -> tile_order -> splat_fwd
+    geom_fwd -> assign_bins (6 kernels, + inverse table and tile order) -> splat_fwd
              -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
              -> adam_advance -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
@@ -171,8 +171,7 @@ class TrainStep:
                          sh_degree=self.sh_degree, depth_bt=self.dw)
         kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
-                            self.ncand, self.inv)
-        kernels.tile_order(self.count, self.K, self.order)
+                            self.ncand, self.inv, self.order)
         if self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
