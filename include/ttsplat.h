@@ -170,7 +170,8 @@ int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* vali
 
 /* -------------------------------------------------------------------- loss ---------- */
 
-/* Bytes of scratch tts_loss_grad needs for an H x W image (no initialisation needed). */
+/* Bytes of scratch tts_loss_grad needs for an H x W image: the SSIM partial maps, 9 planes of
+ * (H-10) x (W-10) floats (no initialisation needed). */
 size_t tts_loss_workspace_bytes(int H, int W);
 
 /* Number of fp32 partial sums tts_loss_grad writes.  The first *n_ssim are sums of the SSIM
@@ -186,18 +187,6 @@ int tts_loss_partials_count(int H, int W, int* n_ssim);
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);
-
-/* Target statistics of the SSIM term: stats [2][3][H-10][W-10] = mu_y and
- * E[y^2] - mu_y^2 of the clamped target on the valid map.  They depend on the target alone, so a
- * training loop computes them once per view (the precomputed y maps of
- * tools/resident_traced.py:431-464). */
-int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream);
-
-/* tts_loss_grad with the target statistics supplied; workspace: 9 (H-10)(W-10) floats (the
- * partial maps). */
-int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
-                        int W, float lambda, float* gimage, float* partials, void* workspace,
-                        size_t workspace_bytes, hipStream_t stream);
 
 /* -------------------------------------------------------------------- adam ---------- */
 

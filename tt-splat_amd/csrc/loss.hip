@@ -4,11 +4,12 @@
 //
 // Two kernels, one colour channel per block, separable filters with register blocking (each
 // value read from LDS once per pass instead of once per tap):
-//   k_ssim_stats  the target's statistics mu_y, s_y on the valid SSIM map (once per target in a
-//                 training loop).
-//   k_ssim_maps   per OUTPUT pixel of the valid SSIM map: the image's filtered moments, S and
-//                 its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] -> maps[3][3][Ho][Wo], the
-//                 tile's sum of S.
+//   k_ssim_maps   per OUTPUT pixel of the valid SSIM map: the five filtered moments mu_x,
+//                 E[x^2], E[xy], mu_y, E[y^2], S and its partials dS/dmu_x, dS/dE[x^2],
+//                 dS/dE[xy] -> maps[3][3][Ho][Wo], the tile's sum of S.  The target's moments
+//                 are filtered in the same passes rather than read from a precomputed buffer:
+//                 in a training step the target arrives from HBM, and its two statistics planes
+//                 per channel would cost twice its own bytes again.
 //   k_ssim_grad   per INPUT pixel: the transposed filter (zero outside the valid map) of the
 //                 three maps, combined as  dmeanS/dx = (F'(A) + 2 x F'(B) + y F'(Cxy)) / Ns,
 //                 gated by 0 <= x <= 1 (the clamp), plus the L1 term (1-l) sign(x-y) / N.
@@ -46,88 +47,18 @@ __device__ __forceinline__ TileItem tile_item(int gx, int gy) {
 
 __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
 
-// Target statistics (per valid map pixel, per channel): mu_y = G*y and s_y = G*(y^2) - mu_y^2
-// of the clamped target.  They depend on the target only, so a training loop computes them once
-// per view (as tools/resident_traced.py:431-464 precomputes its y maps).
-__global__ __launch_bounds__(256) void k_ssim_stats(const float* __restrict__ y, int H, int W,
-                                                    Taps taps, float* __restrict__ stats) {
-  const int Ho = H - kHalo, Wo = W - kHalo;
-  const TileItem it = tile_item((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH);
-  const int ox0 = it.tx * kTW, oy0 = it.ty * kTH, ch = it.ch;
-  __shared__ float sy[kRH][kRW + 1];
-  __shared__ float v[2][kTH][kRW + 1];
-  const int tid = threadIdx.x;
-  for (int i = tid; i < kRH * kRW; i += 256) {
-    const int r = i / kRW, c = i % kRW;
-    const int gr = oy0 + r, gc = ox0 + c;
-    sy[r][c] = (gr < H && gc < W) ? clamp01(y[((int64_t)gr * W + gc) * 3 + ch]) : 0.f;
-  }
-  __syncthreads();
-  if (tid < kRW * (kTH / kVRows)) {
-    const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
-    float acc[2][kVRows];
-#pragma unroll
-    for (int o = 0; o < kVRows; ++o) acc[0][o] = acc[1][o] = 0.f;
-#pragma unroll
-    for (int k = 0; k < kVRows + kHalo; ++k) {
-      const float yv = sy[r0 + k][c], yy = yv * yv;
-#pragma unroll
-      for (int o = 0; o < kVRows; ++o) {
-        const int tap = k - o;
-        if (tap >= 0 && tap < kWin) {
-          acc[0][o] += taps.g[tap] * yv;
-          acc[1][o] += taps.g[tap] * yy;
-        }
-      }
-    }
-#pragma unroll
-    for (int o = 0; o < kVRows; ++o) {
-      v[0][r0 + o][c] = acc[0][o];
-      v[1][r0 + o][c] = acc[1][o];
-    }
-  }
-  __syncthreads();
-  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
-  float f[2][kHCols];
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) f[0][o] = f[1][o] = 0.f;
-#pragma unroll
-  for (int k = 0; k < kHCols + kHalo; ++k) {
-    const float a = v[0][r][c0 + k], b = v[1][r][c0 + k];
-#pragma unroll
-    for (int o = 0; o < kHCols; ++o) {
-      const int tap = k - o;
-      if (tap >= 0 && tap < kWin) {
-        f[0][o] += taps.g[tap] * a;
-        f[1][o] += taps.g[tap] * b;
-      }
-    }
-  }
-  const int64_t plane = (int64_t)Ho * Wo;
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) {
-    const int orow = oy0 + r, ocol = ox0 + c0 + o;
-    if (orow < Ho && ocol < Wo) {
-      const int64_t oi = (int64_t)orow * Wo + ocol;
-      stats[(0 * 3 + ch) * plane + oi] = f[0][o];
-      stats[(1 * 3 + ch) * plane + oi] = f[1][o] - f[0][o] * f[0][o];
-    }
-  }
-}
-
-// Map kernel: per output pixel of the valid SSIM map, the image moments mu_x, E[x^2], E[xy]
-// (three filtered images; the target's mu_y, s_y come precomputed), S and its partials
-// dS/dmu_x, dS/dE[x^2], dS/dE[xy] -> maps[3][3][Ho][Wo]; the tile's sum of S.
+// Map kernel: per output pixel of the valid SSIM map, the moments mu_x, E[x^2], E[xy], mu_y,
+// E[y^2] (five filtered images), S and its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] ->
+// maps[3][3][Ho][Wo]; the tile's sum of S.
 __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
-                                                   const float* __restrict__ y,
-                                                   const float* __restrict__ stats, int H, int W,
+                                                   const float* __restrict__ y, int H, int W,
                                                    Taps taps, float* __restrict__ maps,
                                                    float* __restrict__ partials) {
   const int Ho = H - kHalo, Wo = W - kHalo;
   const TileItem it = tile_item((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH);
   const int ox0 = it.tx * kTW, oy0 = it.ty * kTH, ch = it.ch;
   __shared__ float sx[kRH][kRW + 1], sy[kRH][kRW + 1];
-  __shared__ float v[3][kTH][kRW + 1];
+  __shared__ float v[5][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
   const int tid = threadIdx.x;
   const int64_t plane = (int64_t)Ho * Wo;
@@ -153,29 +84,22 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
       }
     }
   }
-  // this thread's output pixels and their target statistics (loaded ahead of the filtering)
+  // this thread's output pixels in the horizontal pass
   const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
   const int orow = oy0 + r;
-  float smu[kHCols], ssy[kHCols];
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) {
-    const int64_t oi = (int64_t)min(orow, Ho - 1) * Wo + min(ox0 + c0 + o, Wo - 1);
-    smu[o] = stats[(0 * 3 + ch) * plane + oi];
-    ssy[o] = stats[(1 * 3 + ch) * plane + oi];
-  }
   __syncthreads();
   // vertical: thread = (column c, chunk of kVRows output rows)
   if (tid < kRW * (kTH / kVRows)) {
     const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
-    float acc[3][kVRows];
+    float acc[5][kVRows];
 #pragma unroll
-    for (int m = 0; m < 3; ++m)
+    for (int m = 0; m < 5; ++m)
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) acc[m][o] = 0.f;
 #pragma unroll
     for (int k = 0; k < kVRows + kHalo; ++k) {
       const float xv = sx[r0 + k][c], yv = sy[r0 + k][c];
-      const float xx = xv * xv, xy = xv * yv;
+      const float xx = xv * xv, xy = xv * yv, yy = yv * yv;
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) {
         const int tap = k - o;
@@ -184,33 +108,35 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
           acc[0][o] += gk * xv;
           acc[1][o] += gk * xx;
           acc[2][o] += gk * xy;
+          acc[3][o] += gk * yv;
+          acc[4][o] += gk * yy;
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < 3; ++m)
+    for (int m = 0; m < 5; ++m)
 #pragma unroll
       for (int o = 0; o < kVRows; ++o) v[m][r0 + o][c] = acc[m][o];
   }
   __syncthreads();
   // horizontal: thread = (output row r, chunk of kHCols outputs)
-  float f[3][kHCols];
+  float f[5][kHCols];
 #pragma unroll
-  for (int m = 0; m < 3; ++m)
+  for (int m = 0; m < 5; ++m)
 #pragma unroll
     for (int o = 0; o < kHCols; ++o) f[m][o] = 0.f;
 #pragma unroll
   for (int k = 0; k < kHCols + kHalo; ++k) {
-    float vv[3];
+    float vv[5];
 #pragma unroll
-    for (int m = 0; m < 3; ++m) vv[m] = v[m][r][c0 + k];
+    for (int m = 0; m < 5; ++m) vv[m] = v[m][r][c0 + k];
 #pragma unroll
     for (int o = 0; o < kHCols; ++o) {
       const int tap = k - o;
       if (tap >= 0 && tap < kWin) {
         const float gk = taps.g[tap];
 #pragma unroll
-        for (int m = 0; m < 3; ++m) f[m][o] += gk * vv[m];
+        for (int m = 0; m < 5; ++m) f[m][o] += gk * vv[m];
       }
     }
   }
@@ -219,11 +145,11 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
   for (int o = 0; o < kHCols; ++o) {
     const int ocol = ox0 + c0 + o;
     if (orow < Ho && ocol < Wo) {
-      const float mx = f[0][o], my = smu[o];
+      const float mx = f[0][o], my = f[3][o];
       const float A1 = 2.f * mx * my + kC1;
       const float A2 = 2.f * (f[2][o] - mx * my) + kC2;
       const float B1 = mx * mx + my * my + kC1;
-      const float B2 = (f[1][o] - mx * mx) + ssy[o] + kC2;
+      const float B2 = (f[1][o] - mx * mx) + (f[4][o] - my * my) + kC2;
       const float inv_d = 1.0f / (B1 * B2);  // one division; 1/B2 = B1/(B1 B2)
       const float Sv = A1 * A2 * inv_d;
       const int64_t oi = (int64_t)orow * Wo + ocol;
@@ -387,13 +313,8 @@ using namespace tts;
 extern "C" {
 
 size_t tts_loss_workspace_bytes(int H, int W) {
-  // target statistics [2][3] + SSIM partial maps [3][3] planes of (H-10) x (W-10)
+  // the SSIM partial maps: [3][3] planes of (H-10) x (W-10)
   if (H < kWin || W < kWin) return 0;
-  return sizeof(float) * 15 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
-}
-
-// workspace for tts_loss_grad_stats: the three partial maps
-static size_t maps_bytes(int H, int W) {
   return sizeof(float) * 9 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
 }
 
@@ -404,40 +325,19 @@ int tts_loss_partials_count(int H, int W, int* n_ssim) {
   return gm + gg;
 }
 
-int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream) {
-  if (!target || !stats) return TTS_EINVAL;
-  if (H < kWin || W < kWin) return TTS_EINVAL;
-  k_ssim_stats<<<maps_grid(H, W), 256, 0, stream>>>(target, H, W, make_taps(), stats);
-  return launch_status();
-}
-
-int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
-                        int W, float lambda, float* gimage, float* partials, void* workspace,
-                        size_t workspace_bytes, hipStream_t stream) {
-  if (!image || !target || !stats || !gimage) return TTS_EINVAL;
-  if (H < kWin || W < kWin) return TTS_EINVAL;
-  if (!workspace || workspace_bytes < maps_bytes(H, W)) return TTS_EWORKSPACE;
-  const Taps taps = make_taps();
-  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
-  float* maps = static_cast<float*>(workspace);
-  k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, stats, H, W, taps, maps, partials);
-  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
-                                      partials ? partials + gm : nullptr);
-  return launch_status();
-}
-
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
   if (!image || !target || !gimage) return TTS_EINVAL;
   if (H < kWin || W < kWin) return TTS_EINVAL;
   if (!workspace || workspace_bytes < tts_loss_workspace_bytes(H, W)) return TTS_EWORKSPACE;
-  float* stats = static_cast<float*>(workspace);
-  float* maps = stats + 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
-  const int e = tts_loss_target_stats(target, H, W, stats, stream);
-  if (e) return e;
-  return tts_loss_grad_stats(image, target, stats, H, W, lambda, gimage, partials, maps,
-                             maps_bytes(H, W), stream);
+  const Taps taps = make_taps();
+  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
+  float* maps = static_cast<float*>(workspace);
+  k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, H, W, taps, maps, partials);
+  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
+                                      partials ? partials + gm : nullptr);
+  return launch_status();
 }
 
 }  // extern "C"

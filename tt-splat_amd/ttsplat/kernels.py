@@ -339,42 +339,9 @@ def loss_grad(image, target, lam=0.2, gimage=None, partials=None, workspace=None
     if partials is not None:
         require(partials, "partials", F32, (loss_partials_count(H, W)[0],), dev)
     workspace = loss_workspace(H, W, dev) if workspace is None else workspace
+    require(workspace, "workspace", F32)
     call("tts_loss_grad", ptr(image), ptr(target), H, W, float(lam), ptr(gimage), ptr(partials),
          ptr(workspace), workspace.numel() * 4, stream())
-    return gimage
-
-
-def loss_target_stats(target, stats=None):
-    """SSIM statistics of a fixed target: [2,3,H-10,W-10] fp32 (mu_y, E[y^2]-mu_y^2)."""
-    H, W = target.shape[0], target.shape[1]
-    dev = target.device
-    require(target, "target", F32, (H, W, 3))
-    stats = torch.empty(2, 3, H - 10, W - 10, device=dev, dtype=F32) if stats is None else stats
-    require(stats, "stats", F32, (2, 3, H - 10, W - 10), dev)
-    call("tts_loss_target_stats", ptr(target), H, W, ptr(stats), stream())
-    return stats
-
-
-def loss_maps_workspace(H, W, device):
-    """Workspace of loss_grad_stats: the three SSIM partial maps."""
-    return torch.empty(9 * (H - 10) * (W - 10), device=device, dtype=F32)
-
-
-def loss_grad_stats(image, target, stats, lam=0.2, gimage=None, partials=None, workspace=None):
-    """loss_grad with precomputed target statistics."""
-    H, W = image.shape[0], image.shape[1]
-    dev = image.device
-    require(image, "image", F32, (H, W, 3))
-    require(target, "target", F32, (H, W, 3), dev)
-    require(stats, "stats", F32, (2, 3, H - 10, W - 10), dev)
-    gimage = torch.empty_like(image) if gimage is None else gimage
-    require(gimage, "gimage", F32, (H, W, 3), dev)
-    if partials is not None:
-        require(partials, "partials", F32, (loss_partials_count(H, W)[0],), dev)
-    workspace = loss_maps_workspace(H, W, dev) if workspace is None else workspace
-    require(workspace, "workspace", F32)
-    call("tts_loss_grad_stats", ptr(image), ptr(target), ptr(stats), H, W, float(lam),
-         ptr(gimage), ptr(partials), ptr(workspace), workspace.numel() * 4, stream())
     return gimage
 
 

@@ -147,9 +147,7 @@ class TrainStep:
         self.image = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.den = torch.empty(H, W, device=dev, dtype=F32)
         self.gimage = torch.empty(H, W, 3, device=dev, dtype=F32)
-        # the targets are fixed: their SSIM statistics are computed once
-        self.tstats = [kernels.loss_target_stats(t) for t in self.targets]
-        self.loss_ws = kernels.loss_maps_workspace(H, W, dev)
+        self.loss_ws = kernels.loss_workspace(H, W, dev)
         self.partials = torch.empty(kernels.loss_partials_count(H, W)[0], device=dev, dtype=F32)
         self.batch = int(batch)
         if self.batch < 1 or len(self.cams) % self.batch:
@@ -188,8 +186,8 @@ class TrainStep:
     def _view_backward(self, ci):
         """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
         self.forward(ci)
-        kernels.loss_grad_stats(self.image, self.targets[ci], self.tstats[ci], self.lam,
-                                self.gimage, self.partials, self.loss_ws)
+        kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
+                          self.loss_ws)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                           self.k, self.image, self.den, self.gimage, self.gslot,
                           order=self.order)
