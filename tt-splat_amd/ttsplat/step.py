@@ -5,7 +5,7 @@ captures the step as ttnn traces (:551-567) and replays them per iteration (:667
 host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
 host round trip:
 
-    geom_fwd -> assign_bins (6 kernels, + inverse table and tile order) -> splat_fwd
+    geom_fwd -> assign_bins (5 kernels, + inverse table and tile order) -> splat_fwd
              -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
              -> adam_advance -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
