@@ -21,7 +21,11 @@
 //                       in g order.
 //   2. k_far_colscan    per border cell, exclusive scan of the far counts over count blocks.
 //   3. k_bin_scan       one block: copy offsets and exclusive scans -> cell_start[T+1],
-//                       far_start[T+1]; resets the counters for the next call.
+//                       far_start[T+1]; resets the counters for the next call.  When the tile
+//                       grid fits its LDS (T <= 8192) it also classifies the tiles (a tile's
+//                       candidates are the 3x3 box sum of the cell totals, formed as row
+//                       3-sums then column 3-sums) and writes the heaviest-first tile order;
+//                       larger grids run k_tile_classify / k_tile_order instead.
 //   4. k_bin_scatter    regular gaussians -> (g, mu_x, mu_y) records, far -> g at their ranks:
 //                       every cell's far ids end up ascending.
 //   5. k_bin_select     one block per tile (below).
@@ -363,10 +367,107 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
                                                    int32_t* __restrict__ order) {
   __shared__ int s_v[2][kScanChunk];
   __shared__ int s_tmp[2][16];
-  __shared__ int s_n[kScanChunk];     // fused: candidates per tile
+  __shared__ int s_n[kScanChunk];     // fused: cell totals, then their row 3-sums
   __shared__ int s_bins[kMaxK + 2];   // fused: counting-sort buckets
   __shared__ int s_cnt[2];            // fused: heavy / light list lengths
   const int T = ntx * nty;
+  if (fuse) {
+    // ---- T <= kScanChunk: counts, starts and the tile classification all in LDS ----
+    int* s_r = s_v[0];
+    int* s_f = s_v[1];
+    for (int i = threadIdx.x; i < T; i += 1024) {
+      const int r = reg_cnt[i], f = far_cnt[i];
+      s_r[i] = r;
+      s_f[i] = f;
+      s_n[i] = r + f;
+      reg_cnt[i] = 0;
+      far_cnt[i] = 0;
+    }
+    if (threadIdx.x < 2) s_cnt[threadIdx.x] = 0;
+    for (int c = threadIdx.x; c <= K + 1; c += 1024) s_bins[c] = 0;
+    __syncthreads();
+    // thread = tiles [lo, lo + per): its partial sums of both counts, and the row 3-sums of the
+    // cell totals (a tile's candidates are the 3x3 box sum of the totals around its cell)
+    constexpr int kPer = kScanChunk / 1024;
+    const int per = (T + 1023) / 1024;
+    const int lo = threadIdx.x * per;
+    int sr = 0, sf = 0, hs[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int t = lo + k;
+      hs[k] = 0;
+      if (k < per && t < T) {
+        sr += s_r[t];
+        sf += s_f[t];
+        const int tx = t % ntx;
+        hs[k] = s_n[t] + (tx > 0 ? s_n[t - 1] : 0) + (tx + 1 < ntx ? s_n[t + 1] : 0);
+      }
+    }
+    int tr, tf;
+    int er = block_excl_scan<1024>(sr, s_tmp[0], &tr);  // barriers: every LDS read above is done
+    int ef = block_excl_scan<1024>(sf, s_tmp[1], &tf);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int t = lo + k;
+      if (k < per && t < T) {
+        const int r = s_r[t], f = s_f[t];
+        s_r[t] = er;
+        s_f[t] = ef;
+        er += r;
+        ef += f;
+        s_n[t] = hs[k];
+      }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < T; i += 1024) {
+      cell_start[i] = s_r[i];
+      far_start[i] = s_f[i];
+    }
+    if (threadIdx.x == 0) {
+      cell_start[T] = tr;
+      far_start[T] = tf;
+    }
+    // classification: candidates <= K -> light, else heavy (heavy listed first); the kept count
+    // every tile ends with, min(candidates, K), keys the heaviest-first order
+    int ncs[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      ncs[k] = 0;
+      if (k * 1024 < T) {  // uniform: wave-aggregated appends inside
+        const int t = k * 1024 + threadIdx.x;
+        int nc = 0;
+        if (t < T) {
+          const int ty = t / ntx;
+          nc = s_n[t] + (ty > 0 ? s_n[t - ntx] : 0) + (ty + 1 < nty ? s_n[t + ntx] : 0);
+        }
+        ncs[k] = nc;
+        const int ph = wave_append(&s_cnt[0], t < T && nc > K);
+        if (ph >= 0) lists[ph] = t;
+        const int pl = wave_append(&s_cnt[1], t < T && nc <= K);
+        if (pl >= 0) lists[T - 1 - pl] = t;
+        if (order && t < T) agg_inc(s_bins, K - min(nc, K));
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      nlist[0] = s_cnt[0];
+      nlist[1] = s_cnt[1];
+    }
+    if (!order) return;
+    // K + 1 <= 513 buckets: one per thread
+    const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
+    int total;
+    const int ex = block_excl_scan<1024>(v, s_tmp[0], &total);
+    if (threadIdx.x <= K) s_bins[threadIdx.x] = ex;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int t = k * 1024 + threadIdx.x;
+      if (k * 1024 < T && t < T) order[agg_inc(s_bins, K - min(ncs[k], K))] = t;
+    }
+    return;
+  }
+  // ---- larger grids: chunked scans; k_tile_classify / k_tile_order run separately ----
   int carry[2] = {0, 0};
   for (int base = 0; base < T; base += kScanChunk) {
     const int n = min(kScanChunk, T - base);
@@ -400,57 +501,14 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
       cell_start[base + i] = s_v[0][i];
       far_start[base + i] = s_v[1][i];
     }
-    if (!fuse) __syncthreads();
+    __syncthreads();
   }
   if (threadIdx.x == 0) {
     cell_start[T] = carry[0];
     far_start[T] = carry[1];
+    nlist[0] = 0;  // tile lists of k_tile_classify
+    nlist[1] = 0;
   }
-  if (!fuse) {
-    if (threadIdx.x == 0) {
-      nlist[0] = 0;  // tile lists of k_tile_classify
-      nlist[1] = 0;
-    }
-    return;
-  }
-  // ---- fused tile classification (T <= kScanChunk: every start is in s_v) ----
-  if (threadIdx.x < 2) s_cnt[threadIdx.x] = 0;
-  for (int c = threadIdx.x; c <= K + 1; c += 1024) s_bins[c] = 0;
-  __syncthreads();
-  auto start = [&](int w, int c) { return c < T ? s_v[w][c] : carry[w]; };
-  for (int t0 = 0; t0 < T; t0 += 1024) {  // uniform trip count: wave-aggregated appends inside
-    const int t = t0 + threadIdx.x;
-    int nc = 0;
-    if (t < T) {
-      const int tx = t % ntx, ty = t / ntx;
-      for (int j = 0; j < 9; ++j) {
-        const int cx = tx - (j % 3 - 1), cy = ty - (j / 3 - 1);
-        if (cx >= 0 && cx < ntx && cy >= 0 && cy < nty) {
-          const int c = cy * ntx + cx;
-          nc += start(0, c + 1) - start(0, c) + start(1, c + 1) - start(1, c);
-        }
-      }
-      s_n[t] = nc;
-    }
-    const int ph = wave_append(&s_cnt[0], t < T && nc > K);
-    if (ph >= 0) lists[ph] = t;
-    const int pl = wave_append(&s_cnt[1], t < T && nc <= K);
-    if (pl >= 0) lists[T - 1 - pl] = t;
-    if (order && t < T) agg_inc(s_bins, K - min(nc, K));
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    nlist[0] = s_cnt[0];
-    nlist[1] = s_cnt[1];
-  }
-  if (!order) return;
-  // K + 1 <= 513 buckets: one per thread
-  const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
-  int total;
-  const int ex = block_excl_scan<1024>(v, s_tmp[0], &total);
-  if (threadIdx.x <= K) s_bins[threadIdx.x] = ex;
-  __syncthreads();
-  for (int t = threadIdx.x; t < T; t += 1024) order[agg_inc(s_bins, K - min(s_n[t], K))] = t;
 }
 
 __global__ __launch_bounds__(256) void k_bin_scatter(const float* __restrict__ mu2d, int mu_stride,
