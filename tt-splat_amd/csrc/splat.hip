@@ -12,7 +12,7 @@
 // contracted over the tile's pixels slot-parallel (TPS threads share one slot and split its
 // rows).  Along a pixel row, u = (th0*lx + c1)*lx + c0 with c0, c1 fixed per row, and the
 // theta gradient is gathered as three row moments sum(gu*lx^2), sum(gu*lx), sum(gu), so the
-// inner loop costs 16 VALU ops per (pixel, slot) pair.  Each slot's 10 partial sums are
+// inner loop costs 17 VALU ops per (pixel, slot) pair (per-row terms included).  Each slot's 10 partial sums are
 // combined in LDS and pushed through the theta backward; the slot's 9 gradients are stored to
 // gslot[T,K,9] (no atomics: the per-gaussian sum over its <= 9 slots is a gather through the
 // inverse bin table, in a fixed order, done by the geometry backward).
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
 }
 
 template <int S, bool FROM_PROJ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void k_splat_bwd(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_splat_bwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
     const uint8_t* __restrict__ valid, const float* __restrict__ theta,
     const float* __restrict__ col, const float* __restrict__ oc,
@@ -174,6 +174,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     float* __restrict__ gwb) {
   constexpr int P = S * S;
   constexpr int PPT = P / 256;
+  constexpr int kRowChunks = S == 16 ? 2 : 1;  // 8-pixel chunks of a row unrolled
   extern __shared__ unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   __shared__ float s_ftmp[4];
@@ -239,6 +240,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f;
     float gr = 0.f, gg = 0.f, gb = 0.f, go = 0.f;
     if (active) {
+#pragma unroll 2
       for (int y = h; y < S; y += tps) {
         const float ly = (float)y + 0.5f;
         const float yy = ly * ly;
@@ -246,8 +248,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         const float cc1 = A.z * ly + A.w;
         float m0 = 0.f, m1 = 0.f, m2 = 0.f;
         const float4* row = s_px + y * S;
-        // 8-pixel chunks keep the in-flight LDS operands (and so the VGPR count) bounded
-#pragma unroll 1
+        // S = 16: fully unrolled along the row, so lx and lx^2 are literals (2 VALU ops per pair
+        // fewer than a rolled loop over 8-pixel chunks, which recomputes them).  S = 32 keeps
+        // the rolled chunks: unrolled, its 32-pixel rows spill registers.
+#pragma unroll kRowChunks
         for (int xb = 0; xb < S; xb += 8) {
           const float xbf = (float)xb;
 #pragma unroll
