@@ -238,10 +238,14 @@ int tts_geom_bwd_accum(const float* params, int G, const float* camera, float ne
  * for it (the dense arm-B autograd of spike/render.py). */
 
 /* Geometry forward with SH colour and/or the depth weight.  Replaces the SHD > 0 and
- * --depth-weight branches of tools/resident_traced.py:327-346 (geom_fwd). */
+ * --depth-weight branches of tools/resident_traced.py:327-346 (geom_fwd).
+ * step_adv (optional, the training step's Adam step block): also advanced in this launch, as
+ * tts_adam_advance(step_adv, beta1, beta2) would (the first kernel of a training step carries
+ * the advance instead of a launch of its own).  NULL: beta1, beta2 are ignored. */
 int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
                     const float* depth_bt, int G, const float* camera, float near_z, float blur,
-                    float* proj, uint8_t* keep, hipStream_t stream);
+                    float* proj, uint8_t* keep, int32_t* step_adv, float beta1, float beta2,
+                    hipStream_t stream);
 
 /* Geometry backward with SH colour and/or the depth weight: grad9 -> gparams[G,14], gsh_rest
  * (rest layout; rows beyond the degree written as zero; needed when sh_degree > 0), gdepth [G,2]

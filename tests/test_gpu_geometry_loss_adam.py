@@ -102,6 +102,28 @@ def test_adam_matches_torch():
     assert max_abs(p, ref) <= 1e-6
 
 
+def test_geom_fwd_carries_the_step_advance():
+    """geom_fwd(advance=step) advances the Adam step block exactly as adam_advance does and
+    renders the same projection; without it the block is untouched."""
+    cfg, P, cam = config_inputs("c1_ref")
+    camb = cam.device_block("cuda")
+    Pc = P.cuda()
+    ref_proj, ref_keep = kernels.geom_fwd(Pc, camb)
+    s1 = kernels.adam_state("cuda")
+    s2 = kernels.adam_state("cuda")
+    for _ in range(3):
+        kernels.adam_advance(s1)
+        proj, keep = kernels.geom_fwd(Pc, camb, advance=s2)
+        torch.cuda.synchronize()
+        assert torch.equal(s1, s2)
+        assert torch.equal(proj, ref_proj) and torch.equal(keep, ref_keep)
+    assert int(s2[0]) == 3
+    before = s2.clone()
+    kernels.geom_fwd(Pc, camb)
+    torch.cuda.synchronize()
+    assert torch.equal(s2, before)
+
+
 def test_geom_bwd_adam_fused_equals_separate():
     """slot gather-reduce + geometry bwd + Adam in one kernel == the three separate ops."""
     cfg, P, cam = config_inputs("c1_ref")

@@ -51,7 +51,7 @@ def test_geom_fwd_sh_degree0_and_zero_rest_equal_dc():
     p0 = torch.empty_like(base)
     k0 = torch.empty(cfg.G, device="cuda", dtype=torch.uint8)
     _lib.call("tts_geom_fwd_ex", _lib.ptr(Pc), _lib.ptr(zero), 0, None, cfg.G, _lib.ptr(camb),
-              0.2, 0.3, _lib.ptr(p0), _lib.ptr(k0), _lib.stream())
+              0.2, 0.3, _lib.ptr(p0), _lib.ptr(k0), None, 0.9, 0.999, _lib.stream())
     assert torch.equal(k0, _lib_keep(Pc, camb))
     assert float(((p0 - base).abs() / base.abs().clamp(min=1.0)).max()) <= 1e-6
     # zero rest at degree 3: the colour is the DC colour (up to the summation order)
@@ -93,7 +93,7 @@ def test_bad_sh_arguments_raise():
     keep = torch.empty(cfg.G, device="cuda", dtype=torch.uint8)
     with pytest.raises(_lib.TTSError, match="SH degree"):   # the C ABI's own check
         _lib.call("tts_geom_fwd_ex", _lib.ptr(Pc), None, 2, None, cfg.G, _lib.ptr(camb), 0.2,
-                  0.3, _lib.ptr(proj), _lib.ptr(keep), _lib.stream())
+                  0.3, _lib.ptr(proj), _lib.ptr(keep), None, 0.9, 0.999, _lib.stream())
 
 
 def target_for(cfg, cam, rest=None, deg=0):

@@ -398,6 +398,21 @@ __device__ __forceinline__ void gather_slots(const float* __restrict__ gslot, co
   }
 }
 
+// Adam step block: step[0] int32 step number; step[1..2] fp32 1/bc1 and 1/sqrt(bc2) for that
+// step (double-precision powers, as torch.optim.Adam's host-side bias corrections).  One thread.
+__device__ __forceinline__ void advance_step(int32_t* step, float b1, float b2) {
+  const int t = step[0] + 1;
+  step[0] = t;
+  const double bc1 = 1.0 - pow((double)b1, (double)t);
+  const double bc2 = 1.0 - pow((double)b2, (double)t);
+  float* f = reinterpret_cast<float*>(step);
+  f[1] = (float)(1.0 / bc1);
+  f[2] = (float)(1.0 / sqrt(bc2));
+}
+
+// adv (optional): a training step's Adam step block, advanced by block 0 after its rows (what a
+// separate k_adam_advance launch would do; nothing between this kernel and the Adam update
+// reads the block).
 // SH = true: view-dependent colour from the first n = sh_rest_count(deg) rest coefficients.
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
@@ -405,7 +420,8 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
                                                   const float* __restrict__ dw,
                                                   const float* __restrict__ camera, float near_z,
                                                   float blur, float* __restrict__ proj,
-                                                  uint8_t* __restrict__ keep) {
+                                                  uint8_t* __restrict__ keep, int32_t* adv,
+                                                  float b1, float b2) {
   __shared__ float s_p[kGeoBlock * 15];
   __shared__ float s_o[kGeoBlock * 13];
   const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
@@ -435,6 +451,7 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
   }
   __syncthreads();
   stage_out<12, 13>(proj, g0, rows, s_o);
+  if (adv && blockIdx.x == 0 && threadIdx.x == 0) advance_step(adv, b1, b2);
 }
 
 // gsh (SH only): dL/drest in the rest layout; rows l >= n_rest are written as zero.
@@ -475,16 +492,9 @@ __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ para
   }
 }
 
-// step[0]: int32 step number; step[1..2]: fp32 1/bc1 and 1/sqrt(bc2) for that step.
 __global__ void k_adam_advance(int32_t* step, float b1, float b2) {
   if (threadIdx.x != 0 || blockIdx.x != 0) return;
-  const int t = step[0] + 1;
-  step[0] = t;
-  const double bc1 = 1.0 - pow((double)b1, (double)t);
-  const double bc2 = 1.0 - pow((double)b2, (double)t);
-  float* f = reinterpret_cast<float*>(step);
-  f[1] = (float)(1.0 / bc1);
-  f[2] = (float)(1.0 / sqrt(bc2));
+  advance_step(step, b1, b2);
 }
 
 __device__ __forceinline__ void adam_update(float& p, float& m, float& v, float g, float lr,
@@ -836,7 +846,8 @@ int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, 
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
   k_geom_fwd<false><<<grid1d(G, 256), 256, 0, stream>>>(params, G, nullptr, 0, nullptr, camera,
-                                                        near_z, blur, proj, keep);
+                                                        near_z, blur, proj, keep, nullptr, 0.f,
+                                                        0.f);
   return launch_status();
 }
 
@@ -849,18 +860,23 @@ static int sh_args(int deg, const void* rest) {
 
 int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
                     const float* depth_bt, int G, const float* camera, float near_z, float blur,
-                    float* proj, uint8_t* keep, hipStream_t stream) {
+                    float* proj, uint8_t* keep, int32_t* step_adv, float beta1, float beta2,
+                    hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
   if (const int e = sh_args(sh_degree, sh_rest)) return e;
   if (G >= (1 << 30)) return TTS_EG;
-  if (G == 0) return TTS_OK;
+  if (G == 0) {  // no rows: the advance alone
+    if (step_adv) k_adam_advance<<<1, 64, 0, stream>>>(step_adv, beta1, beta2);
+    return launch_status();
+  }
   const dim3 grid = grid1d(G, 256);
   if (sh_degree > 0)
     k_geom_fwd<true><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_rest_count(sh_degree),
-                                               depth_bt, camera, near_z, blur, proj, keep);
+                                               depth_bt, camera, near_z, blur, proj, keep,
+                                               step_adv, beta1, beta2);
   else
     k_geom_fwd<false><<<grid, 256, 0, stream>>>(params, G, nullptr, 0, depth_bt, camera, near_z,
-                                                blur, proj, keep);
+                                                blur, proj, keep, step_adv, beta1, beta2);
   return launch_status();
 }
 

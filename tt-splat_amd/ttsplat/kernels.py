@@ -60,10 +60,12 @@ def _dw_check(depth_bt, dev):
 
 
 def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest=None,
-             sh_degree=0, depth_bt=None):
+             sh_degree=0, depth_bt=None, advance=None, b1=None, b2=None):
     """Projection + activations -> proj[G,12], keep[G].  sh_degree > 0: view-dependent colour
     from the rest coefficients sh_rest [15,3,G] (sh_rest_layout of spike's color_rest).
-    depth_bt (device (beta, tau)): the depth weight sigmoid(beta (tau - z_cam)) on the opacity."""
+    depth_bt (device (beta, tau)): the depth weight sigmoid(beta (tau - z_cam)) on the opacity.
+    advance (a training step's Adam step block): advanced in the same launch, as
+    adam_advance(advance, b1, b2) would."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
@@ -74,9 +76,12 @@ def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest
     keep = torch.empty(G, device=dev, dtype=U8) if keep is None else keep
     _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
     require(keep, "keep", U8, (G,), dev)
-    if sh_degree > 0 or depth_bt is not None:
+    if advance is not None:
+        require(advance, "advance", I32, (4,), dev)
+    if sh_degree > 0 or depth_bt is not None or advance is not None:
         call("tts_geom_fwd_ex", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt), G,
-             ptr(camera), near, blur, ptr(proj), ptr(keep), stream())
+             ptr(camera), near, blur, ptr(proj), ptr(keep), ptr(advance),
+             BETA1 if b1 is None else b1, BETA2 if b2 is None else b2, stream())
     else:
         call("tts_geom_fwd", ptr(params), G, ptr(camera), near, blur, ptr(proj), ptr(keep),
              stream())

@@ -5,9 +5,9 @@ captures the step as ttnn traces (:551-567) and replays them per iteration (:667
 host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
 host round trip:
 
-    geom_fwd -> assign_bins (5 kernels, + inverse table and tile order) -> splat_fwd
-             -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
-             -> adam_advance -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
+    geom_fwd (+ Adam step advance) -> assign_bins (5 kernels, + inverse table and tile order)
+             -> splat_fwd -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
+             -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
 captured once per camera into a HIP graph (torch.cuda.CUDAGraph) and replayed.  The step
 counter and Adam bias corrections live in device memory, so replays need no re-capture.
@@ -163,10 +163,12 @@ class TrainStep:
         return None if self.sh is None else kernels.sh_rest_model(self.sh)
 
     # ---------------------------------------------------------------------------------
-    def forward(self, ci=0):
-        """Geometry + binning + fused splat for camera ci into self.image (no training)."""
+    def forward(self, ci=0, advance=False):
+        """Geometry + binning + fused splat for camera ci into self.image.  advance=True: the
+        geometry launch also advances the Adam step block (a training step's first kernel)."""
         kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep, sh_rest=self.sh,
-                         sh_degree=self.sh_degree, depth_bt=self.dw)
+                         sh_degree=self.sh_degree, depth_bt=self.dw,
+                         advance=self.step_block if advance else None)
         kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
                             self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
                             self.ncand, self.inv, self.order)
@@ -183,9 +185,9 @@ class TrainStep:
         """Number of distinct steps (views for batch = 1, batches otherwise)."""
         return len(self.cams) // self.batch
 
-    def _view_backward(self, ci):
+    def _view_backward(self, ci, advance=False):
         """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
-        self.forward(ci)
+        self.forward(ci, advance)
         kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
                           self.loss_ws)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
@@ -197,8 +199,7 @@ class TrainStep:
         sh = dict(sh_rest=self.sh, sh_degree=self.sh_degree)
         mc = self.mc
         if self.batch == 1:
-            self._view_backward(i)
-            kernels.adam_advance(self.step_block)
+            self._view_backward(i, advance=True)   # the step advance rides on geom_fwd
             kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
                                   self.lr, self.step_block, sh_m=self.sh_m, sh_v=self.sh_v,
                                   lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
