@@ -337,8 +337,8 @@ def cpu_baseline(cfg, seconds, torch):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py runs on exactly one GPU: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md)", file=sys.stderr)
+        print("bench.py runs on exactly one GPU: the training step has no multi-GPU path "
+              "(one process, one device); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
     import torch
     from ttsplat import kernels, scenes
