@@ -4,14 +4,16 @@
 
 Headline (`value`): training iterations per second at G=100k (clustered), 1264x832, K=128,
 8 orbit cameras round-robin (one camera per step), fp32: each step is geometry fwd, binning,
-fused splat fwd, L1+SSIM loss gradient, fused splat bwd (+theta bwd + slot->gaussian atomics),
-geometry bwd + Adam, replayed as one HIP graph per camera.  Inputs are resident on the GPU
-before the timed region; the timed region is exactly K steps between two synchronisations.
+fused splat fwd, L1+SSIM loss gradient, fused splat bwd (+theta bwd, per-slot gradients),
+slot gather + geometry bwd + Adam, replayed as one HIP graph per camera.  Inputs are resident
+on the GPU before the timed region; the timed region is exactly K steps between two
+synchronisations.
 
 Also reported: forward fps (geometry + binning + splat, graph replay) for the same scene, the
-G=2000 128x128 numbers, per-kernel times from HIP events on the launch stream, the roofline of
-the dominant kernel, and the CPU oracle (PyTorch-CPU restatement of the reference path) timed on
-this host's cores on a bounded sample of the same workload.
+G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from HIP events on
+the launch stream, the roofline of the dominant kernel, and the CPU oracle (PyTorch-CPU
+restatement of the reference path) timed on this host's cores, and on one thread, on bounded
+samples of the same workload.
 """
 import argparse
 import json
@@ -328,10 +330,23 @@ def cpu_baseline(cfg, seconds, torch):
             osplat.render_binned(P, cam, tmap, K=cfg.K, k=cfg.k)
             nf += 1
     df = time.perf_counter() - t1
-    return dict(value=n / dt, unit="it/s", cores=torch.get_num_threads(), kind="port",
+    cores = torch.get_num_threads()
+    # the same train step on one thread (a shorter bounded sample)
+    torch.set_num_threads(1)
+    try:
+        n1, t2 = 0, time.perf_counter()
+        while n1 < 1 or time.perf_counter() - t2 < seconds / 3:
+            opipe.train_step(P, m, v, n + n1 + 2, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)
+            n1 += 1
+        d1 = time.perf_counter() - t2
+    finally:
+        torch.set_num_threads(cores)
+    return dict(value=n / dt, unit="it/s", cores=cores, kind="port",
                 sample=f"{n} oracle train steps ({dt:.1f} s) + {nf} forwards ({df:.1f} s) "
                        f"after 1 warm-up, {cfg.name} camera 0",
-                fwd_fps=nf / df)
+                fwd_fps=nf / df,
+                one_thread=dict(value=n1 / d1, unit="it/s", cores=1,
+                                sample=f"{n1} oracle train steps ({d1:.1f} s)"))
 
 
 def main():
