@@ -140,3 +140,48 @@ def test_bf16_train_step():
     assert float(ts.loss()) < 0.8 * l0
     with pytest.raises(ValueError):
         TrainStep(P, [cam], [tgt], K=cfg.K, S=32, k=cfg.k, dtype="bf16")
+
+
+@pytest.mark.parametrize("G", [1, 257])
+def test_train_step_small_and_ragged_sets(G):
+    """One gaussian, and a set that leaves the last geometry workgroup ragged (257 rows): the
+    step still matches the oracle's step."""
+    cfg, P, cam = config_inputs("c1_ref", G=G)
+    P[:, 0:3] *= 0.3                      # keep the few gaussians in view
+    tgt = target_for(cfg, cam)
+    ts = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k)
+    ts.enqueue(0)
+    torch.cuda.synchronize()
+    bins = (ts.idx.cpu().long(), ts.valid.cpu().bool())
+    assert int(ts.valid.sum()) > 0
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    Pr = P.clone()
+    m = torch.zeros_like(Pr)
+    v = torch.zeros_like(Pr)
+    img, L, g = opipe.train_step(Pr, m, v, 1, cam_dict(cam), tmap, tgt.cpu(),
+                                 lr_vector(device="cpu"), K=cfg.K, k=cfg.k, bins=bins)
+    assert float((ts.image.cpu() - img).abs().max()) <= 1e-4
+    assert abs(float(ts.loss()) - float(L)) <= 1e-5
+    assert rel_l2(ts.P.cpu() - P, Pr - P) <= 1e-2
+
+
+def test_train_step_with_everything_culled():
+    """Every gaussian behind the camera: the image is the background, no gradient reaches the
+    parameters (Adam leaves them unchanged), and graph replays agree with eager steps."""
+    cfg, P, cam = config_inputs("c1_ref")
+    P = P.clone()
+    P[:, 2] = 10.0                        # the camera sits at z = 3 looking at the origin
+    tgt = torch.rand(cfg.H, cfg.W, 3, generator=torch.Generator().manual_seed(4))
+    eager = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k)
+    graph = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k)
+    graph.capture()
+    for _ in range(3):
+        eager.step(0)
+        graph.step(0)
+    torch.cuda.synchronize()
+    assert int(eager.keep.sum()) == 0 and int(eager.valid.sum()) == 0
+    assert float((eager.image - 1.0).abs().max()) <= 1e-6        # w_b c_b / w_b = c_b = 1
+    assert torch.equal(eager.P.cpu(), P) and torch.equal(graph.P.cpu(), P)
+    assert float(eager.m.abs().max()) == 0.0
+    assert abs(float(eager.loss()) - float(graph.loss())) == 0.0
+    assert int(graph.step_block[0]) == 3
