@@ -183,7 +183,8 @@ int tts_loss_partials_count(int H, int W, int* n_ssim);
  * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4.
  * Replaces spike/metrics.py:26-28 (loss_fn, differentiated by autograd), the manual gradient
  * tools/loss_manual.py:76-103 and the device loss tools/resident_traced.py:431-464.
- * image, target, gimage: [H,W,3]; H, W >= 11.  partials may be NULL. */
+ * image, target, gimage: [H,W,3]; H, W >= 11 and H*W*36 <= 2^31-1 (TTS_EINVAL otherwise: the
+ * kernels address with 32-bit buffer offsets; 7680x4320 fits).  partials may be NULL. */
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);

@@ -47,6 +47,22 @@ __device__ __forceinline__ TileItem tile_item(int gx, int gy) {
 
 __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
 
+// Buffer-resource addressing: a wave-uniform base (scalar offset: row, plane) plus a 32-bit
+// per-lane byte offset (column), so no lane forms a 64-bit address.  Every buffer handed to
+// these kernels is under 2^31 bytes (the entry point checks); a resource's size is its bound,
+// and the indices are clamped inside it as well.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc rsrc(const float* p, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float bld(Rsrc r, unsigned voff, unsigned soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void bst(Rsrc r, unsigned voff, unsigned soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
+}
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
 // Map kernel: per output pixel of the valid SSIM map, the moments mu_x, E[x^2], E[xy], mu_y,
 // E[y^2] (five filtered images), S and its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] ->
 // maps[3][3][Ho][Wo]; the tile's sum of S.
@@ -61,26 +77,27 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
   __shared__ float v[5][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
   const int tid = threadIdx.x;
-  const int64_t plane = (int64_t)Ho * Wo;
-  {
-    constexpr int kPer = (kRH * kRW + 255) / 256;
-    float a[kPer], b[kPer];
+  const unsigned plane = (unsigned)(Ho * Wo);
+  {  // region rows [oy0, oy0+26), cols [ox0, ox0+42): lane = column, wave w takes rows w, w+4, ...
+    constexpr int NI = (kRH + 3) / 4;
+    const Rsrc xs = rsrc(x, (size_t)H * W * 12), ys = rsrc(y, (size_t)H * W * 12);
+    const int lane = tid & 63, wv = wave_id();
+    const unsigned coff = ((unsigned)min(ox0 + lane, W - 1) * 3u + (unsigned)ch) * 4u;
+    float a[NI], b[NI];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {  // every load in flight before any is used
-      const int i = min(tid + 256 * k, kRH * kRW - 1);
-      const int gr = min(oy0 + i / kRW, H - 1), gc = min(ox0 + i % kRW, W - 1);
-      const int64_t pi = ((int64_t)gr * W + gc) * 3 + ch;
-      a[k] = x[pi];
-      b[k] = y[pi];
+    for (int i = 0; i < NI; ++i) {
+      const int gr = min(oy0 + wv + 4 * i, H - 1);
+      a[i] = bld(xs, coff, (unsigned)(gr * W) * 12u);
+      b[i] = bld(ys, coff, (unsigned)(gr * W) * 12u);
     }
+    const bool col_ok = lane < kRW && ox0 + lane < W;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = tid + 256 * k;
-      if (i < kRH * kRW) {
-        const int r = i / kRW, c = i % kRW;
-        const bool in = oy0 + r < H && ox0 + c < W;
-        sx[r][c] = in ? clamp01(a[k]) : 0.f;
-        sy[r][c] = in ? clamp01(b[k]) : 0.f;
+    for (int i = 0; i < NI; ++i) {
+      const int r = wv + 4 * i;
+      if (r < kRH && lane < kRW) {
+        const bool in = col_ok && oy0 + r < H;
+        sx[r][lane] = in ? clamp01(a[i]) : 0.f;
+        sy[r][lane] = in ? clamp01(b[i]) : 0.f;
       }
     }
   }
@@ -150,12 +167,14 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
       const float A2 = 2.f * (f[2][o] - mx * my) + kC2;
       const float B1 = mx * mx + my * my + kC1;
       const float B2 = (f[1][o] - mx * mx) + (f[4][o] - my * my) + kC2;
-      const float inv_d = 1.0f / (B1 * B2);  // one division; 1/B2 = B1/(B1 B2)
+      // hardware reciprocal (1 ulp): B1 >= C1 and B2 >= C2 - rounding, so B1*B2 is normal
+      const float inv_d = __builtin_amdgcn_rcpf(B1 * B2);
       const float Sv = A1 * A2 * inv_d;
-      const int64_t oi = (int64_t)orow * Wo + ocol;
-      maps[(0 * 3 + ch) * plane + oi] = 2.f * inv_d * (my * (A2 - A1) - Sv * mx * (B2 - B1));
-      maps[(1 * 3 + ch) * plane + oi] = -Sv * B1 * inv_d;
-      maps[(2 * 3 + ch) * plane + oi] = 2.f * A1 * inv_d;
+      const unsigned oi = (unsigned)(orow * Wo + ocol) * 4u;
+      const Rsrc mp = rsrc(maps, (size_t)plane * 36);
+      bst(mp, oi, ch * plane * 4u, 2.f * inv_d * (my * (A2 - A1) - Sv * mx * (B2 - B1)));
+      bst(mp, oi, (3 + ch) * plane * 4u, -Sv * B1 * inv_d);
+      bst(mp, oi, (6 + ch) * plane * 4u, 2.f * A1 * inv_d);
       ssum += Sv;
     }
   }
@@ -167,7 +186,8 @@ __global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
 __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
                                                    const float* __restrict__ y, int H, int W,
                                                    Taps taps, const float* __restrict__ maps,
-                                                   float lambda, float* __restrict__ gout,
+                                                   float lambda, float inv_n, float inv_ns,
+                                                   float* __restrict__ gout,
                                                    float* __restrict__ partials) {
   const int Ho = H - kHalo, Wo = W - kHalo;
   const TileItem it = tile_item((W + kTW - 1) / kTW, (H + kTH - 1) / kTH);
@@ -176,41 +196,45 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
   __shared__ float v[3][kTH][kRW + 1];
   __shared__ float s_ftmp[4];
   const int tid = threadIdx.x;
-  const int64_t plane = (int64_t)Ho * Wo;
-  // map rows [iy0-10, iy0+16), cols [ix0-10, ix0+32); zero outside the valid map
+  const unsigned plane = (unsigned)(Ho * Wo);
+  const int lane = tid & 63, wv = wave_id();
+  // map rows [iy0-10, iy0+16), cols [ix0-10, ix0+32); zero outside the valid map.
+  // lane = column, wave w takes rows w, w+4, ...
   {
-    constexpr int kPer = (kRH * kRW + 255) / 256;
-    float mv[3][kPer];
+    constexpr int NI = (kRH + 3) / 4;
+    const Rsrc ms = rsrc(maps, (size_t)plane * 36);
+    const int mc = ix0 - kHalo + lane;
+    const unsigned coff = (unsigned)min(max(mc, 0), Wo - 1) * 4u;
+    float mv[3][NI];
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {  // every load in flight before any is used
-      const int i = min(tid + 256 * k, kRH * kRW - 1);
-      const int mr = min(max(iy0 - kHalo + i / kRW, 0), Ho - 1);
-      const int mc = min(max(ix0 - kHalo + i % kRW, 0), Wo - 1);
-      const int64_t o = (int64_t)mr * Wo + mc;
+    for (int i = 0; i < NI; ++i) {  // every load in flight before any is used
+      const int mr = min(max(iy0 - kHalo + wv + 4 * i, 0), Ho - 1);
 #pragma unroll
-      for (int m = 0; m < 3; ++m) mv[m][k] = maps[(m * 3 + ch) * plane + o];
+      for (int m = 0; m < 3; ++m)
+        mv[m][i] = bld(ms, coff, ((unsigned)(m * 3 + ch) * plane + (unsigned)(mr * Wo)) * 4u);
     }
+    const bool col_ok = lane < kRW && mc >= 0 && mc < Wo;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = tid + 256 * k;
-      if (i < kRH * kRW) {
-        const int r = i / kRW, c = i % kRW;
-        const int mr = iy0 - kHalo + r, mc = ix0 - kHalo + c;
-        const bool ok = mr >= 0 && mr < Ho && mc >= 0 && mc < Wo;
+    for (int i = 0; i < NI; ++i) {
+      const int r = wv + 4 * i, mr = iy0 - kHalo + r;
+      if (r < kRH && lane < kRW) {
+        const bool ok = col_ok && mr >= 0 && mr < Ho;
 #pragma unroll
-        for (int m = 0; m < 3; ++m) sm[m][r][c] = ok ? mv[m][k] : 0.f;
+        for (int m = 0; m < 3; ++m) sm[m][r][lane] = ok ? mv[m][i] : 0.f;
       }
     }
   }
   // this thread's pixels (loaded ahead of the filtering)
   const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
   const int gr = iy0 + r;
+  const Rsrc xs = rsrc(x, (size_t)H * W * 12), ys = rsrc(y, (size_t)H * W * 12);
+  const unsigned roff = (unsigned)(min(gr, H - 1) * W) * 12u;  // per lane: 4 rows per wave
   float xv[kHCols], yv[kHCols];
 #pragma unroll
   for (int o = 0; o < kHCols; ++o) {
-    const int64_t pi = ((int64_t)min(gr, H - 1) * W + min(ix0 + c0 + o, W - 1)) * 3 + ch;
-    xv[o] = x[pi];
-    yv[o] = y[pi];
+    const unsigned po = ((unsigned)min(ix0 + c0 + o, W - 1) * 3u + (unsigned)ch) * 4u;
+    xv[o] = bld(xs, roff + po, 0);
+    yv[o] = bld(ys, roff + po, 0);
   }
   __syncthreads();
   // transposed vertical: input row r receives sum_k g[k] * map[r + 10 - k]
@@ -262,21 +286,20 @@ __global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
       }
     }
   }
-  const float inv_n = 1.0f / (3.0f * (float)H * (float)W);
-  const float inv_ns = 1.0f / (3.0f * (float)Ho * (float)Wo);
+  const Rsrc gs_out = rsrc(gout, (size_t)H * W * 12);
   float l1sum = 0.0f;
 #pragma unroll
   for (int o = 0; o < kHCols; ++o) {
     const int gc = ix0 + c0 + o;
     if (gr < H && gc < W) {
-      const int64_t pi = ((int64_t)gr * W + gc) * 3 + ch;
       const float xr = xv[o], yr = yv[o];
       const float d = xr - yr;
       const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
       const bool pass = xr >= 0.f && xr <= 1.f;
       const float gs = pass ? (t[0][o] + 2.f * clamp01(xr) * t[1][o] + clamp01(yr) * t[2][o]) * inv_ns
                             : 0.f;
-      gout[pi] = (1.f - lambda) * sgn * inv_n - lambda * gs;
+      bst(gs_out, roff + ((unsigned)gc * 3u + (unsigned)ch) * 4u, 0,
+          (1.f - lambda) * sgn * inv_n - lambda * gs);
       l1sum += fabsf(d);
     }
   }
@@ -330,13 +353,17 @@ int tts_loss_grad(const float* image, const float* target, int H, int W, float l
                   hipStream_t stream) {
   if (!image || !target || !gimage) return TTS_EINVAL;
   if (H < kWin || W < kWin) return TTS_EINVAL;
+  // buffer resources take 32-bit sizes: the 9 map planes (the largest buffer) stay below 2^31 B
+  if ((int64_t)H * W * 36 > INT32_MAX) return TTS_EINVAL;
   if (!workspace || workspace_bytes < tts_loss_workspace_bytes(H, W)) return TTS_EWORKSPACE;
   const Taps taps = make_taps();
   const int gm = maps_grid(H, W), gg = grad_grid(H, W);
+  const float inv_n = 1.0f / (3.0f * (float)H * (float)W);
+  const float inv_ns = 1.0f / (3.0f * (float)(H - kHalo) * (float)(W - kHalo));
   float* maps = static_cast<float*>(workspace);
   k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, H, W, taps, maps, partials);
-  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, gimage,
-                                      partials ? partials + gm : nullptr);
+  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, inv_n, inv_ns,
+                                      gimage, partials ? partials + gm : nullptr);
   return launch_status();
 }
 
