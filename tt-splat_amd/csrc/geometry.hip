@@ -358,18 +358,47 @@ __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
 // row from LDS.  Direct row-per-thread accesses would make every wave instruction touch ~28
 // cache lines 56 bytes apart, which the L1 address path, not HBM, turns into the limit.  LDS
 // rows are padded to an odd stride, so the per-thread row reads are free of bank conflicts.
+// The copy has a fixed trip count (W words per thread; the ragged last block clamps its loads
+// and masks its writes), so all of a thread's loads are in flight before the first LDS write:
+// a loop bounded by rows * W would wait out one memory round trip per word.
 constexpr int kGeoBlock = 256;
+template <int W, typename T>
+__device__ __forceinline__ void stage_load(const T* __restrict__ src, int g0, int rows, T (&r)[W]) {
+  const T* base = src + (int64_t)g0 * W;
+  const int last = rows * W - 1;
+#pragma unroll
+  for (int k = 0; k < W; ++k) r[k] = base[min((int)threadIdx.x + k * kGeoBlock, last)];
+}
+template <int W, int SW, typename T>
+__device__ __forceinline__ void stage_put(const T (&r)[W], int rows, T* s) {
+  const int n = rows * W;
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int i = threadIdx.x + k * kGeoBlock;
+    if (i < n) s[(i / W) * SW + i % W] = r[k];
+  }
+}
 template <int W, int SW, typename T>
 __device__ __forceinline__ void stage_in(const T* __restrict__ src, int g0, int rows, T* s) {
-  const T* base = src + (int64_t)g0 * W;
-  const int n = rows * W;
-  for (int i = threadIdx.x; i < n; i += kGeoBlock) s[(i / W) * SW + i % W] = base[i];
+  T r[W];
+  stage_load<W>(src, g0, rows, r);
+  stage_put<W, SW>(r, rows, s);
 }
 template <int W, int SW, typename T>
 __device__ __forceinline__ void stage_out(T* __restrict__ dst, int g0, int rows, const T* s) {
   T* base = dst + (int64_t)g0 * W;
   const int n = rows * W;
-  for (int i = threadIdx.x; i < n; i += kGeoBlock) base[i] = s[(i / W) * SW + i % W];
+  T r[W];
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int i = min((int)threadIdx.x + k * kGeoBlock, n - 1);
+    r[k] = s[(i / W) * SW + i % W];
+  }
+#pragma unroll
+  for (int k = 0; k < W; ++k) {
+    const int i = threadIdx.x + k * kGeoBlock;
+    if (i < n) base[i] = r[k];
+  }
 }
 
 // Slot gradient sum through inverse-table entries e[9] already loaded (see gather_slot_grads):
@@ -593,10 +622,18 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
   __shared__ int s_inv[kGeoBlock * 9];
   const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
   const int g = g0 + threadIdx.x;
-  stage_in<9, 9>(inv, g0, rows, s_inv);
-  stage_in<14, 15>(params, g0, rows, s_p);
-  stage_in<14, 15>(m, g0, rows, s_m);
-  stage_in<14, 15>(v, g0, rows, s_v);
+  {  // all four row copies in flight at once
+    int ri[9];
+    float rp[14], rm[14], rv[14];
+    stage_load<9>(inv, g0, rows, ri);
+    stage_load<14>(params, g0, rows, rp);
+    stage_load<14>(m, g0, rows, rm);
+    stage_load<14>(v, g0, rows, rv);
+    stage_put<9, 9>(ri, rows, s_inv);
+    stage_put<14, 15>(rp, rows, s_p);
+    stage_put<14, 15>(rm, rows, s_m);
+    stage_put<14, 15>(rv, rows, s_v);
+  }
   __syncthreads();
   if ((int)threadIdx.x < rows) {
   const int t = threadIdx.x;
