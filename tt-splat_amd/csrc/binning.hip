@@ -251,25 +251,24 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
   // far ranks inside the wave's range: per round, lanes of one cell are grouped by ballots
   // (registers only); each group's leader then adds the group to the wave's running count of
   // the cell with one LDS atomic, and the lanes take the returned base from their leader.
+  // The group of a lane is matched on the bits of its border index b: one ballot per bit, so
+  // the cost does not grow with the number of distinct far cells in the round.
   if (NB > 0) {
     int* wrun = s_wrun + wave * NB;
+    const int nbits = 32 - __clz(max(NB - 1, 1));  // b < NB fits in nbits bits
 #pragma unroll
     for (int i = 0; i < kCountPerLane; ++i) {
       const bool far = farv[i];
       const int b = far ? border_index(cell[i] % ntx, cell[i] / ntx, ntx, nty) : -1;
-      unsigned long long pending = __ballot(far);
-      int rw = 0, ldr = lane, cnt = 0;
-      while (pending) {  // one pass per distinct far cell in the round
-        const int leader = first_lane(pending);
-        const int bl = read_lane(b, leader);
-        const unsigned long long m = __ballot(b == bl);
-        if (b == bl) {
-          rw = __popcll(m & __lanemask_lt());
-          ldr = leader;
-          cnt = __popcll(m);
-        }
-        pending &= ~m;
+      unsigned long long m = __ballot(far);  // far lanes with every bit of b equal to this lane's
+      for (int k = 0; k < nbits; ++k) {
+        const bool bit = (b >> k) & 1;
+        const unsigned long long bk = __ballot(far && bit);
+        m &= bit ? bk : ~bk;
       }
+      const int rw = __popcll(m & __lanemask_lt());
+      const int cnt = __popcll(m);
+      const int ldr = far ? first_lane(m) : lane;
       int base = 0;
       if (far && ldr == lane) base = atomicAdd(&wrun[b], cnt);
       base = __shfl(base, ldr);

@@ -33,14 +33,18 @@ __device__ __forceinline__ long long f2i64_x86(float f) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Wave64 inclusive prefix sum of an int.
+// Wave64 inclusive prefix sum of an int, on DPP lane moves (VALU only; a shuffle would take six
+// dependent LDS-crossbar round trips): Hillis-Steele inside each row of 16 lanes (row_shr 1, 2,
+// 4, 8, lanes shifted in from outside the row read 0), then lane 15 of rows 0 and 2 is added
+// into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31).  DPP reads
+// the neighbour lanes' registers whatever their exec bit: all 64 lanes of the wave must call.
 __device__ __forceinline__ int wave_incl_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    int o = __shfl_up(v, d, 64);
-    if (lane >= d) v += o;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 
