@@ -365,10 +365,9 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
                                                    int* __restrict__ nlist,
                                                    int32_t* __restrict__ order) {
   __shared__ int s_v[2][kScanChunk];
-  __shared__ int s_tmp[2][16];
+  __shared__ int s_tmp[32];
   __shared__ int s_n[kScanChunk];     // fused: cell totals, then their row 3-sums
   __shared__ int s_bins[kMaxK + 2];   // fused: counting-sort buckets
-  __shared__ int s_cnt[2];            // fused: heavy / light list lengths
   const int T = ntx * nty;
   if (fuse) {
     // ---- T <= kScanChunk: counts, starts and the tile classification all in LDS ----
@@ -382,7 +381,6 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
       reg_cnt[i] = 0;
       far_cnt[i] = 0;
     }
-    if (threadIdx.x < 2) s_cnt[threadIdx.x] = 0;
     for (int c = threadIdx.x; c <= K + 1; c += 1024) s_bins[c] = 0;
     __syncthreads();
     // thread = tiles [lo, lo + per): its partial sums of both counts, and the row 3-sums of the
@@ -402,9 +400,8 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
         hs[k] = s_n[t] + (tx > 0 ? s_n[t - 1] : 0) + (tx + 1 < ntx ? s_n[t + 1] : 0);
       }
     }
-    int tr, tf;
-    int er = block_excl_scan<1024>(sr, s_tmp[0], &tr);  // barriers: every LDS read above is done
-    int ef = block_excl_scan<1024>(sf, s_tmp[1], &tf);
+    int tr, tf, er, ef;  // barriers inside: every LDS read above is done
+    block_excl_scan2<1024>(sr, sf, s_tmp, &er, &ef, &tr, &tf);
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int t = lo + k;
@@ -426,44 +423,51 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
       cell_start[T] = tr;
       far_start[T] = tf;
     }
-    // classification: candidates <= K -> light, else heavy (heavy listed first); the kept count
-    // every tile ends with, min(candidates, K), keys the heaviest-first order
+    // classification: candidates <= K -> light, else heavy.  Each thread takes its contiguous
+    // tiles [lo, lo + per) again, and one block scan of its packed counts (heavy << 16 | light,
+    // totals <= 8192) places them: heavy tiles to lists[0, ...), light ones to lists[T-1],
+    // lists[T-2], ..., both in ascending tile order.  The kept count every tile ends with,
+    // min(candidates, K), keys the heaviest-first order (histogram here, placement below).
     int ncs[kPer];
+    int nh = 0, nlt = 0;
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      ncs[k] = 0;
-      if (k * 1024 < T) {  // uniform: wave-aggregated appends inside
-        const int t = k * 1024 + threadIdx.x;
-        int nc = 0;
-        if (t < T) {
-          const int ty = t / ntx;
-          nc = s_n[t] + (ty > 0 ? s_n[t - ntx] : 0) + (ty + 1 < nty ? s_n[t + ntx] : 0);
-        }
+      const int t = lo + k;
+      ncs[k] = -1;
+      if (k < per && t < T) {
+        const int ty = t / ntx;
+        const int nc = s_n[t] + (ty > 0 ? s_n[t - ntx] : 0) + (ty + 1 < nty ? s_n[t + ntx] : 0);
         ncs[k] = nc;
-        const int ph = wave_append(&s_cnt[0], t < T && nc > K);
-        if (ph >= 0) lists[ph] = t;
-        const int pl = wave_append(&s_cnt[1], t < T && nc <= K);
-        if (pl >= 0) lists[T - 1 - pl] = t;
-        if (order && t < T) agg_inc(s_bins, K - min(nc, K));
+        nh += nc > K;
+        nlt += nc <= K;
+        if (order) agg_inc(s_bins, K - min(nc, K));
       }
     }
-    __syncthreads();
+    int tot;
+    const int ex = block_excl_scan<1024>((nh << 16) | nlt, s_tmp, &tot);
+    int ph = ex >> 16, pl = ex & 0xffff;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      if (ncs[k] >= 0) {
+        const int t = lo + k;
+        if (ncs[k] > K) lists[ph++] = t;
+        else lists[T - 1 - pl++] = t;
+      }
+    }
     if (threadIdx.x == 0) {
-      nlist[0] = s_cnt[0];
-      nlist[1] = s_cnt[1];
+      nlist[0] = tot >> 16;
+      nlist[1] = tot & 0xffff;
     }
     if (!order) return;
     // K + 1 <= 513 buckets: one per thread
     const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
     int total;
-    const int ex = block_excl_scan<1024>(v, s_tmp[0], &total);
-    if (threadIdx.x <= K) s_bins[threadIdx.x] = ex;
+    const int bx = block_excl_scan<1024>(v, s_tmp, &total);
+    if (threadIdx.x <= K) s_bins[threadIdx.x] = bx;
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int t = k * 1024 + threadIdx.x;
-      if (k * 1024 < T && t < T) order[agg_inc(s_bins, K - min(ncs[k], K))] = t;
-    }
+    for (int k = 0; k < kPer; ++k)
+      if (ncs[k] >= 0) order[agg_inc(s_bins, K - min(ncs[k], K))] = lo + k;
     return;
   }
   // ---- larger grids: chunked scans; k_tile_classify / k_tile_order run separately ----
@@ -485,7 +489,7 @@ __global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
       for (int k = 0; k < per; ++k)
         if (lo + k < n) sum += s_v[w][lo + k];
       int total;
-      int ex = block_excl_scan<1024>(sum, s_tmp[w], &total) + carry[w];
+      int ex = block_excl_scan<1024>(sum, s_tmp + 16 * w, &total) + carry[w];
       for (int k = 0; k < per; ++k) {
         if (lo + k < n) {
           const int v = s_v[w][lo + k];

@@ -70,6 +70,37 @@ __device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total) {
   return base + incl - v;
 }
 
+// Two independent block-wide exclusive prefix sums under one pair of barriers.  `tmp` holds
+// 2 * NT/64 ints.
+template <int NT>
+__device__ __forceinline__ void block_excl_scan2(int a, int b, int* tmp, int* ea, int* eb,
+                                                 int* ta, int* tb) {
+  constexpr int NW = NT / 64;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ia = wave_incl_scan(a), ib = wave_incl_scan(b);
+  if (lane == 63) {
+    tmp[wave] = ia;
+    tmp[NW + wave] = ib;
+  }
+  __syncthreads();
+  int ba = 0, bb = 0, sa = 0, sb = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const int xa = tmp[w], xb = tmp[NW + w];
+    if (w < wave) {
+      ba += xa;
+      bb += xb;
+    }
+    sa += xa;
+    sb += xb;
+  }
+  __syncthreads();
+  *ea = ba + ia - a;
+  *eb = bb + ib - b;
+  *ta = sa;
+  *tb = sb;
+}
+
 __device__ __forceinline__ int block_excl_scan256(int v, int* tmp, int* total) {
   return block_excl_scan<256>(v, tmp, total);
 }
