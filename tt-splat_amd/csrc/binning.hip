@@ -248,6 +248,20 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
     for (int i = 0; i < kCountPerLane; ++i)
       if (cell[i] >= 0 && !farv[i]) rank[i] = atomicAdd(&reg_cnt[cell[i]], 1);
   }
+  // REG_LDS: once the block's regular counts are final, one global atomic per touched cell
+  // (at most kCountBlock of them, two per thread) takes the block's base in the cell.  They are
+  // issued here and their results used only after the far ranks, which they do not touch, so
+  // the round trip overlaps that work.
+  static_assert(kCountBlock <= 2 * 256, "two touched cells per thread");
+  int tc0 = -1, tc1 = -1, tb0, tb1;  // tbK is set and read only when tcK >= 0
+  if (REG_LDS) {
+    __syncthreads();
+    const int nt = s_ntouched;
+    if ((int)threadIdx.x < nt) tc0 = s_touched[threadIdx.x];
+    if ((int)threadIdx.x + 256 < nt) tc1 = s_touched[threadIdx.x + 256];
+    if (tc0 >= 0) tb0 = atomicAdd(&reg_cnt[tc0], s_reg[tc0]);
+    if (tc1 >= 0) tb1 = atomicAdd(&reg_cnt[tc1], s_reg[tc1]);
+  }
   // far ranks inside the wave's range: per round, lanes of one cell are grouped by ballots
   // (registers only); each group's leader then adds the group to the wave's running count of
   // the cell with one LDS atomic, and the lanes take the returned base from their leader.
@@ -294,24 +308,9 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
           s_wrun[b] + s_wrun[NB + b] + s_wrun[2 * NB + b] + s_wrun[3 * NB + b];
   }
   if (REG_LDS) {
-    // one global atomic per touched cell, several in flight per thread
-    const int nt = s_ntouched;
-    for (int b0 = threadIdx.x; b0 < nt; b0 += 4 * 256) {
-      int c[4], h[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int e = b0 + k * 256;
-        c[k] = e < nt ? s_touched[e] : -1;
-        h[k] = c[k] >= 0 ? s_reg[c[k]] : 0;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (c[k] >= 0) h[k] = atomicAdd(&reg_cnt[c[k]], h[k]);
-      // each touched cell is listed once: this thread alone reads and rewrites its entry
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (c[k] >= 0) s_reg[c[k]] = h[k];
-    }
+    // each touched cell is listed once: this thread alone rewrites its entry with the base
+    if (tc0 >= 0) s_reg[tc0] = tb0;
+    if (tc1 >= 0) s_reg[tc1] = tb1;
     __syncthreads();
   }
 #pragma unroll
