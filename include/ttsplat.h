@@ -43,7 +43,7 @@ extern "C" {
 #endif
 
 #define TTS_OK 0
-#define TTS_EINVAL (-1)     /* null pointer or non-positive size */
+#define TTS_EINVAL (-1)     /* null pointer, non-positive size, or a size over an entry's limit */
 #define TTS_ETILE (-2)      /* S not in {16,32}, or H/W not a multiple of S */
 #define TTS_EK (-3)         /* K outside [1, 512] */
 #define TTS_EWORKSPACE (-4) /* workspace missing or too small */

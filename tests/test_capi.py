@@ -85,6 +85,16 @@ def test_splat_rejects_bad_tile(lib):
     assert lib.tts_loss_grad(p, p, 64, 64, 0.2, p, None, None, 0, None) == -4
 
 
+def test_loss_grad_size_limit(lib):
+    """The loss kernels address with 32-bit buffer offsets: images whose nine map planes
+    (H*W*36 bytes) exceed 2^31-1 are refused before launch; 7680x4320 passes the check (and
+    then stops at the missing workspace)."""
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    assert lib.tts_loss_grad(p, p, 8000, 8000, 0.2, p, None, None, 0, None) == -1
+    assert lib.tts_loss_grad(p, p, 4320, 7680, 0.2, p, None, None, 0, None) == -4
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from ttsplat import _lib
     monkeypatch.setattr(_lib, "_lib", None)
