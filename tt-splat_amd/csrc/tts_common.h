@@ -162,10 +162,21 @@ __device__ __forceinline__ void normals3(const Philox4& p, float* z) {
   z[2] = r1 * c1;
 }
 
+// Wave64 float sum on the DPP pattern of wave_incl_scan (lane 63 ends with the total, a fixed
+// summation order), broadcast from lane 63.  All 64 lanes of the wave must call.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false);
+  return v + __builtin_bit_cast(float, o);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-  return v;
+  v = dpp_add<0x111, 0xf>(v);  // row_shr:1
+  v = dpp_add<0x112, 0xf>(v);  // row_shr:2
+  v = dpp_add<0x114, 0xf>(v);  // row_shr:4
+  v = dpp_add<0x118, 0xf>(v);  // row_shr:8
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast:15
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast:31
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 // Block-wide float sum for blockDim.x == 256; result valid in every thread.
