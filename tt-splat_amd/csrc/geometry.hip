@@ -402,29 +402,40 @@ __device__ __forceinline__ void stage_out(T* __restrict__ dst, int g0, int rows,
 }
 
 // Slot gradient sum through inverse-table entries e[9] already loaded (see gather_slot_grads):
-// each 36-byte record is read as two 16-byte and one 4-byte load.
+// each 36-byte record is read as two 16-byte and one 4-byte load.  Split in two so a caller can
+// put independent work between the loads (slot_loads) and their first use (slot_sum).
 typedef float f4u __attribute__((ext_vector_type(4), aligned(4)));
-__device__ __forceinline__ void gather_slots(const float* __restrict__ gslot, const int* e,
-                                             float* gin) {
+struct SlotRecs {
   f4u a[9], b[9];
   float c[9];
+};
+__device__ __forceinline__ void slot_loads(const float* __restrict__ gslot, const int* e,
+                                           SlotRecs& r) {
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
     const float* src = gslot + (int64_t)(e[j] >= 0 ? e[j] : 0) * 9;
-    a[j] = *reinterpret_cast<const f4u*>(src);
-    b[j] = *reinterpret_cast<const f4u*>(src + 4);
-    c[j] = src[8];
+    r.a[j] = *reinterpret_cast<const f4u*>(src);
+    r.b[j] = *reinterpret_cast<const f4u*>(src + 4);
+    r.c[j] = src[8];
   }
+}
+__device__ __forceinline__ void slot_sum(const int* e, const SlotRecs& r, float* gin) {
 #pragma unroll
   for (int k = 0; k < 9; ++k) gin[k] = 0.0f;
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
     if (e[j] >= 0) {
-      gin[0] += a[j].x; gin[1] += a[j].y; gin[2] += a[j].z; gin[3] += a[j].w;
-      gin[4] += b[j].x; gin[5] += b[j].y; gin[6] += b[j].z; gin[7] += b[j].w;
-      gin[8] += c[j];
+      gin[0] += r.a[j].x; gin[1] += r.a[j].y; gin[2] += r.a[j].z; gin[3] += r.a[j].w;
+      gin[4] += r.b[j].x; gin[5] += r.b[j].y; gin[6] += r.b[j].z; gin[7] += r.b[j].w;
+      gin[8] += r.c[j];
     }
   }
+}
+__device__ __forceinline__ void gather_slots(const float* __restrict__ gslot, const int* e,
+                                             float* gin) {
+  SlotRecs r;
+  slot_loads(gslot, e, r);
+  slot_sum(e, r, gin);
 }
 
 // Adam step block: step[0] int32 step number; step[1..2] fp32 1/bc1 and 1/sqrt(bc2) for that
@@ -641,7 +652,8 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
 #pragma unroll
   for (int j = 0; j < 9; ++j) e[j] = s_inv[t * 9 + j];
   float gin[9], gout[14], gcol[3];
-  gather_slots(gslot, e, gin);
+  SlotRecs recs;
+  slot_loads(gslot, e, recs);  // in flight during the forward recompute below
   float pl[14], mm[14], vv[14];
 #pragma unroll
   for (int i = 0; i < 14; ++i) {
@@ -660,6 +672,7 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
     sh_apply(pl, b, rv, n_rest, s);
   }
   float gdw[2];
+  slot_sum(e, recs, gin);
   geo_backward(pl, cam, s, gin, gout, gcol, gdw, dwa.zgrad != 0);
   depthw_store(dwa, g, gdw);
   if (MC) reg_add(pl, mc.reg_o, mc.reg_s, gout);
