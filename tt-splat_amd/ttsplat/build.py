@@ -8,6 +8,8 @@ Flags
   -Xclang -target-feature -Xclang -packed-fp32-ops
                                    no packed-FP32 (v_pk_*_f32) codegen
   -ffp-contract=off (binning.hip)  binning keys are products and sums rounded one by one
+  -mllvm -amdgpu-mfma-vgpr-form (splat.hip)
+                                   matrix-core results in VGPRs, not accumulator registers
 """
 import concurrent.futures as cf
 import os
@@ -26,7 +28,9 @@ OBJ_DIR = os.path.join(ROOT, "_build")
 COMMON = ["-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           "-Wno-unused-command-line-argument", "-I", INCLUDE, "-I", CSRC]
-PER_FILE = {"binning.hip": ["-ffp-contract=off"]}
+PER_FILE = {"binning.hip": ["-ffp-contract=off"],
+            # matrix-core results straight into VGPRs (no accumulator-register copies)
+            "splat.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc():
