@@ -43,18 +43,22 @@ __device__ __forceinline__ SlotLDS carve_slots(unsigned char* base, int K) {
 
 __device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (3 * 16 + 8); }
 
-// Tile-local theta_u for one gaussian record (tools/m4_train_binned.py:130-143).
-__device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
-                                           float oy, float inv_k, float4& ta, float4& tb,
-                                           float4& cl) {
-  const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
-  const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+// Tile-local theta_u for one gaussian record r0..r2 of proj (tools/m4_train_binned.py:130-143).
+__device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, const float4 r2,
+                                              float ox, float oy, float inv_k, float4& ta,
+                                              float4& tb, float4& cl) {
   const float a = r0.z, b = r0.w, c = r1.x;
   const float mx = r0.x - ox, my = r0.y - oy;
   const float Q0 = a * mx * mx + 2.0f * b * mx * my + c * my * my;
   ta = make_float4(-a * inv_k, -c * inv_k, -2.0f * b * inv_k, 2.0f * (a * mx + b * my) * inv_k);
   tb = make_float4(2.0f * (b * mx + c * my) * inv_k, 1.0f - Q0 * inv_k, 0.0f, 0.0f);
   cl = make_float4(r1.z, r1.w, r2.x, r2.y);
+}
+__device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
+                                           float oy, float inv_k, float4& ta, float4& tb,
+                                           float4& cl) {
+  const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+  slot_from_rec(r[0], r[1], r[2], ox, oy, inv_k, ta, tb, cl);
 }
 
 // Compact the tile's valid slots into LDS in slot order.  Returns the valid count.
@@ -63,16 +67,28 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
                                                const uint8_t* __restrict__ valid, int t, int K,
                                                float ox, float oy, float inv_k, SlotLDS sl,
                                                int* s_tmp) {
+  // idx is read beside valid (every slot's entry is written; an invalid one is not used), and a
+  // valid slot's proj record is requested before the compaction scan, whose barriers then
+  // overlap that round trip
   int base = 0;
   for (int s0 = 0; s0 < K; s0 += 256) {
     const int s = s0 + threadIdx.x;
-    const int v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
+    const int64_t ts = (int64_t)t * K + min(s, K - 1);
+    const uint8_t vb = valid[ts];  // both loads unconditional: in flight together
+    const int g = idx[ts];
+    const int v = (s < K && vb != 0) ? 1 : 0;
+    float4 r0, r1, r2;
+    if (v) {
+      const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+      r0 = r[0];
+      r1 = r[1];
+      r2 = r[2];
+    }
     int total;
     const int pos = base + block_excl_scan256(v, s_tmp, &total);
     if (v) {
-      const int g = idx[(int64_t)t * K + s];
       float4 ta, tb, cl;
-      build_slot(proj, g, ox, oy, inv_k, ta, tb, cl);
+      slot_from_rec(r0, r1, r2, ox, oy, inv_k, ta, tb, cl);
       sl.ta[pos] = ta;
       sl.tb[pos] = tb;
       sl.cl[pos] = cl;
