@@ -51,12 +51,16 @@ def test_c5_splat_sampled_tiles(c5):
                       device="cuda")
     th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, cfg.k)
     img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
-    # the fused kernel and the pre-gathered-operand kernel agree over the whole frame
+    # the fused kernel (u on fp32 matrix cores) and the pre-gathered-operand kernel (u on the
+    # VALU) round differently; over the whole frame they agree within the fp32 contract, and the
+    # tiles where they differ most join the sample checked against the oracle below
     img2, _ = kernels.splat_fwd_theta(th, col, oc, bg, cfg.H, cfg.W, cfg.S)
-    assert max_abs(img, img2) <= 1e-5
+    assert max_abs(img, img2) <= 1e-4
+    dif = (img - img2).abs().amax(-1).reshape(cfg.H // cfg.S, cfg.S, cfg.W // cfg.S, cfg.S)
+    worst = torch.argsort(dif.amax((1, 3)).reshape(-1), descending=True)[:8].cpu()
     g = torch.Generator().manual_seed(9)
     heavy = torch.argsort(count.cpu(), descending=True)[:24]
-    sel = torch.cat([heavy, torch.randint(0, T, (40,), generator=g)]).unique()
+    sel = torch.cat([heavy, worst, torch.randint(0, T, (40,), generator=g)]).unique()
     tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
     Phi = tmap.Phi.double()
     ths = th[sel.cuda()].cpu().double().requires_grad_(True)

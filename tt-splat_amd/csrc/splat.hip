@@ -555,19 +555,21 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
   }
 }
 
-// Forward on fp32 matrix cores (S = 16, slots from proj).  For each chunk of 16 slots and each
-// pixel row, u for 16 slots x 16 pixels is one v_mfma_f32_16x16x4f32 pair over depth 8 (the six
-// monomials lx^2, ly^2, lx*ly, lx, ly, 1 and two zeros); w = relu(u)^2 and the colour / density
-// sums stay on the VALU (6 instructions per pair instead of 12 when u is formed there too), while
-// the matrix cores work beside them.  Lane layout of the instruction (checked on gfx950):
-// A[i][k] in lane i + 16k, B[k][j] in lane j + 16k, D[i][j] in lane j + 16*(i/4), element i % 4.
-// Slots run along i and the row's pixels along j, so lane (q, j) holds the u of slots 4q..4q+3 of
-// the chunk at pixel j and adds their contributions itself; the four lane groups' partial sums
-// meet in LDS at the end.  Padding slots of the last chunk are zero (u = 0, w = 0).
-constexpr int kMfRows = 4;  // pixel rows per wave (4 waves x 4 rows = the 16-row tile)
+// Forward on fp32 matrix cores (S = 16, slots from proj).  Along one pixel row (ly fixed) the
+// quadratic form is a quadratic in lx alone:
+//   u = theta0 lx^2 + (theta2 ly + theta3) lx + (theta1 ly^2 + theta4 ly + theta5),
+// so one v_mfma_f32_16x16x4f32 evaluates it for 4 pixel rows x 4 slots (the 16 A rows, i = 4 row
+// + slot) against the 16 pixels of a row (B columns: lx^2, lx, 1, 0).  Lane layout of the
+// instruction (checked on gfx950): A[i][k] in lane i + 16k, B[k][j] in lane j + 16k, D[i][j] in
+// lane j + 16*(i/4), element i % 4 -- so lane (q, j) receives u of its own pixel (row q of the
+// wave's four, column j) for the group's four slots and sums them without any cross-lane step.
+// Each A entry is (p ly + q) ly + r with (p, q, r) per (slot, depth k) staged in LDS:
+// k = 0: (0, 0, theta0), k = 1: (0, theta2, theta3), k = 2: (theta1, theta4, theta5), k = 3: 0.
+// The VALU keeps relu^2 and the colour / density sums (6 instructions per pair, 2 more per
+// 256 pairs for A); padding slots of the last group are zero (u = 0, w = 0).
 inline size_t fwd_mf_lds(int K) {
-  const int k16 = (K + 15) & ~15;
-  return (size_t)k16 * (3 * 16 + 8) + (size_t)4 * kMfRows * 4 * 64 * sizeof(float);
+  const int k4 = (K + 3) & ~3;
+  return (size_t)k4 * 5 * sizeof(float4);
 }
 __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
@@ -576,87 +578,89 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     float* __restrict__ den_out) {
   extern __shared__ unsigned char s_dyn[];
   __shared__ int s_tmp[4];
-  const int k16 = (K + 15) & ~15;
-  const SlotLDS sl = carve_slots(s_dyn, k16);
-  float* s_part = reinterpret_cast<float*>(s_dyn + slot_lds_bytes(k16));  // [wave][row*4+ch][lane]
+  const int k4 = (K + 3) & ~3;
+  float4* s_coef = reinterpret_cast<float4*>(s_dyn);  // [k4][4]: (p, q, r, 0) per depth k
+  float4* s_col = s_coef + (size_t)k4 * 4;           // [k4]: col_o r, g, b, o_col
   const int t = order ? order[blockIdx.x] : blockIdx.x;
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * 16, oy = ty * 16;
-  const int n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
-  const int nch = (n + 15) >> 4;
-  for (int p = n + threadIdx.x; p < nch * 16; p += 256) {
+  const float oxf = (float)ox, oyf = (float)oy;
+  // compact the valid slots in slot order (idx beside valid; a valid slot's proj record in flight
+  // across the scan), build theta and stage the per-depth coefficients and the colours
+  int n = 0;
+  for (int s0 = 0; s0 < K; s0 += 256) {
+    const int s = s0 + threadIdx.x;
+    const int64_t ts = (int64_t)t * K + min(s, K - 1);
+    const uint8_t vb = valid[ts];
+    const int g = idx[ts];
+    const int v = (s < K && vb != 0) ? 1 : 0;
+    float4 r0, r1, r2;
+    if (v) {
+      const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+      r0 = r[0];
+      r1 = r[1];
+      r2 = r[2];
+    }
+    int total;
+    const int pos = n + block_excl_scan256(v, s_tmp, &total);
+    if (v) {
+      float4 ta, tb, cl;
+      slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
+      float4* c = s_coef + (size_t)pos * 4;
+      c[0] = make_float4(0.f, 0.f, ta.x, 0.f);
+      c[1] = make_float4(0.f, ta.z, ta.w, 0.f);
+      c[2] = make_float4(ta.y, tb.x, tb.y, 0.f);
+      c[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_col[pos] = cl;
+    }
+    n += total;
+  }
+  const int ngrp = (n + 3) >> 2;
+  for (int p = n + (int)threadIdx.x; p < ngrp * 4; p += 256) {  // at most 3 padding slots
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    sl.ta[p] = z;
-    sl.tb[p] = z;
-    sl.cl[p] = z;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_coef[(size_t)p * 4 + k] = z;
+    s_col[p] = z;
   }
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
-  // B operands: depth q of pixel (j, row): b0 = (lx^2, ly^2, lx*ly, lx)[q], b1 = (ly, 1, 0, 0)[q]
+  // A side of this lane: row (lane >> 2) & 3 of the wave, slot lane & 3 of a group, depth q
+  const float ly_a = (float)(4 * wave + ((lane >> 2) & 3)) + 0.5f;
+  const int a_off = (lane & 3) * 4 + q;  // float4 index inside a group's coefficients
+  // B side: pixel column j at depth q: (lx^2, lx, 1, 0)[q]
   const float lx = (float)j + 0.5f;
-  float b0[kMfRows], b1[kMfRows];
-#pragma unroll
-  for (int r = 0; r < kMfRows; ++r) {
-    const float ly = (float)(kMfRows * wave + r) + 0.5f;
-    b0[r] = q == 0 ? lx * lx : (q == 1 ? ly * ly : (q == 2 ? lx * ly : lx));
-    b1[r] = q == 0 ? ly : (q == 1 ? 1.0f : 0.0f);
-  }
-  const float* s_ta = reinterpret_cast<const float*>(sl.ta);  // theta 0..3 of each slot
-  const float* s_tb = reinterpret_cast<const float*>(sl.tb);  // theta 4, 5, 0, 0
-  float acc[kMfRows][4];
-#pragma unroll
-  for (int r = 0; r < kMfRows; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[r][c] = 0.0f;
+  const float bq = q == 0 ? lx * lx : (q == 1 ? lx : (q == 2 ? 1.0f : 0.0f));
+  float ar = 0.f, ag = 0.f, ab = 0.f, ad = 0.f;
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < nch; ++c) {
-    const int sa = c * 16 + j;  // the A row (slot) this lane supplies
-    const float a0 = s_ta[sa * 4 + q], a1 = s_tb[sa * 4 + q];
-    float4 col[4];
+#pragma unroll 4
+  for (int gi = 0; gi < ngrp; ++gi) {
+    const float4 pc = s_coef[(size_t)gi * 16 + a_off];
+    const float a = fmaf(fmaf(pc.x, ly_a, pc.y), ly_a, pc.z);
+    const floatx4 u = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq, zero4, 0, 0, 0);
+    // elements copied out before their bits are reinterpreted (a bit cast applied to the
+    // vector-element expression itself compiled to element 0 for every e)
+    const float ue[4] = {u[0], u[1], u[2], u[3]};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) col[e] = sl.cl[c * 16 + 4 * q + e];
-#pragma unroll
-    for (int r = 0; r < kMfRows; ++r) {
-      floatx4 u = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0[r], zero4, 0, 0, 0);
-      u = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1[r], u, 0, 0, 0);
-      // elements copied out before their bits are reinterpreted (a bit cast applied to the
-      // vector-element expression itself compiled to element 0 for every e)
-      const float ue[4] = {u[0], u[1], u[2], u[3]};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // relu as one integer max on the bit pattern (a float max would first canonicalise the
-        // matrix-core result): u >= +0 keeps its bits, negative u becomes +0
-        const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
-        const float w = rl * rl;
-        acc[r][0] += w * col[e].x;
-        acc[r][1] += w * col[e].y;
-        acc[r][2] += w * col[e].z;
-        acc[r][3] += w * col[e].w;
-      }
+    for (int e = 0; e < 4; ++e) {
+      const float4 cl = s_col[gi * 4 + e];
+      // relu as one integer max on the bit pattern (a float max would first canonicalise the
+      // matrix-core result): u >= +0 keeps its bits, negative u becomes +0
+      const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
+      const float w = rl * rl;
+      ar += w * cl.x;
+      ag += w * cl.y;
+      ab += w * cl.z;
+      ad += w * cl.w;
     }
   }
-  // lane groups q hold disjoint slot subsets of the same pixels: sum them through LDS, then lane
-  // (q, j) finishes pixel j of the wave's row q
-  float* pw = s_part + (size_t)wave * (kMfRows * 4 * 64);
-#pragma unroll
-  for (int r = 0; r < kMfRows; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) pw[(r * 4 + c) * 64 + lane] = acc[r][c];
-  __syncthreads();
-  float v[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const float* src = pw + (q * 4 + c) * 64 + j;
-    v[c] = (src[0] + src[16]) + (src[32] + src[48]);
-  }
   const float wb = bg[0];
-  const int64_t pix = (int64_t)(oy + kMfRows * wave + q) * W + ox + j;
-  const float d = v[3] + wb;
-  image[pix * 3 + 0] = (v[0] + wb * bg[1]) / d;
-  image[pix * 3 + 1] = (v[1] + wb * bg[2]) / d;
-  image[pix * 3 + 2] = (v[2] + wb * bg[3]) / d;
+  const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
+  const float d = ad + wb;
+  image[pix * 3 + 0] = (ar + wb * bg[1]) / d;
+  image[pix * 3 + 1] = (ag + wb * bg[2]) / d;
+  image[pix * 3 + 2] = (ab + wb * bg[3]) / d;
   if (den_out) den_out[pix] = d;
 }
 
