@@ -6,7 +6,10 @@
 // Forward: the tile's valid slots are compacted into LDS as theta_u (6) and (col_o, o_col) (4);
 // each thread owns S*S/256 pixels and walks the slots:
 //     u = theta . [lx^2, ly^2, lx*ly, lx, ly, 1],  w = max(u,0)^2,  num += w*col, den += w*oc
-// and writes C = (num + w_b c_b) / (den + w_b) straight into the [H,W,3] image.
+// and writes C = (num + w_b c_b) / (den + w_b) straight into the [H,W,3] image.  For S = 16
+// from proj (tts_splat_fwd) u is formed on the fp32 matrix cores instead (k_splat_fwd_mf: per
+// pixel row u is a quadratic in lx, evaluated for 4 rows x 4 slots x 16 pixels per
+// v_mfma_f32_16x16x4f32), the rest of the walk staying on the VALU.
 //
 // Backward: per-pixel gnum = gC/den, gden = -(gC.C)/den are staged in LDS; the slots are then
 // contracted over the tile's pixels slot-parallel (TPS threads share one slot and split its
