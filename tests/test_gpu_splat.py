@@ -46,6 +46,28 @@ def test_splat_fwd_parity(name, k):
     assert max_abs(den, ex["den"]) <= 1e-4 * float(ex["den"].abs().max())
 
 
+@pytest.mark.parametrize("K", [1, 30, 61])
+def test_splat_fwd_ragged_budgets(K):
+    """Slot budgets that are not multiples of the matrix-core forward's 4-slot groups (its LDS is
+    sized from K rounded up, the padding slots zeroed), down to a single slot per tile."""
+    cfg, P, cam = config_inputs("c1_ref")
+    camera = cam.device_block("cuda")
+    proj, keep = kernels.geom_fwd(P.cuda(), camera)
+    idx, valid, count, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, K,
+                                               cfg.span)
+    assert int(count.max()) == K
+    bg = torch.tensor([float(torch.nn.functional.softplus(torch.tensor(-3.0))), 1.0, 1.0, 1.0],
+                      device="cuda")
+    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ref, ex = osplat.render_binned(P, cam_dict(cam), tmap, K=K, k=cfg.k,
+                                   bins=(idx.cpu().long(), valid.cpu().bool()), return_all=True)
+    err = max_abs(img, ref)
+    print(f"[fwd] K={K} max|err|={err:.3e}", flush=True)
+    assert err <= 1e-4
+    assert max_abs(den, ex["den"]) <= 1e-4 * float(ex["den"].abs().max())
+
+
 def test_theta_gather_matches_operands():
     cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c1_ref")
     th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, k)
