@@ -51,6 +51,7 @@ extern "C" {
 #define TTS_EG (-6)         /* G above 2^30 (2^28 for binning) */
 #define TTS_ERADIUS (-7)    /* stencil radius other than 1 */
 #define TTS_ESH (-8)        /* SH degree outside [0, 3], or rest coefficients missing */
+#define TTS_ESCRATCH (-9)   /* sizes beyond the fixed scratch of an allocation-free entry point */
 
 /* Library version, (major << 16) | minor. */
 int tts_version(void);
@@ -96,6 +97,25 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
                     int G, int H, int W, int S, int R, int K, int span,
                     int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
                     int32_t* order, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Size of the fixed device scratch behind tts_assign_bins_noalloc (40 MiB per GPU: enough for
+ * G = 2^20 gaussians on images up to 4096 x 4096 at S = 16). */
+#define TTS_BIN_SCRATCH_BYTES ((size_t)40 << 20)
+
+/* tts_assign_bins without a caller workspace and without any allocation: the binning scratch
+ * lives in a file-scope device array of TTS_BIN_SCRATCH_BYTES in the library (each GPU the
+ * library runs on holds its own copy until the process ends; its address is looked up on the
+ * first call on a device).  Same arguments, checks and results as tts_assign_bins; returns
+ * TTS_ESCRATCH when tts_bin_workspace_bytes(G, H, W, S) exceeds TTS_BIN_SCRATCH_BYTES.  The
+ * per-cell counters are cleared by a fill kernel at the start of every call, so a call does
+ * not depend on what an earlier one left.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (different streams or threads without ordering) race.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* keep,
+                            int keep_stride, int G, int H, int W, int S, int R, int K, int span,
+                            int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand,
+                            int32_t* inv, int32_t* order, hipStream_t stream);
 
 /* Tile ids ordered by kept count, heaviest first (counting sort of count[T], values in [0,K]).
  * Handing it to tts_splat_fwd / tts_splat_bwd makes the expensive tiles start first.  No

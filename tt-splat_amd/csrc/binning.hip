@@ -31,6 +31,8 @@
 //   5. k_bin_select     one block per tile (below).
 // The result does not depend on the order atomics land in.
 
+#include <mutex>
+
 #include "tts_common.h"
 
 namespace tts {
@@ -1130,11 +1132,14 @@ size_t tts_bin_workspace_bytes(int G, int H, int W, int S) {
   return bin_ws_layout(G, W / S, H / S, nullptr, nullptr);
 }
 
-int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
-                    int G, int H, int W, int S, int R, int K, int span, int32_t* idx,
-                    uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
-                    int32_t* order, void* workspace, size_t workspace_bytes,
-                    hipStream_t stream) {
+}  // extern "C"
+
+namespace tts {
+
+// Argument checks shared by both binning entry points (nothing is launched on failure).
+static int bin_check(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
+                     int G, int H, int W, int S, int R, int K, int span, const int32_t* idx,
+                     const uint8_t* valid) {
   if (G < 0 || H <= 0 || W <= 0 || !idx || !valid) return TTS_EINVAL;
   if (G > 0 && (!mu2d || !keep || mu_stride < 2 || keep_stride < 1)) return TTS_EINVAL;
   if (G > (1 << 28)) return TTS_EG;  // (j << gbits) | g must fit in 32 bits
@@ -1143,11 +1148,28 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
   if (R != 1) return TTS_ERADIUS;
   if (K < 1 || K > kMaxK) return TTS_EK;
   if (span < 1 || span > kMaxSpan) return TTS_ESPAN;
+  return TTS_OK;
+}
+
+__global__ void k_zero_i32(int* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// The binning passes on a laid-out workspace (arguments already checked).  clear_counters: the
+// per-cell counters (reg_cnt, far_cnt) are zeroed by a fill kernel first instead of being
+// trusted to be zero from the previous call.
+static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
+                   int G, int H, int W, int S, int K, int span, int32_t* idx, uint8_t* valid,
+                   int32_t* count, int32_t* ncand, int32_t* inv, int32_t* order,
+                   const BinWorkspace& ws, bool clear_counters, hipStream_t stream) {
   const int ntx = W / S, nty = H / S, T = ntx * nty;
-  if (!workspace || workspace_bytes < bin_ws_layout(G, ntx, nty, nullptr, nullptr))
-    return TTS_EWORKSPACE;
-  BinWorkspace ws;
-  bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
+  if (clear_counters) {
+    // reg_cnt and far_cnt are the first two sub-buffers: one fill covers both
+    const int n = static_cast<int>((reinterpret_cast<char*>(ws.far_cnt) -
+                                    reinterpret_cast<char*>(ws.reg_cnt)) / sizeof(int)) + T;
+    k_zero_i32<<<grid1d(n, 256), 256, 0, stream>>>(ws.reg_cnt, n);
+  }
   const float Sf = static_cast<float>(S);
   const int NB = ws.NB;
   const int nblk = ws.nblk;
@@ -1188,11 +1210,75 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
                 gbits, idx, valid, count, ncand, inv};
   k_bin_select<kSelThreads><<<T, kSelThreads, lds, stream>>>(sa, ws.lists, ws.nlist);
   // large grids: the order pass runs on the kept counts (the fused scan wrote it otherwise)
-  if (order && !fuse) {
-    if (count) k_tile_order<<<1, 1024, 0, stream>>>(count, T, K, order);
-    else return TTS_EINVAL;
-  }
+  if (order && !fuse) k_tile_order<<<1, 1024, 0, stream>>>(count, T, K, order);
   return launch_status();
+}
+
+// Fixed scratch of tts_assign_bins_noalloc: one copy per GPU, held until the process ends.
+// Host code never uses the symbol's name as an address: scratch_base() looks up each device's
+// copy once (hipGetSymbolAddress) and every launch takes that pointer.
+constexpr size_t kScratchBytes = TTS_BIN_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of the current device's scratch (looked up on the first call on that device).
+static int scratch_base(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return TTS_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return TTS_EINVAL;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return TTS_OK;
+}
+
+}  // namespace tts
+
+extern "C" {
+
+int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
+                    int G, int H, int W, int S, int R, int K, int span, int32_t* idx,
+                    uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
+                    int32_t* order, void* workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+  const int rc = bin_check(mu2d, mu_stride, keep, keep_stride, G, H, W, S, R, K, span, idx, valid);
+  if (rc != TTS_OK) return rc;
+  const int ntx = W / S, nty = H / S;
+  if (order && ntx * nty > kScanChunk && !count) return TTS_EINVAL;
+  if (!workspace || workspace_bytes < bin_ws_layout(G, ntx, nty, nullptr, nullptr))
+    return TTS_EWORKSPACE;
+  BinWorkspace ws;
+  bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
+  return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
+                 ncand, inv, order, ws, false, stream);
+}
+
+int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* keep,
+                            int keep_stride, int G, int H, int W, int S, int R, int K, int span,
+                            int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand,
+                            int32_t* inv, int32_t* order, hipStream_t stream) {
+  const int rc = bin_check(mu2d, mu_stride, keep, keep_stride, G, H, W, S, R, K, span, idx, valid);
+  if (rc != TTS_OK) return rc;
+  const int ntx = W / S, nty = H / S;
+  if (order && ntx * nty > kScanChunk && !count) return TTS_EINVAL;
+  if (bin_ws_layout(G, ntx, nty, nullptr, nullptr) > kScratchBytes) return TTS_ESCRATCH;
+  void* base = nullptr;
+  const int sc = scratch_base(&base);
+  if (sc != TTS_OK) return sc;
+  BinWorkspace ws;
+  bin_ws_layout(G, ntx, nty, static_cast<char*>(base), &ws);
+  return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
+                 ncand, inv, order, ws, true, stream);
 }
 
 int tts_tile_order(const int32_t* count, int T, int K, int32_t* order, hipStream_t stream) {

@@ -886,6 +886,7 @@ const char* tts_strerror(int code) {
     case TTS_EG: return "G must be below 2^30 (at most 2^28 for binning)";
     case TTS_ERADIUS: return "only stencil radius R = 1 is supported";
     case TTS_ESH: return "SH degree must be in [0, 3], with rest coefficients when above 0";
+    case TTS_ESCRATCH: return "sizes exceed the fixed scratch of the allocation-free entry point";
     default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }
 }

@@ -23,6 +23,9 @@ SIGNATURES = {
     "tts_bin_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
     "tts_assign_bins": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "tts_assign_bins_noalloc": (_c_int, [_vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                         _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         _vp]),
     "tts_theta_u_gathered": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                       _vp, _vp, _vp, _vp]),
     "tts_tile_order": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
