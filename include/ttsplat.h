@@ -71,7 +71,7 @@ int tts_geom_fwd(const float* params, int G, const float* camera, float near_z, 
 
 /* Geometry + activation backward: grad9[G,9] -> gparams[G,14] (overwritten).
  * Replaces tools/geom_bwd.py:67-152 (bwd) and the activation part of
- * tools/operands_manual.py:432-460 (bwd_manual); device form tools/geom_device.py:106-198,
+ * tools/operands_manual.py:83-111 (bwd_manual); device form tools/geom_device.py:106-198,
  * tools/resident_traced.py:397-427. */
 int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, float blur,
                  const float* grad9, float* gparams, hipStream_t stream);

@@ -1,0 +1,208 @@
+"""Pins for the oracle parts that the reference's own tests leave open (CPU, fp64).
+
+Each check is fixed by the mathematics, computed here by a route independent of the oracle's
+code (direct 2-D window sums, autograd of the pinhole map, scipy rotations, closed forms), and
+chosen so that a plausible mistake fails it:
+  SSIM (spike/metrics.py:15-28, pytorch_msssim's published algorithm):
+      C2 = 0.03 instead of 0.03^2, a window sigma other than 1.5, a dropped or mis-signed
+      structure term, and a mean taken over the wrong count all fail;
+  EWA projection (spike/geometry.py:28-57): any sign or index slip in the off-axis Jacobian
+      entries J02 = -fx x/z^2, J12 = -fy y/z^2 fails;
+  depth weight (spike/arms.py:34-37): a flipped sign of beta (tau - z), and gradients other than
+      the closed forms of tools/m8_depthweight_oracle.py:7-12, fail.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import geometry as ogeo
+from oracle import loss as oloss
+
+DT = torch.float64
+
+# The 11-tap gaussian window of sigma 1.5, normalised (taps 0..5; the window is symmetric):
+# exp(-c^2 / 4.5) / sum over c = -5..5.
+WINDOW_11_15 = (0.00102838008447911, 0.007598758135239185, 0.03600077212843083,
+                0.10936068950970002, 0.2130055377112537, 0.26601172486179436)
+C1_LIT = 1e-4     # (0.01 * data_range)^2, data_range 1
+C2_LIT = 9e-4     # (0.03 * data_range)^2
+
+
+def _window_2d():
+    taps = [math.exp(-(c * c) / 4.5) for c in range(-5, 6)]
+    s = sum(taps)
+    w = torch.tensor([t / s for t in taps], dtype=DT)
+    return torch.outer(w, w)
+
+
+def _window_moments(x, y):
+    """Window-weighted mu_x, mu_y, E[x^2], E[y^2], E[xy] over every valid 11x11 window of
+    [C,H,W] images, as direct 2-D weighted sums (no separable filtering)."""
+    W2 = _window_2d()
+    C, H, Wd = x.shape
+    Ho, Wo = H - 10, Wd - 10
+    out = [torch.empty(C, Ho, Wo, dtype=DT) for _ in range(5)]
+    for i in range(Ho):
+        for j in range(Wo):
+            px = x[:, i:i + 11, j:j + 11]
+            py = y[:, i:i + 11, j:j + 11]
+            for o, t in zip(out, (px, py, px * px, py * py, px * py)):
+                o[:, i, j] = (t * W2).sum((1, 2))
+    return out
+
+
+def test_window_taps_are_the_sigma_15_gaussian():
+    for g in (oloss.gauss_1d(), oloss.gauss_1d(oloss.window_size(64, 64))):
+        assert g.numel() == 11
+        for c, v in enumerate(WINDOW_11_15):
+            assert abs(float(g[c]) - v) < 1e-12, (c, float(g[c]), v)
+            assert abs(float(g[10 - c]) - v) < 1e-12
+
+
+def test_ssim_of_an_affine_pair_closed_form():
+    """y = a x + b over a non-constant x: mu_y = a mu_x + b, s_y = a^2 s_x, s_xy = a s_x, so
+    S = (2 mu_x mu_y + C1)(2 a s_x + C2) / ((mu_x^2 + mu_y^2 + C1)(s_x (1 + a^2) + C2))."""
+    gen = torch.Generator().manual_seed(11)
+    x = torch.rand(3, 19, 23, generator=gen, dtype=DT)
+    for a, b in ((0.7, 0.1), (-0.4, 0.8), (1.0, 0.0)):
+        y = a * x + b
+        mx, _, ex2, _, _ = _window_moments(x, x)
+        sx = ex2 - mx * mx
+        my = a * mx + b
+        pred = ((2 * mx * my + C1_LIT) * (2 * a * sx + C2_LIT)) / \
+               ((mx * mx + my * my + C1_LIT) * (sx * (1 + a * a) + C2_LIT))
+        got = oloss.ssim_map(x, y, oloss.gauss_1d())
+        assert got.shape == pred.shape
+        assert float((got - pred).abs().max()) < 1e-12, (a, b)
+
+
+def test_ssim_general_pair_window_sums():
+    """For unrelated x, y the map is the published formula on window moments computed here."""
+    gen = torch.Generator().manual_seed(12)
+    x = torch.rand(3, 16, 21, generator=gen, dtype=DT)
+    y = torch.rand(3, 16, 21, generator=gen, dtype=DT) ** 2
+    mx, my, ex2, ey2, exy = _window_moments(x, y)
+    sx, sy, sxy = ex2 - mx * mx, ey2 - my * my, exy - mx * my
+    pred = ((2 * mx * my + C1_LIT) / (mx * mx + my * my + C1_LIT)) * \
+           ((2 * sxy + C2_LIT) / (sx + sy + C2_LIT))
+    got = oloss.ssim_map(x, y, oloss.gauss_1d())
+    assert float((got - pred).abs().max()) < 1e-12
+
+
+def test_loss_mean_over_channels_and_valid_pixels_non_square():
+    """loss = 0.8 mean|x - y| + 0.2 (1 - sum S / (3 Hout Wout)) on a 13 x 29 image (Hout = 3,
+    Wout = 19), SSIM on the clamped images; values outside [0, 1] exercise the clamp."""
+    gen = torch.Generator().manual_seed(13)
+    H, W = 13, 29
+    pred = torch.rand(H, W, 3, generator=gen, dtype=DT) * 1.3 - 0.15
+    gt = torch.rand(H, W, 3, generator=gen, dtype=DT)
+    x = pred.clamp(0, 1).permute(2, 0, 1)
+    y = gt.clamp(0, 1).permute(2, 0, 1)
+    mx, my, ex2, ey2, exy = _window_moments(x, y)
+    sx, sy, sxy = ex2 - mx * mx, ey2 - my * my, exy - mx * my
+    S = ((2 * mx * my + C1_LIT) * (2 * sxy + C2_LIT)) / \
+        ((mx * mx + my * my + C1_LIT) * (sx + sy + C2_LIT))
+    assert S.shape == (3, 3, 19)
+    l1 = sum(abs(float(pred[i, j, c] - gt[i, j, c]))
+             for i in range(H) for j in range(W) for c in range(3)) / (3 * H * W)
+    expect = 0.8 * l1 + 0.2 * (1.0 - float(S.sum()) / (3 * 3 * 19))
+    assert abs(float(oloss.loss_fn(pred, gt)) - expect) < 1e-12
+
+
+# ------------------------------------------------------------------------ EWA projection
+def _scipy_rot(q_wxyz):
+    from scipy.spatial.transform import Rotation
+    w, x, y, z = q_wxyz
+    return torch.tensor(Rotation.from_quat([x, y, z, w]).as_matrix(), dtype=DT)
+
+
+def test_ewa_off_axis_matches_autograd_of_the_pinhole_map():
+    """At points well off the optical axis: mu2d = pi(mu_cam) with pi(x, y, z) =
+    (fx x / z + cx, fy y / z + cy), J = d pi / d mu_cam (autograd), Sigma2d = J Sigma_cam J^T +
+    0.3 I with Sigma_cam = R_v R diag(s^2) R^T R_v^T (R from scipy), conic = Sigma2d^-1."""
+    gen = torch.Generator().manual_seed(21)
+    cam = ogeo.make_camera(96, 160, (0.4, -0.3, 2.8))
+    cam = {k: (v.to(DT) if torch.is_tensor(v) else v) for k, v in cam.items()}
+    G = 12
+    P = torch.zeros(G, 14, dtype=DT)
+    P[:, 0:3] = torch.rand(G, 3, generator=gen, dtype=DT) * 1.6 - 0.8
+    P[:, 3:7] = torch.randn(G, 4, generator=gen, dtype=DT)
+    P[:, 7:10] = torch.rand(G, 3, generator=gen, dtype=DT) * 2.0 - 3.5
+    pr = ogeo.project_params(P, cam)
+    R_v, t_v = cam["R_v"], cam["t_v"]
+    fx, fy, cx, cy = cam["fx"], cam["fy"], cam["cx"], cam["cy"]
+
+    def pinhole(p):
+        return torch.stack([fx * p[0] / p[2] + cx, fy * p[1] / p[2] + cy])
+
+    n_off = 0
+    for g in range(G):
+        mc = R_v @ P[g, 0:3] + t_v
+        assert float(mc[2]) > 0.2
+        n_off += int(abs(float(mc[0])) > 0.2 and abs(float(mc[1])) > 0.1)
+        J = torch.autograd.functional.jacobian(pinhole, mc)
+        q = P[g, 3:7] / P[g, 3:7].norm()
+        R = _scipy_rot(q.tolist())
+        Sc = R_v @ R @ torch.diag(torch.exp(2 * P[g, 7:10])) @ R.T @ R_v.T
+        S2 = J @ Sc @ J.T + 0.3 * torch.eye(2, dtype=DT)
+        inv = torch.linalg.inv(S2)
+        assert torch.allclose(pr["mu2d"][g], pinhole(mc), atol=1e-10)
+        got = pr["conic"][g]
+        assert torch.allclose(got, torch.stack([inv[0, 0], inv[0, 1], inv[1, 1]]),
+                              rtol=1e-10, atol=1e-14), g
+    assert n_off >= 6
+
+
+# -------------------------------------------------------------------------- depth weight
+def _dw_scene():
+    gen = torch.Generator().manual_seed(31)
+    G = 9
+    P = torch.zeros(G, 14, dtype=DT)
+    P[:, 0:3] = torch.rand(G, 3, generator=gen, dtype=DT) - 0.5
+    P[:, 3] = 1.0
+    P[:, 7:10] = -3.0
+    P[:, 13] = torch.randn(G, generator=gen, dtype=DT)
+    cam = ogeo.make_camera(64, 64, (0.0, 0.0, 3.0))
+    cam = {k: (v.to(DT) if torch.is_tensor(v) else v) for k, v in cam.items()}
+    return P, cam
+
+
+def test_depth_weight_values():
+    """rho = sigmoid(beta (tau - z)): 1/2 at beta = 0, at z = tau, and the closed form at a
+    known (beta, tau, z); rho grows with tau for beta > 0 (nearer than tau -> weight above 1/2)."""
+    P, cam = _dw_scene()
+    base = ogeo.project_params(P, cam)
+    o = torch.sigmoid(P[:, 13])
+    z = base["depth"]
+    half = ogeo.project_params(P, cam, depth_bt=torch.tensor([0.0, 2.5], dtype=DT))
+    assert torch.allclose(half["o_col"], 0.5 * o, atol=1e-15)
+    beta, tau = 1.7, 2.9
+    dw = ogeo.project_params(P, cam, depth_bt=torch.tensor([beta, tau], dtype=DT))
+    for g in range(P.shape[0]):
+        rho = 1.0 / (1.0 + math.exp(-beta * (tau - float(z[g]))))
+        assert abs(float(dw["o_col"][g]) - float(o[g]) * rho) < 1e-14
+        if float(z[g]) < tau:
+            assert float(dw["o_col"][g]) > 0.5 * float(o[g])
+    at_z = ogeo.project_params(P, cam, depth_bt=torch.tensor([beta, float(z[0])], dtype=DT))
+    assert abs(float(at_z["o_col"][0]) - 0.5 * float(o[0])) < 1e-14
+    more = ogeo.project_params(P, cam, depth_bt=torch.tensor([beta, tau + 0.1], dtype=DT))
+    assert bool((more["o_col"] > dw["o_col"]).all())
+
+
+@pytest.mark.parametrize("beta,tau", [(1.3, 2.7), (4.0, 3.1), (-0.8, 2.9)])
+def test_depth_weight_gradients_closed_form(beta, tau):
+    """With L = sum_g c_g keo_g (keo = keep sigmoid(op) rho): dL/dbeta = sum gpre (tau - z),
+    dL/dtau = sum gpre beta, gpre = c_g keep o rho (1 - rho) (tools/m8_depthweight_oracle.py:7-12)."""
+    P, cam = _dw_scene()
+    gen = torch.Generator().manual_seed(32)
+    c = torch.randn(P.shape[0], generator=gen, dtype=DT)
+    bt = torch.tensor([beta, tau], dtype=DT, requires_grad=True)
+    pr = ogeo.project_params(P, cam, depth_bt=bt)
+    (pr["o_col"] * c).sum().backward()
+    z = pr["depth"].detach()
+    o = torch.sigmoid(P[:, 13])
+    rho = torch.sigmoid(beta * (tau - z))
+    gpre = c * o * rho * (1 - rho)
+    assert abs(float(bt.grad[0]) - float((gpre * (tau - z)).sum())) < 1e-13
+    assert abs(float(bt.grad[1]) - float((gpre * beta).sum())) < 1e-13

@@ -1,4 +1,4 @@
-"""The overfit loop under its reference names: spike/train.py:9-47.
+"""The overfit loop under its reference names: spike/train.py:9-41.
 
 `fit(model, cameras, gt_images, arm, iters, lambda_ssim, lr, k, blur_eps, near, log_every,
 sh_degree)` minimises the mean photometric loss over all views per iteration (full batch), as
@@ -139,7 +139,7 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
 
 @torch.no_grad()
 def eval_psnr(model, cameras, gt_images, arm, **kw):
-    """Mean PSNR over the given views (spike/train.py:42-47)."""
+    """Mean PSNR over the given views (spike/train.py:36-41)."""
     vals = [float(psnr(render(model, cam, arm, **kw), gt.to(params_of(model).device)))
             for cam, gt in zip(cameras, gt_images)]
     return sum(vals) / len(vals)
