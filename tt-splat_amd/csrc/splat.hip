@@ -57,6 +57,14 @@ __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, 
   tb = make_float4(2.0f * (b * mx + c * my) * inv_k, 1.0f - Q0 * inv_k, 0.0f, 0.0f);
   cl = make_float4(r1.z, r1.w, r2.x, r2.y);
 }
+// torch.relu propagates NaN: a slot whose u is NaN at every pixel (theta_u holds a NaN, or both
+// infinities -- the basis monomials are positive, so u = theta . Phi is then NaN everywhere)
+// makes every pixel of its tile NaN in the reference.  The forward kernels test each valid slot
+// here and write NaN over such a tile (image and den), so the backward sees NaN there too.
+__device__ __forceinline__ bool theta_poisons(const float4 ta, const float4 tb) {
+  return __builtin_isnan(((ta.x + ta.y) + (ta.z + ta.w)) + (tb.x + tb.y));
+}
+
 __device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
                                            float oy, float inv_k, float4& ta, float4& tb,
                                            float4& cl) {
@@ -69,7 +77,7 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
                                                const int32_t* __restrict__ idx,
                                                const uint8_t* __restrict__ valid, int t, int K,
                                                float ox, float oy, float inv_k, SlotLDS sl,
-                                               int* s_tmp) {
+                                               int* s_tmp, bool* bad) {
   // idx is read beside valid (every slot's entry is written; an invalid one is not used), and a
   // valid slot's proj record is requested before the compaction scan, whose barriers then
   // overlap that round trip
@@ -92,6 +100,7 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, ox, oy, inv_k, ta, tb, cl);
+      *bad = *bad || theta_poisons(ta, tb);
       sl.ta[pos] = ta;
       sl.tb[pos] = tb;
       sl.cl[pos] = cl;
@@ -107,11 +116,12 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
 __device__ __forceinline__ void load_slots_theta(const float* __restrict__ theta,
                                                  const float* __restrict__ col,
                                                  const float* __restrict__ oc, int t, int K,
-                                                 SlotLDS sl) {
+                                                 SlotLDS sl, bool* bad) {
   const float* th = theta + (int64_t)t * 6 * K;
   for (int s = threadIdx.x; s < K; s += blockDim.x) {
     sl.ta[s] = make_float4(th[s], th[K + s], th[2 * K + s], th[3 * K + s]);
     sl.tb[s] = make_float4(th[4 * K + s], th[5 * K + s], 0.0f, 0.0f);
+    *bad = *bad || theta_poisons(sl.ta[s], sl.tb[s]);
     const float* c = col + ((int64_t)t * K + s) * 3;
     sl.cl[s] = make_float4(c[0], c[1], c[2], oc[(int64_t)t * K + s]);
     sl.gid[s] = s;
@@ -134,13 +144,14 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * S, oy = ty * S;
   int n;
+  bool bad = false;
   if constexpr (FROM_PROJ) {
-    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
+    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp, &bad);
   } else {
-    load_slots_theta(theta, col, oc, t, K, sl);
+    load_slots_theta(theta, col, oc, t, K, sl, &bad);
     n = K;
   }
-  __syncthreads();
+  const bool poisoned = __syncthreads_or(bad);
 
   float lx[PPT], ly[PPT], xx[PPT], yy[PPT], xy[PPT];
   float ar[PPT], ag[PPT], ab[PPT], ad[PPT];
@@ -173,10 +184,11 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
   for (int i = 0; i < PPT; ++i) {
     const int p = threadIdx.x + 256 * i;
     const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
-    const float d = ad[i] + wb;
-    image[pix * 3 + 0] = (ar[i] + cbr) / d;
-    image[pix * 3 + 1] = (ag[i] + cbg) / d;
-    image[pix * 3 + 2] = (ab[i] + cbb) / d;
+    const float nanv = __builtin_nanf("");
+    const float d = poisoned ? nanv : ad[i] + wb;
+    image[pix * 3 + 0] = poisoned ? nanv : (ar[i] + cbr) / d;
+    image[pix * 3 + 1] = poisoned ? nanv : (ag[i] + cbg) / d;
+    image[pix * 3 + 2] = poisoned ? nanv : (ab[i] + cbb) / d;
     if (den_out) den_out[pix] = d;
   }
 }
@@ -218,10 +230,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     }
   }
   int n;
+  bool bad = false;  // a poisoned tile's den is NaN already (the forward wrote it)
   if constexpr (FROM_PROJ) {
-    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp);
+    n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp, &bad);
   } else {
-    load_slots_theta(theta, col, oc, t, K, sl);
+    load_slots_theta(theta, col, oc, t, K, sl, &bad);
     n = K;
   }
   // Per-pixel WSR backward: gnum = gC/den, gden = -(gC . C)/den.
@@ -464,6 +477,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
   const float oxf = (float)ox, oyf = (float)oy;
   // compact the valid slots, build theta in fp32 and store its split row and the colours
   int n = 0;
+  bool bad = false;
   for (int s0 = 0; s0 < K; s0 += 256) {
     const int s = s0 + threadIdx.x;
     const int v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
@@ -472,6 +486,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
     if (v) {
       float4 ta, tb, cl;
       build_slot(proj, idx[(int64_t)t * K + s], oxf, oyf, inv_k, ta, tb, cl);
+      bad = bad || theta_poisons(ta, tb);
       const float th[6] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y};
       theta_row(th, s_th + (size_t)pos * 4);
       const float c4[4] = {cl.x, cl.y, cl.z, cl.w};
@@ -499,7 +514,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
 #pragma unroll
     for (int m = 0; m < 8; ++m) dst[m * 8] = to_bf(0.0f);
   }
-  __syncthreads();
+  const bool poisoned = __syncthreads_or(bad);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, q = lane >> 4;
@@ -550,9 +565,9 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
     for (int e = 0; e < 4; ++e) {
       float v = acc[i][e];
       if constexpr (SPLIT_W) v += __shfl(v, (lane + 4) & 63);
-      const float d = __shfl(v, (lane & ~15) + 3) + wb;
+      const float d = poisoned ? __builtin_nanf("") : __shfl(v, (lane & ~15) + 3) + wb;
       const int64_t pix = (int64_t)(oy + row) * W + ox + 4 * q + e;
-      if (l16 < 3) image[pix * 3 + l16] = (v + cbn) / d;
+      if (l16 < 3) image[pix * 3 + l16] = poisoned ? d : (v + cbn) / d;
       if (l16 == 3 && den_out) den_out[pix] = d;
     }
   }
@@ -591,6 +606,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   // compact the valid slots in slot order (idx beside valid; a valid slot's proj record in flight
   // across the scan), build theta and stage the per-depth coefficients and the colours
   int n = 0;
+  bool bad = false;
   for (int s0 = 0; s0 < K; s0 += 256) {
     const int s = s0 + threadIdx.x;
     const int64_t ts = (int64_t)t * K + min(s, K - 1);
@@ -609,6 +625,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
+      bad = bad || theta_poisons(ta, tb);
       float4* c = s_coef + (size_t)pos * 4;
       c[0] = make_float4(0.f, 0.f, ta.x, 0.f);
       c[1] = make_float4(0.f, ta.z, ta.w, 0.f);
@@ -625,7 +642,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     for (int k = 0; k < 4; ++k) s_coef[(size_t)p * 4 + k] = z;
     s_col[p] = z;
   }
-  __syncthreads();
+  const bool poisoned = __syncthreads_or(bad);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
@@ -649,7 +666,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     for (int e = 0; e < 4; ++e) {
       const float4 cl = s_col[gi * 4 + e];
       // relu as one integer max on the bit pattern (a float max would first canonicalise the
-      // matrix-core result): u >= +0 keeps its bits, negative u becomes +0
+      // matrix-core result): u >= +0 keeps its bits, negative u becomes +0; a NaN u (a
+      // poisoned tile, whatever its sign bit) is overwritten by the NaN store below
       const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
       const float w = rl * rl;
       ar += w * cl.x;
@@ -660,10 +678,11 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   }
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
-  const float d = ad + wb;
-  image[pix * 3 + 0] = (ar + wb * bg[1]) / d;
-  image[pix * 3 + 1] = (ag + wb * bg[2]) / d;
-  image[pix * 3 + 2] = (ab + wb * bg[3]) / d;
+  const float nanv = __builtin_nanf("");
+  const float d = poisoned ? nanv : ad + wb;
+  image[pix * 3 + 0] = poisoned ? nanv : (ar + wb * bg[1]) / d;
+  image[pix * 3 + 1] = poisoned ? nanv : (ag + wb * bg[2]) / d;
+  image[pix * 3 + 2] = poisoned ? nanv : (ab + wb * bg[3]) / d;
   if (den_out) den_out[pix] = d;
 }
 

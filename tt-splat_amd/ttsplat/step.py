@@ -58,7 +58,9 @@ class TrainStep:
     (tools/resident_traced.py --depth-weight, :138-140,333-337,418-426,503-512): the opacity is
     multiplied by sigmoid(beta (tau - z_cam)); beta and tau live on the device and take an Adam
     step (learning rate lr_bt) after every step; tau0 = None uses the median camera depth of
-    the gaussians camera 0 keeps, as the reference refines it at warm-up."""
+    the gaussians camera 0 keeps, as the reference refines it at warm-up.
+    keep_grad = True (batch = 1): the fused backward also stores each step's dL/dparams [G,14]
+    in self.gparams (the gradient Adam was given)."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
@@ -67,7 +69,7 @@ class TrainStep:
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
                  dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None,
-                 depth_weight=None):
+                 depth_weight=None, keep_grad=False):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -153,6 +155,10 @@ class TrainStep:
         if self.batch < 1 or len(self.cams) % self.batch:
             raise ValueError(f"{len(self.cams)} views do not split into batches of {batch}")
         self.gacc = torch.zeros(G, 14, device=dev, dtype=F32) if self.batch > 1 else None
+        if keep_grad and self.batch > 1:
+            raise ValueError("keep_grad keeps the per-view gradient: batch must be 1")
+        # dL/dparams of the last step (written by the fused backward + Adam kernel)
+        self.gparams = torch.zeros(G, 14, device=dev, dtype=F32) if keep_grad else None
         self.gacc_sh = (torch.zeros_like(self.sh) if self.batch > 1 and self.sh_degree > 0
                         else None)
         self.graphs = {}
@@ -201,7 +207,8 @@ class TrainStep:
         if self.batch == 1:
             self._view_backward(i, advance=True)   # the step advance rides on geom_fwd
             kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
-                                  self.lr, self.step_block, sh_m=self.sh_m, sh_v=self.sh_v,
+                                  self.lr, self.step_block, gparams=self.gparams,
+                                  sh_m=self.sh_m, sh_v=self.sh_v,
                                   lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
                                   lambda_s=mc["lambda_s"], noise_lr=mc["noise_lr"],
                                   seed=mc["seed"], depth_bt=self.dw, gdepth=self.gdw, **sh)
