@@ -11,14 +11,16 @@
 // pixel row u is a quadratic in lx, evaluated for 4 rows x 4 slots x 16 pixels per
 // v_mfma_f32_16x16x4f32), the rest of the walk staying on the VALU.
 //
-// Backward: per-pixel gnum = gC/den, gden = -(gC.C)/den are staged in LDS; the slots are then
-// contracted over the tile's pixels slot-parallel (TPS threads share one slot and split its
-// rows).  Along a pixel row, u = (th0*lx + c1)*lx + c0 with c0, c1 fixed per row, and the
-// theta gradient is gathered as three row moments sum(gu*lx^2), sum(gu*lx), sum(gu), so the
-// inner loop costs 17 VALU ops per (pixel, slot) pair (per-row terms included).  Each slot's 10 partial sums are
-// combined in LDS and pushed through the theta backward; the slot's 9 gradients are stored to
-// gslot[T,K,9] (no atomics: the per-gaussian sum over its <= 9 slots is a gather through the
-// inverse bin table, in a fixed order, done by the geometry backward).
+// Backward: per-pixel gnum = gC/den, gden = -(gC.C)/den are staged in LDS (rows padded to S+1
+// entries); the slots are then contracted over the tile's pixels slot-parallel (tps adjacent
+// lanes share one slot and split its rows).  Along a pixel row, u = (th0*lx + c1)*lx + c0 with
+// c0, c1 fixed per row, and the theta gradient is gathered as three row moments sum(gu*lx^2),
+// sum(gu*lx), sum(gu), so the inner loop costs 17 VALU ops per (pixel, slot) pair (per-row terms
+// included).  Each slot's 10 partial sums are combined with lane shuffles and pushed through
+// the theta backward, whose conic and tile-local mean were staged in LDS beside theta; the
+// slot's 9 gradients are stored to gslot[T,K,9] (no atomics: the per-gaussian sum over its <= 9
+// slots is a gather through the inverse bin table, in a fixed order, done by the geometry
+// backward).
 
 #include "tts_common.h"
 
@@ -28,8 +30,9 @@ constexpr int kSplatMaxK = 512;
 
 struct SlotLDS {
   float4* ta;  // theta_u 0..3
-  float4* tb;  // theta_u 4..5, -, -
+  float4* tb;  // theta_u 4..5, tile-local mu_y, -
   float4* cl;  // col_o r,g,b, o_col
+  float4* ge;  // conic a, b, c, tile-local mu_x (proj mode: the theta backward's inputs)
   int* gid;    // gaussian id (proj mode) or original slot (theta mode)
   int* sid;    // original slot index of the compacted entry
 };
@@ -39,12 +42,13 @@ __device__ __forceinline__ SlotLDS carve_slots(unsigned char* base, int K) {
   s.ta = reinterpret_cast<float4*>(base);
   s.tb = s.ta + K;
   s.cl = s.tb + K;
-  s.gid = reinterpret_cast<int*>(s.cl + K);
+  s.ge = s.cl + K;
+  s.gid = reinterpret_cast<int*>(s.ge + K);
   s.sid = s.gid + K;
   return s;
 }
 
-__device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (3 * 16 + 8); }
+__host__ __device__ __forceinline__ size_t slot_lds_bytes(int K) { return (size_t)K * (4 * 16 + 8); }
 
 // Tile-local theta_u for one gaussian record r0..r2 of proj (tools/m4_train_binned.py:130-143).
 __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, const float4 r2,
@@ -54,7 +58,7 @@ __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, 
   const float mx = r0.x - ox, my = r0.y - oy;
   const float Q0 = a * mx * mx + 2.0f * b * mx * my + c * my * my;
   ta = make_float4(-a * inv_k, -c * inv_k, -2.0f * b * inv_k, 2.0f * (a * mx + b * my) * inv_k);
-  tb = make_float4(2.0f * (b * mx + c * my) * inv_k, 1.0f - Q0 * inv_k, 0.0f, 0.0f);
+  tb = make_float4(2.0f * (b * mx + c * my) * inv_k, 1.0f - Q0 * inv_k, my, 0.0f);
   cl = make_float4(r1.z, r1.w, r2.x, r2.y);
 }
 // torch.relu propagates NaN: a slot whose u is NaN at every pixel (theta_u holds a NaN, or both
@@ -104,6 +108,7 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
       sl.ta[pos] = ta;
       sl.tb[pos] = tb;
       sl.cl[pos] = cl;
+      sl.ge[pos] = make_float4(r0.z, r0.w, r1.x, r0.x - ox);
       sl.gid[pos] = g;
       sl.sid[pos] = s;
     }
@@ -193,6 +198,120 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
   }
 }
 
+// Contraction of one tile's staged slots over its pixels, then the theta backward and the
+// stores (the main loop of the splat backward).  Every thread of the block must call it (it
+// contains barriers when slots share rows).
+template <int S, bool FROM_PROJ>
+__device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const float4* s_px,
+                                             int t, int K, int ox, int oy,
+                                             float inv_k, const float* __restrict__ proj,
+                                             float* __restrict__ gslot,
+                                             float* __restrict__ gtheta,
+                                             float* __restrict__ gcol, float* __restrict__ goc) {
+  constexpr int kRowChunks = S == 16 ? 2 : 1;  // 8-pixel chunks of a row unrolled
+  // threads per slot: split rows while slots are few.  The tps threads of a slot are adjacent
+  // lanes of one wave (rows h, h + tps, ...), so their partial sums combine with lane shuffles.
+  int tps = 1;
+  while (tps < 16 && tps * 2 * n <= 256) tps <<= 1;
+  const int sg = 256 / tps;
+  const int h = threadIdx.x % tps, sl_local = threadIdx.x / tps;
+  for (int c0s = 0; c0s < n; c0s += sg) {
+    const int s = c0s + sl_local;
+    const bool active = s < n;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f), B = A, C = A;
+    if (active) {
+      A = sl.ta[s];
+      B = sl.tb[s];
+      C = sl.cl[s];
+    }
+    float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f;
+    float gr = 0.f, gg = 0.f, gb = 0.f, go = 0.f;
+    if (active) {
+#pragma unroll 2
+      for (int y = h; y < S; y += tps) {
+        const float ly = (float)y + 0.5f;
+        const float yy = ly * ly;
+        const float cc0 = A.y * yy + B.x * ly + B.y;  // u = (A.x*lx + cc1)*lx + cc0
+        const float cc1 = A.z * ly + A.w;
+        float m0 = 0.f, m1 = 0.f, m2 = 0.f;
+        const float4* row = s_px + y * (S + 1);
+        // S = 16: fully unrolled along the row, so lx and lx^2 are literals (2 VALU ops per pair
+        // fewer than a rolled loop over 8-pixel chunks, which recomputes them).  S = 32 keeps
+        // the rolled chunks: unrolled, its 32-pixel rows spill registers.
+#pragma unroll kRowChunks
+        for (int xb = 0; xb < S; xb += 8) {
+          const float xbf = (float)xb;
+#pragma unroll
+          for (int x8 = 0; x8 < 8; ++x8) {
+            const float lx = xbf + ((float)x8 + 0.5f);
+            const float u = (A.x * lx + cc1) * lx + cc0;
+            const float r = fmaxf(u, 0.0f);
+            const float w = r * r;
+            const float4 q = row[xb + x8];
+            const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
+            const float gu = r * gw;  // half of dL/du
+            gr += w * q.x;
+            gg += w * q.y;
+            gb += w * q.z;
+            go += w * q.w;
+            m0 += gu * (lx * lx);
+            m1 += gu * lx;
+            m2 += gu;
+          }
+        }
+        g0 += m0;
+        g2 += ly * m1;
+        g3 += m1;
+        g1 += yy * m2;
+        g4 += ly * m2;
+        g5 += m2;
+      }
+    }
+    // combine the tps row-partials of each slot (butterfly over its adjacent lanes)
+    for (int d = 1; d < tps; d <<= 1) {
+      g0 += __shfl_xor(g0, d); g1 += __shfl_xor(g1, d); g2 += __shfl_xor(g2, d);
+      g3 += __shfl_xor(g3, d); g4 += __shfl_xor(g4, d); g5 += __shfl_xor(g5, d);
+      gr += __shfl_xor(gr, d); gg += __shfl_xor(gg, d); gb += __shfl_xor(gb, d);
+      go += __shfl_xor(go, d);
+    }
+    if (h == 0 && active) {
+      // dL/du = 2 r gw: the factor 2 was left out of the inner loop
+      g0 *= 2.f; g1 *= 2.f; g2 *= 2.f; g3 *= 2.f; g4 *= 2.f; g5 *= 2.f;
+      if constexpr (FROM_PROJ) {
+        // theta backward (tools/resident_traced.py:72-88), gtQ = gtheta * (-1/k); the conic and
+        // tile-local mean were staged beside theta, so no global re-read
+        const float4 ge = sl.ge[s];
+        const float a = ge.x, b = ge.y, c = ge.z;
+        const float mx = ge.w, my = B.z;
+        const float nk = -inv_k;
+        const float q0 = g0 * nk, q1 = g1 * nk, q2 = g2 * nk, q3 = g3 * nk, q4 = g4 * nk, q5 = g5 * nk;
+        const float ga = q0 - 2.f * mx * q3 + mx * mx * q5;
+        const float gbv = 2.f * q2 - 2.f * my * q3 - 2.f * mx * q4 + 2.f * mx * my * q5;
+        const float gc = q1 - 2.f * my * q4 + my * my * q5;
+        const float gmx = -2.f * a * q3 - 2.f * b * q4 + (2.f * a * mx + 2.f * b * my) * q5;
+        const float gmy = -2.f * b * q3 - 2.f * c * q4 + (2.f * b * mx + 2.f * c * my) * q5;
+        float* dst = gslot + ((int64_t)t * K + sl.sid[s]) * 9;
+        dst[0] = ga;
+        dst[1] = gbv;
+        dst[2] = gc;
+        dst[3] = gmx;
+        dst[4] = gmy;
+        dst[5] = gr;
+        dst[6] = gg;
+        dst[7] = gb;
+        dst[8] = go;
+      } else {
+        float* th = gtheta + (int64_t)t * 6 * K;
+        th[s] = g0; th[K + s] = g1; th[2 * K + s] = g2;
+        th[3 * K + s] = g3; th[4 * K + s] = g4; th[5 * K + s] = g5;
+        float* gcp = gcol + ((int64_t)t * K + s) * 3;
+        gcp[0] = gr; gcp[1] = gg; gcp[2] = gb;
+        goc[(int64_t)t * K + s] = go;
+      }
+    }
+  }
+}
+
 template <int S, bool FROM_PROJ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_splat_bwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
@@ -205,13 +324,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     float* __restrict__ gwb) {
   constexpr int P = S * S;
   constexpr int PPT = P / 256;
-  constexpr int kRowChunks = S == 16 ? 2 : 1;  // 8-pixel chunks of a row unrolled
   extern __shared__ unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   __shared__ float s_ftmp[4];
   const SlotLDS sl = carve_slots(s_dyn, K);
+  // pixel rows padded to S + 1 entries: the tps rows read together fall in different banks
   float4* s_px = reinterpret_cast<float4*>(s_dyn + slot_lds_bytes(K) + (16 - slot_lds_bytes(K) % 16) % 16);
-  float* s_red = reinterpret_cast<float*>(s_px + P);  // [10][256]
 
   const int t = order ? order[blockIdx.x] : blockIdx.x;
   const int tx = t % ntx, ty = t / ntx;
@@ -245,7 +363,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     const float inv = 1.0f / pd[i];
     const float4 q = make_float4(pg[i][0] * inv, pg[i][1] * inv, pg[i][2] * inv,
                                  -(pg[i][0] * pc[i][0] + pg[i][1] * pc[i][1] + pg[i][2] * pc[i][2]) * inv);
-    s_px[threadIdx.x + 256 * i] = q;
+    const int p = threadIdx.x + 256 * i;
+    s_px[(p / S) * (S + 1) + p % S] = q;
     wpart += q.x * bg1 + q.y * bg2 + q.z * bg3 + q.w;
   }
   if (gwb) {  // per-tile partial of dL/dw_b (summed by the caller)
@@ -254,118 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   }
   __syncthreads();
 
-  // threads per slot: split rows while slots are few
-  int tps = 1;
-  while (tps < 16 && tps * 2 * n <= 256) tps <<= 1;
-  const int sg = 256 / tps;
-  const int h = threadIdx.x / sg, sl_local = threadIdx.x % sg;
-  const float ox_f = (float)ox, oy_f = (float)oy;
-  for (int c0s = 0; c0s < n; c0s += sg) {
-    const int s = c0s + sl_local;
-    const bool active = s < n;
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f), B = A, C = A;
-    if (active) {
-      A = sl.ta[s];
-      B = sl.tb[s];
-      C = sl.cl[s];
-    }
-    float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f;
-    float gr = 0.f, gg = 0.f, gb = 0.f, go = 0.f;
-    if (active) {
-#pragma unroll 2
-      for (int y = h; y < S; y += tps) {
-        const float ly = (float)y + 0.5f;
-        const float yy = ly * ly;
-        const float cc0 = A.y * yy + B.x * ly + B.y;  // u = (A.x*lx + cc1)*lx + cc0
-        const float cc1 = A.z * ly + A.w;
-        float m0 = 0.f, m1 = 0.f, m2 = 0.f;
-        const float4* row = s_px + y * S;
-        // S = 16: fully unrolled along the row, so lx and lx^2 are literals (2 VALU ops per pair
-        // fewer than a rolled loop over 8-pixel chunks, which recomputes them).  S = 32 keeps
-        // the rolled chunks: unrolled, its 32-pixel rows spill registers.
-#pragma unroll kRowChunks
-        for (int xb = 0; xb < S; xb += 8) {
-          const float xbf = (float)xb;
-#pragma unroll
-          for (int x8 = 0; x8 < 8; ++x8) {
-            const float lx = xbf + ((float)x8 + 0.5f);
-            const float u = (A.x * lx + cc1) * lx + cc0;
-            const float r = fmaxf(u, 0.0f);
-            const float w = r * r;
-            const float4 q = row[xb + x8];
-            const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
-            const float gu = r * gw;  // half of dL/du
-            gr += w * q.x;
-            gg += w * q.y;
-            gb += w * q.z;
-            go += w * q.w;
-            m0 += gu * (lx * lx);
-            m1 += gu * lx;
-            m2 += gu;
-          }
-        }
-        g0 += m0;
-        g2 += ly * m1;
-        g3 += m1;
-        g1 += yy * m2;
-        g4 += ly * m2;
-        g5 += m2;
-      }
-    }
-    // combine the tps row-partials of each slot
-    if (tps > 1) {
-      float* red = s_red + threadIdx.x;
-      red[0 * 256] = g0; red[1 * 256] = g1; red[2 * 256] = g2; red[3 * 256] = g3;
-      red[4 * 256] = g4; red[5 * 256] = g5; red[6 * 256] = gr; red[7 * 256] = gg;
-      red[8 * 256] = gb; red[9 * 256] = go;
-      __syncthreads();
-      if (h == 0) {
-        for (int k2 = 1; k2 < tps; ++k2) {
-          const float* o = s_red + k2 * sg + sl_local;
-          g0 += o[0 * 256]; g1 += o[1 * 256]; g2 += o[2 * 256]; g3 += o[3 * 256];
-          g4 += o[4 * 256]; g5 += o[5 * 256]; gr += o[6 * 256]; gg += o[7 * 256];
-          gb += o[8 * 256]; go += o[9 * 256];
-        }
-      }
-      __syncthreads();
-    }
-    if (h == 0 && active) {
-      // dL/du = 2 r gw: the factor 2 was left out of the inner loop
-      g0 *= 2.f; g1 *= 2.f; g2 *= 2.f; g3 *= 2.f; g4 *= 2.f; g5 *= 2.f;
-      if constexpr (FROM_PROJ) {
-        // theta backward (tools/resident_traced.py:72-88), gtQ = gtheta * (-1/k)
-        const int g = sl.gid[s];
-        const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
-        const float4 r0 = r[0], r1 = r[1];
-        const float a = r0.z, b = r0.w, c = r1.x;
-        const float mx = r0.x - ox_f, my = r0.y - oy_f;
-        const float nk = -inv_k;
-        const float q0 = g0 * nk, q1 = g1 * nk, q2 = g2 * nk, q3 = g3 * nk, q4 = g4 * nk, q5 = g5 * nk;
-        const float ga = q0 - 2.f * mx * q3 + mx * mx * q5;
-        const float gbv = 2.f * q2 - 2.f * my * q3 - 2.f * mx * q4 + 2.f * mx * my * q5;
-        const float gc = q1 - 2.f * my * q4 + my * my * q5;
-        const float gmx = -2.f * a * q3 - 2.f * b * q4 + (2.f * a * mx + 2.f * b * my) * q5;
-        const float gmy = -2.f * b * q3 - 2.f * c * q4 + (2.f * b * mx + 2.f * c * my) * q5;
-        float* dst = gslot + ((int64_t)t * K + sl.sid[s]) * 9;
-        dst[0] = ga;
-        dst[1] = gbv;
-        dst[2] = gc;
-        dst[3] = gmx;
-        dst[4] = gmy;
-        dst[5] = gr;
-        dst[6] = gg;
-        dst[7] = gb;
-        dst[8] = go;
-      } else {
-        float* th = gtheta + (int64_t)t * 6 * K;
-        th[s] = g0; th[K + s] = g1; th[2 * K + s] = g2;
-        th[3 * K + s] = g3; th[4 * K + s] = g4; th[5 * K + s] = g5;
-        float* gcp = gcol + ((int64_t)t * K + s) * 3;
-        gcp[0] = gr; gcp[1] = gg; gcp[2] = gb;
-        goc[(int64_t)t * K + s] = go;
-      }
-    }
-  }
+  bwd_contract<S, FROM_PROJ>(n, sl, s_px, t, K, ox, oy, inv_k, proj, gslot, gtheta, gcol, goc);
 }
 
 // ------------------------------------------------------------------ matrix-core forward --
@@ -716,11 +724,11 @@ inline int check_tile(int H, int W, int S, int K) {
   return TTS_OK;
 }
 
-inline size_t fwd_lds(int K) { return (size_t)K * (3 * 16 + 8); }
+inline size_t fwd_lds(int K) { return slot_lds_bytes(K); }
 inline size_t bwd_lds(int K, int S) {
-  size_t a = (size_t)K * (3 * 16 + 8);
+  size_t a = slot_lds_bytes(K);
   a += (16 - a % 16) % 16;
-  return a + (size_t)S * S * 16 + 10 * 256 * sizeof(float);
+  return a + (size_t)S * (S + 1) * 16;
 }
 
 template <bool FROM_PROJ>
