@@ -14,6 +14,19 @@ G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from 
 the launch stream, the roofline of the dominant kernel, and the CPU oracle (PyTorch-CPU
 restatement of the reference path) timed on this host's cores, and on one thread, on bounded
 samples of the same workload.
+
+Clock state: before any timed region the GPU replays the forward graphs for ~1.5 s (no state
+change), so every timed region runs at steady clocks; a cold GPU measures several percent slower
+for the first second.  Per-kernel times are HIP events on the launch stream, camera 0 (and each
+of the 8 cameras for the splat kernels, with their pair counts, so the roofline fraction can be
+recomputed from a profile of the same run).
+
+Roofline convention: the splat kernels are priced in the reference's algorithmic flops per
+(pixel, valid slot) pair -- 22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80,
+Phi.theta 12 + relu^2 2 + WSR 8, and the transposed contractions) -- against MI355X's 157.3
+TFLOP/s FP32 peak.  That peak is reachable without packed FP32 instructions on gfx950 (wave64
+FP32 FMAs issue at two cycles each when enough waves are ready), so frac is the fraction of
+the attainable VALU rate.
 """
 import argparse
 import json
@@ -37,9 +50,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--config", default="c4")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="rough total of the oracle's timed CPU samples over all configurations")
     ap.add_argument("--kernel-reps", type=int, default=100)
-    ap.add_argument("--no-small", action="store_true", help="skip the G=2000 128x128 run")
+    ap.add_argument("--no-small", action="store_true",
+                    help="skip the G=2000 128x128 runs (c1 forward, c2 3000-iteration training)")
     ap.add_argument("--no-c3", action="store_true", help="skip the G=10k 800x800 run")
     ap.add_argument("--no-c5", action="store_true", help="skip the G=1M 1920x1072 batch run")
     ap.add_argument("--c5-batches", type=int, default=3)
@@ -122,6 +137,63 @@ def time_forward(ts, steps, warmup, torch):
         graphs[i % ncam].replay()
     torch.cuda.synchronize()
     return time.perf_counter() - t0
+
+
+def warm_clocks(ts, torch, seconds=1.5):
+    """Forward graph replays of every camera for `seconds` (reads the state, changes nothing
+    the training reads), so the following timed regions start at steady GPU clocks."""
+    graphs = []
+    for ci in range(len(ts.cams)):
+        ts.forward(ci)
+    torch.cuda.synchronize()
+    for ci in range(len(ts.cams)):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ts.forward(ci)
+        graphs.append(g)
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            graphs[i % len(graphs)].replay()
+            i += 1
+        torch.cuda.synchronize()
+    return i
+
+
+def time_splat_per_camera(ts, reps, torch, kernels):
+    """Fused splat forward / backward of every camera: HIP-event microseconds per launch and the
+    (pixel, valid slot) pairs of that camera's bins (the state is the current one; the
+    backward's input image gradient is a fixed random field)."""
+    stream = torch.cuda.current_stream()
+    gim = torch.randn(ts.H, ts.W, 3, generator=torch.Generator().manual_seed(11)).cuda()
+    rows = []
+    for ci in range(len(ts.cams)):
+        ts.forward(ci)
+        torch.cuda.synchronize()
+        pairs = int(ts.count.long().sum()) * ts.S * ts.S
+        rec = dict(camera=ci, pairs=pairs)
+        jobs = {"splat_fwd": lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H,
+                                                       ts.W, ts.S, ts.k, ts.image, ts.den,
+                                                       ts.order),
+                "splat_bwd": lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H,
+                                                       ts.W, ts.S, ts.k, ts.image, ts.den, gim,
+                                                       ts.gslot, order=ts.order)}
+        for name, fn in jobs.items():
+            for _ in range(3):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                fn()
+            e1.record(stream)
+            e1.synchronize()
+            rec[name + "_us"] = e0.elapsed_time(e1) / reps * 1e3
+        rows.append(rec)
+    ts.forward(0)
+    torch.cuda.synchronize()
+    return rows
 
 
 def time_kernels(ts, reps, torch, kernels):
@@ -303,50 +375,179 @@ def run_c5(args, torch, scenes, kernels, TrainStep):
         c5_crop="1080 rows cropped to 1072 (whole 16-px tiles)")
 
 
-def cpu_baseline(cfg, seconds, torch):
-    """The oracle's training step (autograd through the PyTorch-CPU restatement of the
-    reference path, torch.optim-equivalent Adam) on this host, camera 0, bounded sample."""
+def cpu_threads():
+    """(host cores, cores this process may run on, threads used): the oracle uses every core
+    of the process's CPU share (capped by OMP_NUM_THREADS when the launcher sets it)."""
+    host = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = host
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return host, avail, (min(avail, omp) if omp > 0 else avail)
+
+
+def _rate(fn, seconds, min_n=1):
+    """(calls, seconds) of fn repeated for at least `seconds` and `min_n` calls."""
+    n, t0 = 0, time.perf_counter()
+    while n < min_n or time.perf_counter() - t0 < seconds:
+        fn()
+        n += 1
+    return n, time.perf_counter() - t0
+
+
+def cpu_baseline(args, torch, scenes, kernels):
+    """The oracle -- the PyTorch-CPU restatement of the reference path (geometry, assign_bins,
+    gather, einsum WSR; autograd backward, the restated L1+SSIM loss, Adam) -- timed on this
+    host's cores, camera 0 of each configuration, bounded samples (the reference's own idiom:
+    warm-up, then repeated calls timed with perf_counter, tools/m3_perf.py:47-56).  Also the
+    dense arm-A render (spike/render.py) at G=2000, one-thread rows, and the bin-table
+    agreement between the GPU and the oracle when each starts from the parameters."""
     from oracle import binning as obin
+    from oracle import geometry as ogeo
     from oracle import pipeline as opipe
     from oracle import splat as osplat
-    cam = cfg.cameras()[0].as_dict()
-    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
-    P = cfg.params(seed=0)
-    with torch.no_grad():
-        tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k)
-    m = torch.zeros_like(P)
-    v = torch.zeros_like(P)
+    host, avail, use = cpu_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(use)
+    sec = args.cpu_seconds
+    rows = {}
     lr = torch.full((14,), 1e-3)
     lr[:3] = 1.6e-4
-    opipe.train_step(P, m, v, 1, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)     # warm-up
-    n, t0 = 0, time.perf_counter()
-    while n < 2 or time.perf_counter() - t0 < seconds:
-        opipe.train_step(P, m, v, n + 2, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)
-        n += 1
-    dt = time.perf_counter() - t0
-    nf, t1 = 0, time.perf_counter()
+    plan = (("c1", sec * 0.06, sec * 0.06), ("c1_ref", sec * 0.06, sec * 0.06),
+            ("c3", sec * 0.1, sec * 0.15), ("c4", sec * 0.12, sec * 0.3), ("c5", 0.0, 0.0))
+    for name, fsec, tsec in plan:
+        cfg = scenes.CONFIGS[name]
+        cam = cfg.cameras()[0].as_dict()
+        tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+        P = cfg.params(seed=0)
+        with torch.no_grad():
+            tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k,
+                                       span=cfg.span)
+            nf, df = _rate(lambda: osplat.render_binned(P, cam, tmap, K=cfg.K, k=cfg.k,
+                                                        span=cfg.span), fsec)
+        m, v = torch.zeros_like(P), torch.zeros_like(P)
+        it = [0]
+
+        def step():
+            it[0] += 1
+            opipe.train_step(P, m, v, it[0], cam, tmap, tgt, lr, K=cfg.K, k=cfg.k, span=cfg.span)
+        if name != "c5":
+            step()                                   # warm-up
+        nt, dt = _rate(step, tsec)
+        rows[name] = dict(fwd_fps=nf / df, fwd_ms=df / nf * 1e3, train_its=nt / dt,
+                          train_ms=dt / nt * 1e3, sample=f"{nf} forwards, {nt} train steps")
+    rows["c2"] = dict(rows["c1_ref"], note="the c2 shape (G=2000, 128x128, S=16, k=4) in fp32: "
+                                           "the oracle has no bf16 mode")
+    # the dense arm-A render (spike/render.py:14-49) at G=2000, 128x128, k=9
+    cfg = scenes.CONFIGS["c1"]
+    cam = cfg.cameras()[0].as_dict()
+    P = cfg.params(seed=0)
     with torch.no_grad():
-        while nf < 2 or time.perf_counter() - t1 < seconds / 3:
-            osplat.render_binned(P, cam, tmap, K=cfg.K, k=cfg.k)
-            nf += 1
-    df = time.perf_counter() - t1
-    cores = torch.get_num_threads()
-    # the same train step on one thread (a shorter bounded sample)
+        osplat.render_dense(P, cam, k=cfg.k)
+        nd, dd = _rate(lambda: osplat.render_dense(P, cam, k=cfg.k), sec * 0.04, 2)
+    rows["c1_dense_fwd_fps"] = nd / dd
+    # one thread
     torch.set_num_threads(1)
     try:
-        n1, t2 = 0, time.perf_counter()
-        while n1 < 1 or time.perf_counter() - t2 < seconds / 3:
-            opipe.train_step(P, m, v, n + n1 + 2, cam, tmap, tgt, lr, K=cfg.K, k=cfg.k)
-            n1 += 1
-        d1 = time.perf_counter() - t2
+        one = {}
+        for name, tsec in (("c1_ref", sec * 0.05), ("c4", 0.0)):
+            cfg = scenes.CONFIGS[name]
+            cam = cfg.cameras()[0].as_dict()
+            tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+            P = cfg.params(seed=0)
+            with torch.no_grad():
+                tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k)
+            m, v = torch.zeros_like(P), torch.zeros_like(P)
+            n1, d1 = _rate(lambda: opipe.train_step(P, m, v, 1, cam, tmap, tgt, lr, K=cfg.K,
+                                                    k=cfg.k), tsec)
+            one[name] = dict(train_its=n1 / d1, train_ms=d1 / n1 * 1e3, steps=n1)
     finally:
-        torch.set_num_threads(cores)
-    return dict(value=n / dt, unit="it/s", cores=cores, kind="port",
-                sample=f"{n} oracle train steps ({dt:.1f} s) + {nf} forwards ({df:.1f} s) "
-                       f"after 1 warm-up, {cfg.name} camera 0",
-                fwd_fps=nf / df,
-                one_thread=dict(value=n1 / d1, unit="it/s", cores=1,
-                                sample=f"{n1} oracle train steps ({d1:.1f} s)"))
+        torch.set_num_threads(use)
+    # bin tables: GPU geometry + binning vs oracle geometry + binning, each from the parameters
+    agree = {}
+    for name in ("c1_ref", "c3", "c4", "c5"):
+        cfg = scenes.CONFIGS[name]
+        camo = cfg.cameras()[5 if name == "c5" else 0]
+        P = cfg.params(seed=0)
+        proj, keep = kernels.geom_fwd(P.cuda(), camo.device_block("cuda"))
+        idx, valid, _, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S,
+                                                   cfg.K, cfg.span)
+        pr = ogeo.project_params(P, camo.as_dict())
+        tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+        ridx, rvalid = obin.assign_bins(pr["mu2d"].detach(), pr["keep"], tmap, 1, cfg.K,
+                                        cfg.span, stable=True)
+        diff = (idx.cpu().long() != ridx).any(1) | (valid.cpu().bool() != rvalid).any(1)
+        agree[name] = dict(tiles=tmap.T, tiles_differ=int(diff.sum()),
+                           pairs=int(ncand.long().sum()))
+    # below 32768 pairs the reference's argsort is an introsort: G=2000 128x128 against the
+    # reference order on the GPU's own centres
+    cfg = scenes.CONFIGS["c1_ref"]
+    camo = cfg.cameras()[0]
+    proj, keep = kernels.geom_fwd(cfg.params(seed=0).cuda(), camo.device_block("cuda"))
+    idx, valid, _, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, cfg.K,
+                                           cfg.span)
+    mu, kp = proj[:, 0:2].cpu(), keep.cpu().bool()
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ridx, rvalid = obin.assign_bins(mu, kp, tmap, 1, cfg.K, cfg.span, stable=False)
+    ic, vc = idx.cpu().long(), valid.cpu().bool()
+    reordered = (ic != ridx).any(1) | (vc != rvalid).any(1)
+    set_diff, swapped = 0, 0
+    for t in torch.nonzero(reordered).flatten().tolist():
+        a, b = set(ic[t][vc[t]].tolist()), set(ridx[t][rvalid[t]].tolist())
+        if a != b:
+            set_diff += 1
+            swapped += len(a - b)
+    intro = dict(tiles=tmap.T, tie_tiles=len(obin.tie_tiles(mu, kp, tmap, 1, cfg.span)),
+                 tiles_ordered_differently=int(reordered.sum()),
+                 tiles_with_different_kept_set=set_diff, gaussians_swapped=swapped)
+    torch.set_num_threads(prev)
+    c4 = rows["c4"]
+    return dict(value=c4["train_its"], unit="it/s", cores=use, kind="port",
+                sample=f"oracle train steps and forwards, camera 0 of each configuration, about "
+                       f"{sec:.0f} s of CPU work in all; headline: c4 {c4['sample']}",
+                host_cores=host, cores_available=avail, fwd_fps=c4["fwd_fps"], rows=rows,
+                one_thread=dict(cores=1, value=one["c4"]["train_its"], unit="it/s", rows=one),
+                bins_from_parameters=agree, bins_reference_order_g2000=intro)
+
+
+def small_configs(torch, scenes, TrainStep):
+    """G=2000, 128x128: forward fps as configured (fp32, 32x32 tiles, k=9) and in the
+    reference's own constants (16x16 tiles, k=4); the c2 training run for its 3000 iterations
+    (bf16 render forward, fp32 Adam), wall-clock it/s and the final loss, beside the oracle's
+    own 3000-step run of that shape (fp32, recorded in tests/golden/c2_oracle_trajectory.json)."""
+    out = {}
+    for name in ("c1", "c1_ref"):
+        cfg = scenes.CONFIGS[name]
+        ts = build_step(cfg, torch, TrainStep)
+        out[f"{name}_fwd_fps"] = 1000 / time_forward(ts, 1000, 100, torch)
+        del ts
+    out["c1_note"] = "c1: fp32, S=32, k=9 as configured; c1_ref: S=16, k=4 (reference constants)"
+    cfg = scenes.CONFIGS["c2"]
+    ts = build_step(cfg, torch, TrainStep)
+    ts.capture()
+    ts.step(0)
+    torch.cuda.synchronize()
+    loss0 = float(ts.loss())
+    t0 = time.perf_counter()
+    for _ in range(2999):
+        ts.step(0)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    out.update(c2_train_its=2999 / dt, c2_iterations=3000, c2_seconds_3000=dt * 3000 / 2999,
+               c2_loss_first=loss0, c2_loss_final=float(ts.loss()),
+               c2_fwd_fps=1000 / time_forward(ts, 1000, 100, torch),
+               c2_note="G=2000 128x128, bf16 render forward (matrix cores), fp32 params/Adam, "
+                       "target = GPU bf16 render of the seed-1 set")
+    path = os.path.join(ROOT, "tests", "golden", "c2_oracle_trajectory.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            rec = json.load(f)
+        out.update(c2_oracle_loss_final=rec["final_loss"],
+                   c2_oracle_loss_first=rec["loss_at"]["1"],
+                   c2_oracle_note="oracle (fp32 CPU) 3000-step run, target = oracle render of "
+                                  "the seed-1 set")
+    return out
 
 
 def main():
@@ -362,30 +563,34 @@ def main():
     cfg = scenes.CONFIGS[args.config]
     torch.cuda.set_device(0)
     ts = build_step(cfg, torch, TrainStep)
+    warm_clocks(ts, torch)
     train_s = time_train(ts, args.steps, args.warmup, torch)
     its = args.steps / train_s
     fwd_s = time_forward(ts, args.steps, args.warmup, torch)
     fps = args.steps / fwd_s
     loss_last = float(ts.loss())
     kt = time_kernels(ts, args.kernel_reps, torch, kernels)
-    pairs = int(ts.count.long().sum()) * ts.S * ts.S
+    per_cam = time_splat_per_camera(ts, max(10, args.kernel_reps // 2), torch, kernels)
+    pairs = per_cam[0]["pairs"]
     rows = {}
     for name in ("splat_fwd", "splat_bwd"):
         flops = FLOP_PER_PAIR[name] * pairs
         tfl = flops / (kt[name] * 1e-6) / 1e12
         rows[name] = dict(us=kt[name], tflops=tfl, frac=tfl / PEAK_FP32_TFLOPS)
     dom = max(("splat_fwd", "splat_bwd"), key=lambda n: kt[n])
+    all_pairs = sum(r["pairs"] for r in per_cam)
+    all_us = sum(r[dom + "_us"] for r in per_cam)
     roofline = dict(bound="valu", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
                     unit="TFLOP/s", frac=rows[dom]["frac"], traffic=load_traffic(dom, cfg.name),
-                    flops_per_launch=FLOP_PER_PAIR[dom] * pairs, pairs_per_launch=pairs,
-                    us_per_launch=kt[dom])
-    # the small configuration (G=2000, 128x128)
-    its2 = fps2 = None
-    if not args.no_small:
-        small = scenes.CONFIGS["c2"]
-        ts2 = build_step(small, torch, TrainStep)
-        its2 = 1000 / time_train(ts2, 1000, 50, torch)
-        fps2 = 1000 / time_forward(ts2, 1000, 50, torch)
+                    flops_per_pair=FLOP_PER_PAIR[dom], flops_per_launch=FLOP_PER_PAIR[dom] * pairs,
+                    pairs_per_launch=pairs, us_per_launch=kt[dom], camera=0,
+                    frac_all_cameras=FLOP_PER_PAIR[dom] * all_pairs / (all_us * 1e-6) / 1e12
+                    / PEAK_FP32_TFLOPS,
+                    convention="algorithmic flops of the reference's GEMM form per (pixel, "
+                               "valid slot) pair (22 fwd / 44 bwd) x pairs of the launch / its "
+                               "HIP-event duration, camera 0; peak = MI355X FP32 157.3 TFLOP/s, "
+                               "attainable without packed FP32 instructions")
+    small = {} if args.no_small else small_configs(torch, scenes, TrainStep)
     extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
     extra_sh = {} if args.no_sh else run_sh(args, torch, scenes, kernels, TrainStep)
@@ -398,7 +603,7 @@ def main():
         torch.cuda.synchronize()
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(cfg, args.cpu_seconds, torch)
+        cpu = cpu_baseline(args, torch, scenes, kernels)
     out = {
         "metric": METRIC,
         "value": its,
@@ -424,12 +629,11 @@ def main():
             f"{cfg.name}_loss_after_steps": loss_last,
             "kernel_us": kt,
             "kernel_roofline": rows,
+            "splat_per_camera": per_cam,
             "overflow_tiles": int((ts.ncand > ts.K).sum()),
             "pairs_kept": int(ts.count.long().sum()),
             "candidates": int(ts.ncand.long().sum()),
-            "c2_train_its": its2,
-            "c2_fwd_fps": fps2,
-            "c2_note": "G=2000 128x128, bf16 render forward (matrix cores), fp32 params/Adam",
+            **small,
             **extra_c3,
             **extra_c5,
             **extra_sh,

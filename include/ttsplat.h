@@ -158,6 +158,13 @@ int tts_splat_fwd_theta(const float* theta, const float* col, const float* oc,
                         int H, int W, int S, int K, const float* bg,
                         float* image, float* den, hipStream_t stream);
 
+/* tts_splat_fwd_theta on bf16 operands: theta[T,6,K], col[T,K,3], oc[T,K] as bfloat16 (raw
+ * 16-bit patterns), the reference's device upload (`up`, tools/m4_train_binned.py:42-43, used by
+ * _DevRenderBinned.forward :154-166); arithmetic and outputs fp32. */
+int tts_splat_fwd_theta_bf16(const uint16_t* theta, const uint16_t* col, const uint16_t* oc,
+                             int H, int W, int S, int K, const float* bg, float* image,
+                             float* den, hipStream_t stream);
+
 /* Fused binned splat backward: given dL/dimage, recompute w per (pixel, slot), contract over
  * the tile's pixels per slot and apply the theta backward; each valid slot's 9 gradients are
  * stored to gslot[T,K,9] (entries of invalid slots are left untouched).  gwb, if not NULL,
@@ -177,6 +184,14 @@ int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc,
                         const float* image, const float* den, const float* gimage,
                         float* gtheta, float* gcol, float* goc, float* gwb,
                         hipStream_t stream);
+
+/* tts_splat_bwd_theta on bf16 operands (as tts_splat_fwd_theta_bf16): the backward of
+ * _DevRenderBinned (tools/m4_train_binned.py:168-186) on the reference's bf16 upload; fp32
+ * gradients out. */
+int tts_splat_bwd_theta_bf16(const uint16_t* theta, const uint16_t* col, const uint16_t* oc,
+                             int H, int W, int S, int K, const float* bg, const float* image,
+                             const float* den, const float* gimage, float* gtheta, float* gcol,
+                             float* goc, float* gwb, hipStream_t stream);
 
 /* Slot -> gaussian reduce: grad9[g] = sum over the gaussian's slots of gslot, gathered through
  * inv in stencil order (deterministic, no atomics).  Replaces the device gather-reduce
@@ -258,7 +273,14 @@ int tts_geom_bwd_accum(const float* params, int G, const float* camera, float ne
  * keo = keep * sigmoid(op) * sigmoid(beta (tau - z_cam)).  gdepth [G,2] receives each gaussian's
  * dL/d(beta, tau); tts_depth_weight_adam reduces it and updates (beta, tau).  As in the device
  * step no gradient reaches the means through z_cam, unless depth_zgrad (tts_geom_bwd_ex only) asks
- * for it (the dense arm-B autograd of spike/render.py). */
+ * for it (the dense arm-B autograd of spike/render.py).
+ *
+ * depth_zgrad of tts_geom_bwd_ex is a set of flags for the dense render's autograd
+ * (spike/render.py:14-49, where nothing is detached): TTS_GRAD_DEPTH_Z adds the gradient through
+ * z_cam in the depth weight, TTS_GRAD_SH_DIR the gradient of the SH colour through its view
+ * direction mean - centre (both into the means). */
+#define TTS_GRAD_DEPTH_Z 1
+#define TTS_GRAD_SH_DIR 2
 
 /* Geometry forward with SH colour and/or the depth weight.  Replaces the SHD > 0 and
  * --depth-weight branches of tools/resident_traced.py:327-346 (geom_fwd).

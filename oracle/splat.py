@@ -10,7 +10,8 @@ Restates
   spike/forward.py:61-66    poly_splat_wgeo = max(0, 1-Q/k)^2 (* keep)
   spike/arms.py:22-31       WSR blend, arm A: C = (sum w c + w_b c_b) / (sum w + w_b), w = o*w_geo
   spike/backward.py:11-20   wsr_polysplat_ref
-  spike/render.py:14-49     dense render, arms A, B, SZ, RV (spike/arms.py:34-83), SH degree 0
+  spike/render.py:14-49     dense render, arms A, B, SZ, RV (spike/arms.py:34-83), SH colour
+                            (spike/render.py:23-25, direction differentiable)
   tools/m4_train_binned.py:130-143  theta_u_gathered (per-tile origin fold, [T,6,K])
   tools/m4_train_binned.py:189-212  _operands (returns the 5-tuple it is meant to)
   tools/bh_views.py:65-71   binned forward: w = relu(einsum(Phi, theta))^2,
@@ -96,17 +97,25 @@ def blend_rv(W, color, c_b, eps=1e-6):
 
 
 def render_dense(P, cam, k=4.0, blur_eps=0.3, near=0.2, w_b_raw=-3.0, c_b=None, depth_bt=None,
-                 arm="A", softz_beta=None):
-    """Dense render of the [G,14] parameter set (spike/render.py:14-49, SH degree 0): arm "A";
-    with depth_bt = (depth_beta, depth_tau) arm B (spike/arms.py:34-37), the depth
-    differentiable as in spike's autograd; arm "SZ" (softz_beta) and "RV".  O(H*W*G) memory:
-    small images only."""
+                 arm="A", softz_beta=None, rest=None, sh_degree=0):
+    """Dense render of the [G,14] parameter set (spike/render.py:14-49): arm "A"; with
+    depth_bt = (depth_beta, depth_tau) arm B (spike/arms.py:34-37), the depth differentiable as
+    in spike's autograd; arm "SZ" (softz_beta) and "RV".  With sh_degree > 0 and rest [G,15,3]
+    the colour is the SH colour in the direction means3d - camera centre, that direction
+    differentiable too (spike/render.py:23-25, not detached there).  O(H*W*G) memory: small
+    images only."""
+    from . import sh
     pr = geometry.project_params(P, cam, blur_eps, near)
     dt = P.dtype
     px, py = geometry.pixel_grid(cam["H"], cam["W"], dtype=dt)
     Q = quad_form(px, py, pr["mu2d"], pr["conic"])
     w_geo = poly_splat_wgeo(Q, k, pr["keep"])
-    color = geometry.color_from_dc(P[:, 10:13])
+    if sh_degree > 0 and rest is not None:
+        centre = sh.camera_center(cam["R_v"].to(dt), cam["t_v"].to(dt))
+        coeffs = torch.cat([P[:, 10:13][:, None, :], rest], dim=1)
+        color = sh.eval_sh_color(sh_degree, coeffs, P[:, 0:3] - centre[None, :])
+    else:
+        color = geometry.color_from_dc(P[:, 10:13])
     o = torch.sigmoid(P[:, 13])
     if depth_bt is not None:
         o = o * torch.sigmoid(depth_bt[0] * (depth_bt[1] - pr["depth"]))

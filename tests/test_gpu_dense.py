@@ -188,3 +188,66 @@ def test_fit_reduces_loss_and_eval_psnr():
     print(f"[fit] loss {hist[0]:.4f} -> {hist[-1]:.4f}, psnr {p0:.2f} -> {p1:.2f}")
     assert hist[-1] < 0.8 * hist[0]
     assert p1 > p0
+
+
+@pytest.mark.parametrize("arm,deg", [("A", 1), ("A", 3), ("B", 2), ("SZ", 3), ("RV", 3)])
+def test_render_dense_view_dependent_colour(arm, deg):
+    """spike/render.py with sh_degree > 0 (:23-25): SH colour in the direction means - centre,
+    its gradient reaching the means through that direction, rest coefficients trained."""
+    cfg, P, cam = config_inputs("c1_ref", G=600)
+    g = torch.Generator().manual_seed(deg)
+    rest = torch.randn(P.shape[0], 15, 3, generator=g) * 0.3
+    print(f"[dense-sh] arm {arm} degree {deg}", flush=True)
+    model = GaussianModel(P.cuda(), color_rest=rest.cuda())
+    model.params.requires_grad_(True)
+    model.color_rest.requires_grad_(True)
+    img = trender.render(model, cam, arm, k=4.0, sh_degree=deg)
+    R = torch.randn(cam.H, cam.W, 3, generator=torch.Generator().manual_seed(7))
+    (img * R.cuda()).sum().backward()
+    Pr = P.double().clone().requires_grad_(True)
+    rr = rest.double().clone().requires_grad_(True)
+    camd = {n: (v.double() if torch.is_tensor(v) else v) for n, v in cam_dict(cam).items()}
+    kw = dict(k=4.0, rest=rr, sh_degree=deg)
+    if arm == "B":
+        kw["depth_bt"] = torch.tensor([1.0, 3.0], dtype=torch.float64)
+    if arm == "SZ":
+        kw["softz_beta"] = torch.tensor(4.0, dtype=torch.float64)
+    ref = osplat.render_dense(Pr, camd, arm="A" if arm == "B" else arm, **kw)
+    err = max_abs(img, ref)
+    assert err <= 1e-4, err
+    (ref * R.double()).sum().backward()
+    for gname, sl in GROUPS.items():
+        e = rel_l2(model.params.grad[:, sl], Pr.grad[:, sl])
+        print(f"[dense-sh] {arm} deg {deg} d{gname}: rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-3, gname
+    n = (deg + 1) ** 2 - 1
+    assert rel_l2(model.color_rest.grad[:, :n], rr.grad[:, :n]) <= 1e-3
+    if n < 15:       # rows beyond the degree take no gradient
+        assert float(model.color_rest.grad[:, n:].abs().max()) == 0.0
+
+
+def test_fit_with_view_dependent_colour():
+    """fit(..., sh_degree=2): the rest coefficients train (Adam at lr color / 20, spike/model.py:91)
+    and the loss falls; one step equals Adam on the oracle's gradient."""
+    cfg, P, cam = config_inputs("c1_ref", G=400)
+    rest = torch.zeros(P.shape[0], 15, 3)
+    tgt_model = GaussianModel(cfg.params(seed=1)[:400].cuda(),
+                              color_rest=torch.randn(400, 15, 3, generator=torch.Generator()
+                                                     .manual_seed(3)).cuda() * 0.2)
+    with torch.no_grad():
+        tgt = trender.render(tgt_model, cam, "A", sh_degree=2)
+    model = GaussianModel(P.cuda(), color_rest=rest.cuda())
+    hist = ttrain.fit(model, [cam], [tgt], "A", iters=1, sh_degree=2)
+    # oracle: one Adam step (first step: p -= lr * sign(g)) on the rest block
+    rr = rest.double().clone().requires_grad_(True)
+    camd = {n: (v.double() if torch.is_tensor(v) else v) for n, v in cam_dict(cam).items()}
+    ref = osplat.render_dense(P.double(), camd, k=4.0, rest=rr, sh_degree=2)
+    oloss.loss_fn(ref, tgt.cpu().double()).backward()
+    lr_rest = ttrain.DEFAULT_LR["color"] / 20.0
+    step = model.color_rest.cpu().double() - rest.double()
+    exp = -lr_rest * rr.grad / (rr.grad.abs() + 1e-8)      # Adam's first step, eps = 1e-8
+    big = rr.grad.abs() > 1e-5
+    assert int(big.sum()) > 100
+    assert torch.allclose(step[big], exp[big], rtol=1e-3, atol=1e-9)
+    hist += ttrain.fit(model, [cam], [tgt], "A", iters=30, sh_degree=2)
+    assert hist[-1] < 0.9 * hist[0]

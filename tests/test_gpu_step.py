@@ -185,3 +185,38 @@ def test_train_step_with_everything_culled():
     assert float(eager.m.abs().max()) == 0.0
     assert abs(float(eager.loss()) - float(graph.loss())) == 0.0
     assert int(graph.step_block[0]) == 3
+
+
+def test_bin_every_reuses_bins_between_rebins():
+    """bin_every = 5 (tools/resident_traced.py:103,683): the bin table is rebuilt on steps 0, 5,
+    10, ... only; in between the step runs on the last table.  Graph replay equals eager, and a
+    reused-bin step equals the oracle's step on those (stale) bins."""
+    cfg, P, cam = config_inputs("c1_ref")
+    tgt = target_for(cfg, cam)
+    eager = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5, keep_grad=True)
+    graph = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5)
+    graph.capture()
+    assert set(graph.graphs) == {(0, True), (0, False)}
+    rebinned = []
+    for i in range(7):
+        eager.count.fill_(-1)           # the binning kernels rewrite it; a reused table leaves it
+        graph.count.fill_(-1)
+        if i == 3:
+            Pb = eager.P.cpu().clone()
+        eager.step(0)
+        graph.step(0)
+        torch.cuda.synchronize()
+        rebinned.append((int(eager.count.min()) >= 0, int(graph.count.min()) >= 0))
+        assert abs(float(eager.loss()) - float(graph.loss())) <= 1e-5 * max(1.0, float(eager.loss()))
+        if i == 3:      # a reused-bin step against the oracle on the same (stale) bins
+            tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+            bins = (eager.idx.cpu().long(), eager.valid.cpu().bool())
+            img, L, g, _ = opipe.render_and_grad(Pb, cam_dict(cam), tmap, tgt.cpu(), K=cfg.K,
+                                                 k=cfg.k, bins=bins)
+            assert float((eager.image.cpu() - img).abs().max()) <= 1e-4
+            assert rel_l2(eager.gparams.cpu(), g) <= 1e-3
+    assert [e for e, _ in rebinned] == [True, False, False, False, False, True, False]
+    assert [g for _, g in rebinned] == [True, False, False, False, False, True, False]
+    assert rel_l2(graph.P, eager.P) <= 1e-3
+    with pytest.raises(ValueError):
+        TrainStep(P, [cam, cam], [tgt, tgt], K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5, batch=2)

@@ -74,8 +74,8 @@ def test_render_rejects_arms_off_the_hip_path():
         with pytest.raises(NotImplementedError):
             render.render(None, None, arm)
     assert render.ARMS == ("A", "B", "SZ", "RV")
-    with pytest.raises(NotImplementedError):
-        render.render(None, None, "A", sh_degree=1)
+    with pytest.raises(ValueError):             # SH degree outside [0, 3]
+        render.render(None, None, "A", sh_degree=4)
     assert train.DEFAULT_LR["means"] == 5e-3 and train.DEFAULT_LR["wb"] == 1e-2
 
 

@@ -55,7 +55,8 @@ struct DepthW {
   float* grad;       // [G,2] per-gaussian dL/d(beta, tau), or null
   float scale;       // grad (+)= scale * value
   int accumulate;    // 1: grad += ..., 0: grad = ...
-  int zgrad;         // 1: dL/dz_cam through rho reaches the means
+  int zgrad;         // TTS_GRAD_DEPTH_Z: dL/dz_cam through rho reaches the means; TTS_GRAD_SH_DIR
+                     // (k_geom_bwd): the SH colour's gradient through its direction too
 };
 __device__ __forceinline__ void depthw_store(const DepthW& d, int g, const float* v) {
   if (!d.bt || !d.grad) return;
@@ -175,6 +176,56 @@ __device__ __forceinline__ void sh_basis(const float* __restrict__ p, const Came
   b[13] = kSC3[4] * x * (4.0f * zz - xx - yy);
   b[14] = kSC3[5] * z * (xx - yy);
   b[15] = kSC3[6] * x * (xx - 3.0f * yy);
+}
+
+// Gradient through the view direction (spike's dense autograd, spike/render.py:23-25: the
+// direction d = mean - centre is not detached there).  gcol[c] = dL/d(raw colour c) after the
+// clamp gate; gd_hat = sum_l grad b_l(d_hat) * sum_c gcol[c] rest_l,c, then through
+// d_hat = d / max(|d|, 1e-12): dL/dd = (gd_hat - d_hat (d_hat . gd_hat)) / |d| (or gd_hat / 1e-12
+// where the clamp holds).  Added to dL/dmeans.
+__device__ __forceinline__ void sh_dir_grad(const float* __restrict__ p, const Camera& cam,
+                                            const float* rv, int n, const float* gcol,
+                                            float* gmean) {
+  float d[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+    d[i] = p[i] + (cam.R[0 * 3 + i] * cam.t[0] + cam.R[1 * 3 + i] * cam.t[1] +
+                   cam.R[2 * 3 + i] * cam.t[2]);
+  const float raw = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+  const float nrm = fmaxf(raw, 1e-12f);
+  const float x = d[0] / nrm, y = d[1] / nrm, z = d[2] / nrm;
+  const float xx = x * x, yy = y * y, zz = z * z, xy = x * y, yz = y * z, xz = x * z;
+  float a[kShRest];  // sum_c gcol[c] rest_l,c
+#pragma unroll
+  for (int l = 0; l < kShRest; ++l)
+    a[l] = l < n ? gcol[0] * rv[l * 3 + 0] + gcol[1] * rv[l * 3 + 1] + gcol[2] * rv[l * 3 + 2]
+                 : 0.0f;
+  // grad of b_{l+1} w.r.t. (x, y, z), times a[l]
+  float gx = -kSC1 * a[2], gy = -kSC1 * a[0], gz = kSC1 * a[1];
+  gx += kSC2[0] * y * a[3] + (-2.0f * kSC2[2] * x) * a[5] + kSC2[3] * z * a[6] +
+        2.0f * kSC2[4] * x * a[7];
+  gy += kSC2[0] * x * a[3] + kSC2[1] * z * a[4] + (-2.0f * kSC2[2] * y) * a[5] -
+        2.0f * kSC2[4] * y * a[7];
+  gz += kSC2[1] * y * a[4] + 4.0f * kSC2[2] * z * a[5] + kSC2[3] * x * a[6];
+  gx += 6.0f * kSC3[0] * xy * a[8] + kSC3[1] * yz * a[9] - 2.0f * kSC3[2] * xy * a[10] -
+        6.0f * kSC3[3] * xz * a[11] + kSC3[4] * (4.0f * zz - 3.0f * xx - yy) * a[12] +
+        2.0f * kSC3[5] * xz * a[13] + kSC3[6] * (3.0f * xx - 3.0f * yy) * a[14];
+  gy += kSC3[0] * (3.0f * xx - 3.0f * yy) * a[8] + kSC3[1] * xz * a[9] +
+        kSC3[2] * (4.0f * zz - xx - 3.0f * yy) * a[10] - 6.0f * kSC3[3] * yz * a[11] -
+        2.0f * kSC3[4] * xy * a[12] - 2.0f * kSC3[5] * yz * a[13] - 6.0f * kSC3[6] * xy * a[14];
+  gz += kSC3[1] * xy * a[9] + 8.0f * kSC3[2] * yz * a[10] +
+        kSC3[3] * (6.0f * zz - 3.0f * xx - 3.0f * yy) * a[11] + 8.0f * kSC3[4] * xz * a[12] +
+        kSC3[5] * (xx - yy) * a[13];
+  if (raw > 1e-12f) {
+    const float dot = x * gx + y * gy + z * gz;
+    gmean[0] += (gx - x * dot) / nrm;
+    gmean[1] += (gy - y * dot) / nrm;
+    gmean[2] += (gz - z * dot) / nrm;
+  } else {
+    gmean[0] += gx / nrm;
+    gmean[1] += gy / nrm;
+    gmean[2] += gz / nrm;
+  }
 }
 
 // Loads this gaussian's first n rest coefficients of each channel (rv[l * 3 + c]).
@@ -519,7 +570,8 @@ __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ para
   float gin[9], gout[14], gcol[3], gdw[2];
 #pragma unroll
   for (int i = 0; i < 9; ++i) gin[i] = grad9[(int64_t)g * 9 + i];
-  geo_backward(p, cam, s, gin, gout, gcol, gdw, dwa.zgrad != 0);
+  geo_backward(p, cam, s, gin, gout, gcol, gdw, (dwa.zgrad & TTS_GRAD_DEPTH_Z) != 0);
+  if (SH && (dwa.zgrad & TTS_GRAD_SH_DIR)) sh_dir_grad(p, cam, rv, n_rest, gcol, gout);
 #pragma unroll
   for (int i = 0; i < 14; ++i) gparams[(int64_t)g * 14 + i] = gout[i];
   depthw_store(dwa, g, gdw);
@@ -952,7 +1004,7 @@ int tts_geom_bwd_ex(const float* params, const float* sh_rest, int sh_degree,
   if (sh_degree > 0 && !gsh_rest) return TTS_EINVAL;
   if (G >= (1 << 30)) return TTS_EG;
   if (G == 0) return TTS_OK;
-  const DepthW dwa{depth_bt, gdepth, 1.0f, 0, depth_zgrad ? 1 : 0};
+  const DepthW dwa{depth_bt, gdepth, 1.0f, 0, depth_zgrad & (TTS_GRAD_DEPTH_Z | TTS_GRAD_SH_DIR)};
   const dim3 grid = grid1d(G, 256);
   if (sh_degree > 0)
     k_geom_bwd<true><<<grid, 256, 0, stream>>>(params, G, sh_rest, sh_rest_count(sh_degree), dwa,

@@ -117,28 +117,34 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
   return base;
 }
 
-// Load pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K] (all K slots).
-__device__ __forceinline__ void load_slots_theta(const float* __restrict__ theta,
-                                                 const float* __restrict__ col,
-                                                 const float* __restrict__ oc, int t, int K,
+__device__ __forceinline__ float opf(float x) { return x; }
+__device__ __forceinline__ float opf(__bf16 x) { return (float)x; }
+
+// Load pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K] (all K slots); OT = float, or
+// __bf16 for the reference's bf16 operand upload (tools/m4_train_binned.py:42-43), widened to
+// fp32 here.
+template <typename OT>
+__device__ __forceinline__ void load_slots_theta(const OT* __restrict__ theta,
+                                                 const OT* __restrict__ col,
+                                                 const OT* __restrict__ oc, int t, int K,
                                                  SlotLDS sl, bool* bad) {
-  const float* th = theta + (int64_t)t * 6 * K;
+  const OT* th = theta + (int64_t)t * 6 * K;
   for (int s = threadIdx.x; s < K; s += blockDim.x) {
-    sl.ta[s] = make_float4(th[s], th[K + s], th[2 * K + s], th[3 * K + s]);
-    sl.tb[s] = make_float4(th[4 * K + s], th[5 * K + s], 0.0f, 0.0f);
+    sl.ta[s] = make_float4(opf(th[s]), opf(th[K + s]), opf(th[2 * K + s]), opf(th[3 * K + s]));
+    sl.tb[s] = make_float4(opf(th[4 * K + s]), opf(th[5 * K + s]), 0.0f, 0.0f);
     *bad = *bad || theta_poisons(sl.ta[s], sl.tb[s]);
-    const float* c = col + ((int64_t)t * K + s) * 3;
-    sl.cl[s] = make_float4(c[0], c[1], c[2], oc[(int64_t)t * K + s]);
+    const OT* c = col + ((int64_t)t * K + s) * 3;
+    sl.cl[s] = make_float4(opf(c[0]), opf(c[1]), opf(c[2]), opf(oc[(int64_t)t * K + s]));
     sl.gid[s] = s;
     sl.sid[s] = s;
   }
 }
 
-template <int S, bool FROM_PROJ>
+template <int S, bool FROM_PROJ, typename OT = float>
 __global__ __launch_bounds__(256) void k_splat_fwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
-    const uint8_t* __restrict__ valid, const float* __restrict__ theta,
-    const float* __restrict__ col, const float* __restrict__ oc,
+    const uint8_t* __restrict__ valid, const OT* __restrict__ theta,
+    const OT* __restrict__ col, const OT* __restrict__ oc,
     const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
     const float* __restrict__ bg, float* __restrict__ image, float* __restrict__ den_out) {
   constexpr int PPT = S * S / 256;  // pixels per thread
@@ -312,11 +318,11 @@ __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const flo
   }
 }
 
-template <int S, bool FROM_PROJ>
+template <int S, bool FROM_PROJ, typename OT = float>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_splat_bwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
-    const uint8_t* __restrict__ valid, const float* __restrict__ theta,
-    const float* __restrict__ col, const float* __restrict__ oc,
+    const uint8_t* __restrict__ valid, const OT* __restrict__ theta,
+    const OT* __restrict__ col, const OT* __restrict__ oc,
     const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
     const float* __restrict__ bg, const float* __restrict__ image,
     const float* __restrict__ den, const float* __restrict__ gimage, float* __restrict__ gslot,
@@ -731,9 +737,9 @@ inline size_t bwd_lds(int K, int S) {
   return a + (size_t)S * (S + 1) * 16;
 }
 
-template <bool FROM_PROJ>
-int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
-               const float* col, const float* oc, const int32_t* order, int H, int W, int S, int K,
+template <bool FROM_PROJ, typename OT = float>
+int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, const OT* theta,
+               const OT* col, const OT* oc, const int32_t* order, int H, int W, int S, int K,
                float k,
                const float* bg, float* image, float* den, hipStream_t stream) {
   const int ntx = W / S, T = (H / S) * ntx;
@@ -742,17 +748,17 @@ int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, cons
     k_splat_fwd_mf<<<T, 256, fwd_mf_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K, inv_k,
                                                        bg, image, den);
   else if (S == 16)
-    k_splat_fwd<16, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(
+    k_splat_fwd<16, FROM_PROJ, OT><<<T, 256, fwd_lds(K), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
   else
-    k_splat_fwd<32, FROM_PROJ><<<T, 256, fwd_lds(K), stream>>>(
+    k_splat_fwd<32, FROM_PROJ, OT><<<T, 256, fwd_lds(K), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
   return launch_status();
 }
 
-template <bool FROM_PROJ>
-int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, const float* theta,
-               const float* col, const float* oc, const int32_t* order, int H, int W, int S, int K,
+template <bool FROM_PROJ, typename OT = float>
+int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, const OT* theta,
+               const OT* col, const OT* oc, const int32_t* order, int H, int W, int S, int K,
                float k,
                const float* bg, const float* image, const float* den, const float* gimage,
                float* gslot, float* gtheta, float* gcol, float* goc, float* gwb,
@@ -760,11 +766,11 @@ int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, cons
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16)
-    k_splat_bwd<16, FROM_PROJ><<<T, 256, bwd_lds(K, 16), stream>>>(
+    k_splat_bwd<16, FROM_PROJ, OT><<<T, 256, bwd_lds(K, 16), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
         gtheta, gcol, goc, gwb);
   else
-    k_splat_bwd<32, FROM_PROJ><<<T, 256, bwd_lds(K, 32), stream>>>(
+    k_splat_bwd<32, FROM_PROJ, OT><<<T, 256, bwd_lds(K, 32), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
         gtheta, gcol, goc, gwb);
   return launch_status();
@@ -794,7 +800,7 @@ int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
   const int e = check_tile(H, W, S, K);
   if (e) return e;
   if (!proj || !idx || !valid || !bg || !image) return TTS_EINVAL;
-  return launch_fwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
+  return launch_fwd<true, float>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
                           image, den, stream);
 }
 
@@ -833,7 +839,7 @@ int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
   const int e = check_tile(H, W, S, K);
   if (e) return e;
   if (!proj || !idx || !valid || !bg || !image || !den || !gimage || !gslot) return TTS_EINVAL;
-  return launch_bwd<true>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
+  return launch_bwd<true, float>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
                           image, den, gimage, gslot, nullptr, nullptr, nullptr, gwb, stream);
 }
 
@@ -847,6 +853,35 @@ int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc, i
     return TTS_EINVAL;
   return launch_bwd<false>(nullptr, nullptr, nullptr, theta, col, oc, nullptr, H, W, S, K, 1.0f,
                            bg, image, den, gimage, nullptr, gtheta, gcol, goc, gwb, stream);
+}
+
+int tts_splat_fwd_theta_bf16(const uint16_t* theta, const uint16_t* col, const uint16_t* oc,
+                             int H, int W, int S, int K, const float* bg, float* image,
+                             float* den, hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!theta || !col || !oc || !bg || !image) return TTS_EINVAL;
+  return launch_fwd<false, __bf16>(nullptr, nullptr, nullptr,
+                                   reinterpret_cast<const __bf16*>(theta),
+                                   reinterpret_cast<const __bf16*>(col),
+                                   reinterpret_cast<const __bf16*>(oc), nullptr, H, W, S, K, 1.0f,
+                                   bg, image, den, stream);
+}
+
+int tts_splat_bwd_theta_bf16(const uint16_t* theta, const uint16_t* col, const uint16_t* oc,
+                             int H, int W, int S, int K, const float* bg, const float* image,
+                             const float* den, const float* gimage, float* gtheta, float* gcol,
+                             float* goc, float* gwb, hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (!theta || !col || !oc || !bg || !image || !den || !gimage || !gtheta || !gcol || !goc)
+    return TTS_EINVAL;
+  return launch_bwd<false, __bf16>(nullptr, nullptr, nullptr,
+                                   reinterpret_cast<const __bf16*>(theta),
+                                   reinterpret_cast<const __bf16*>(col),
+                                   reinterpret_cast<const __bf16*>(oc), nullptr, H, W, S, K, 1.0f,
+                                   bg, image, den, gimage, nullptr, gtheta, gcol, goc, gwb,
+                                   stream);
 }
 
 }  // extern "C"

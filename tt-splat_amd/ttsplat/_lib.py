@@ -37,6 +37,10 @@ SIGNATURES = {
                                      _vp, _vp]),
     "tts_splat_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tts_splat_fwd_theta_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                          _vp, _vp, _vp]),
+    "tts_splat_bwd_theta_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_splat_bwd_theta": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
                                      _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_loss_workspace_bytes": (_c_size, [_c_int, _c_int]),

@@ -119,38 +119,55 @@ def _operands(model, cam, tmap, R=1, K=128, cached_bins=None, k=K_POLY):
     return th, col, oc[..., None], w_b, bins
 
 
+def _dev_render_forward(ctx, operand_dtype, theta_u, color_o, o_col, w_b, Phi, H, W):
+    S = int(round(Phi.shape[0] ** 0.5))
+    dev = theta_u.device
+    bg = torch.cat([torch.as_tensor(w_b, dtype=F32, device=dev).reshape(1),
+                    torch.as_tensor(ctx.c_b, dtype=F32, device=dev).reshape(3)]).contiguous()
+    dt = torch.bfloat16 if theta_u.dtype == torch.bfloat16 else operand_dtype
+    th = theta_u.detach().to(dt).contiguous()
+    col = color_o.detach().to(dt).contiguous()
+    oc = o_col.detach().to(dt).reshape(th.shape[0], th.shape[2]).contiguous()
+    img, den = kernels.splat_fwd_theta(th, col, oc, bg, H, W, S)
+    ctx.save_for_backward(th, col, oc, bg, img, den)
+    ctx.meta = (H, W, S, o_col.shape, theta_u.dtype, color_o.dtype, o_col.dtype)
+    return img
+
+
 class DevRenderBinned(torch.autograd.Function):
     """Splat forward/backward on pre-gathered operands (tools/m4_train_binned.py:154-186).
 
     forward(theta_u[T,6,K], color_o[T,K,3], o_col[T,K,1], w_b, Phi, gidx, c_b, H, W) -> img[H,W,3];
     backward returns (gtheta_u, gcolor_o, go_col, gw_b).  Phi/gidx describe the tile map
-    (only its tile side is used: the kernel evaluates Phi itself)."""
+    (only its tile side is used: the kernel evaluates Phi itself).  fp32 operands (bf16 input
+    tensors run the bf16 entry points); gradients come back in each input's dtype."""
 
     @staticmethod
     def forward(ctx, theta_u, color_o, o_col, w_b, Phi, gidx, c_b, H, W):
-        S = int(round(Phi.shape[0] ** 0.5))
-        dev = theta_u.device
-        bg = torch.cat([torch.as_tensor(w_b, dtype=F32, device=dev).reshape(1),
-                        torch.as_tensor(c_b, dtype=F32, device=dev).reshape(3)]).contiguous()
-        th = theta_u.detach().float().contiguous()
-        col = color_o.detach().float().contiguous()
-        oc = o_col.detach().float().reshape(th.shape[0], th.shape[2]).contiguous()
-        img, den = kernels.splat_fwd_theta(th, col, oc, bg, H, W, S)
-        ctx.save_for_backward(th, col, oc, bg, img, den)
-        ctx.meta = (H, W, S, o_col.shape)
-        return img
+        ctx.c_b = c_b
+        return _dev_render_forward(ctx, F32, theta_u, color_o, o_col, w_b, Phi, H, W)
 
     @staticmethod
     def backward(ctx, gimg):
         th, col, oc, bg, img, den = ctx.saved_tensors
-        H, W, S, oc_shape = ctx.meta
+        H, W, S, oc_shape, dth, dcol, doc = ctx.meta
         gwb = torch.empty(th.shape[0], device=th.device, dtype=F32)
         gth, gcol, goc = kernels.splat_bwd_theta(th, col, oc, bg, H, W, S, img, den,
                                                  gimg.float().contiguous(), gwb)
-        return gth, gcol, goc.reshape(oc_shape), gwb.sum(), None, None, None, None, None
+        return (gth.to(dth), gcol.to(dcol), goc.reshape(oc_shape).to(doc), gwb.sum(), None, None,
+                None, None, None)
 
 
-_DevRenderBinned = DevRenderBinned
+class _DevRenderBinned(DevRenderBinned):
+    """The reference's own class (tools/m4_train_binned.py:154-186): operands uploaded as bf16
+    (`up`, :42-43), the bf16 render variant; fp32 arithmetic on the bf16-rounded operands.  The
+    rounding of theta loses precision as in the reference (:36): 3.6e-2 rel L2 against fp32
+    operands on the 128x128 64-tile scene."""
+
+    @staticmethod
+    def forward(ctx, theta_u, color_o, o_col, w_b, Phi, gidx, c_b, H, W):
+        ctx.c_b = c_b
+        return _dev_render_forward(ctx, torch.bfloat16, theta_u, color_o, o_col, w_b, Phi, H, W)
 
 
 class BinnedRender(torch.autograd.Function):

@@ -89,11 +89,12 @@ def geom_fwd(params, camera, near=NEAR, blur=BLUR, proj=None, keep=None, sh_rest
 
 
 def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None, sh_rest=None, sh_degree=0,
-             gsh_out=None, depth_bt=None, depth_zgrad=False, gdepth=None):
+             gsh_out=None, depth_bt=None, depth_zgrad=False, gdepth=None, sh_dirgrad=False):
     """grad9[G,9] -> dL/dparams[G,14].  With sh_degree > 0 also dL/dsh_rest [15,3,G]; with
     depth_bt also dL/d(beta, tau) per gaussian [G,2] (depth_zgrad: plus the gradient through
-    z_cam into the means).  Returns gparams, or a tuple (gparams, gsh, gdepth) when either
-    extension is on (absent parts None)."""
+    z_cam into the means; sh_dirgrad: plus the SH colour's gradient through its view direction
+    into the means, as spike's dense autograd has them).  Returns gparams, or a tuple
+    (gparams, gsh, gdepth) when either extension is on (absent parts None)."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
@@ -112,9 +113,10 @@ def geom_bwd(params, camera, grad9, near=NEAR, blur=BLUR, out=None, sh_rest=None
         if depth_bt is not None:
             gdw = torch.empty(G, 2, device=dev, dtype=F32) if gdepth is None else gdepth
             require(gdw, "gdepth", F32, (G, 2), dev)
+        flags = (1 if depth_zgrad else 0) | (2 if sh_dirgrad and sh_degree > 0 else 0)
         call("tts_geom_bwd_ex", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt),
-             int(bool(depth_zgrad)), G, ptr(camera), near, blur, ptr(grad9), ptr(out), ptr(gsh),
-             ptr(gdw), stream())
+             flags, G, ptr(camera), near, blur, ptr(grad9), ptr(out), ptr(gsh), ptr(gdw),
+             stream())
         return out, gsh, gdw
     call("tts_geom_bwd", ptr(params), G, ptr(camera), near, blur, ptr(grad9), ptr(out), stream())
     return out
@@ -283,40 +285,49 @@ def slot_scatter(gslot, idx, valid, G, grad9=None):
     return grad9
 
 
-def splat_fwd_theta(theta, col, oc, bg, H, W, S, image=None, den=None):
+def _theta_operands(theta, col, oc, H, W, S):
+    """Checked operand triple; fp32 or bf16 (all three the same): returns (T, K, suffix)."""
     dev = theta.device
     T = (H // S) * (W // S)
     K = theta.shape[-1]
-    require(theta, "theta", F32, (T, 6, K))
-    require(col, "col", F32, (T, K, 3), dev)
-    require(oc, "oc", F32, (T, K), dev)
+    dt = theta.dtype
+    if dt not in (F32, torch.bfloat16):
+        raise ValueError(f"theta must be float32 or bfloat16, got {dt}")
+    require(theta, "theta", dt, (T, 6, K))
+    require(col, "col", dt, (T, K, 3), dev)
+    require(oc, "oc", dt, (T, K), dev)
+    return T, K, ("_bf16" if dt == torch.bfloat16 else "")
+
+
+def splat_fwd_theta(theta, col, oc, bg, H, W, S, image=None, den=None):
+    """Splat forward from pre-gathered operands theta[T,6,K], col[T,K,3], oc[T,K]: fp32, or
+    bf16 (the reference's operand upload, tools/m4_train_binned.py:42-43; fp32 arithmetic)."""
+    dev = theta.device
+    T, K, sfx = _theta_operands(theta, col, oc, H, W, S)
     require(bg, "bg", F32, (4,), dev)
     image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
     den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
-    call("tts_splat_fwd_theta", ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg), ptr(image),
-         ptr(den), stream())
+    call("tts_splat_fwd_theta" + sfx, ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg),
+         ptr(image), ptr(den), stream())
     return image, den
 
 
 def splat_bwd_theta(theta, col, oc, bg, H, W, S, image, den, gimage, gwb=None):
-    """Per-slot gtheta, gcol, goc; gwb[T] (optional) gets per-tile dL/dw_b partials."""
+    """Per-slot gtheta, gcol, goc (fp32, whatever the operand type); gwb[T] (optional) gets
+    per-tile dL/dw_b partials."""
     dev = theta.device
-    T = (H // S) * (W // S)
-    K = theta.shape[-1]
-    require(theta, "theta", F32, (T, 6, K))
-    require(col, "col", F32, (T, K, 3), dev)
-    require(oc, "oc", F32, (T, K), dev)
+    T, K, sfx = _theta_operands(theta, col, oc, H, W, S)
     require(bg, "bg", F32, (4,), dev)
     require(image, "image", F32, (H, W, 3), dev)
     require(den, "den", F32, (H, W), dev)
     require(gimage, "gimage", F32, (H, W, 3), dev)
     if gwb is not None:
         require(gwb, "gwb", F32, (T,), dev)
-    gtheta = torch.empty_like(theta)
-    gcol = torch.empty_like(col)
-    goc = torch.empty_like(oc)
-    call("tts_splat_bwd_theta", ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg), ptr(image),
-         ptr(den), ptr(gimage), ptr(gtheta), ptr(gcol), ptr(goc), ptr(gwb), stream())
+    gtheta = torch.empty(theta.shape, device=dev, dtype=F32)
+    gcol = torch.empty(col.shape, device=dev, dtype=F32)
+    goc = torch.empty(oc.shape, device=dev, dtype=F32)
+    call("tts_splat_bwd_theta" + sfx, ptr(theta), ptr(col), ptr(oc), H, W, S, K, ptr(bg),
+         ptr(image), ptr(den), ptr(gimage), ptr(gtheta), ptr(gcol), ptr(goc), ptr(gwb), stream())
     return gtheta, gcol, goc
 
 

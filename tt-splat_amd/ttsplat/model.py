@@ -16,10 +16,12 @@ PN = ("mx", "my", "mz", "qw", "qx", "qy", "qz", "lx", "ly", "lz", "cr", "cg", "c
 
 class GaussianModel:
     """depth_beta, depth_tau: the global depth-weight scalars of arm B; softz_beta: the gate
-    sharpness of arm SZ (spike/model.py:48-50 defaults 1.0, 3.0 and 4.0)."""
+    sharpness of arm SZ (spike/model.py:48-50 defaults 1.0, 3.0 and 4.0).  color_rest: the SH
+    rest coefficients [G,15,3] of view-dependent colour (spike/model.py:45), or None (DC colour
+    only; the reference keeps a zero tensor there)."""
 
     def __init__(self, params, w_b_raw=-3.0, c_b=(1.0, 1.0, 1.0), depth_beta=1.0, depth_tau=3.0,
-                 softz_beta=4.0):
+                 softz_beta=4.0, color_rest=None):
         if params.dim() != 2 or params.shape[1] != 14:
             raise ValueError(f"params must be [G,14], got {tuple(params.shape)}")
         self.params = params.float().contiguous()
@@ -29,13 +31,21 @@ class GaussianModel:
         self.depth_beta = torch.tensor(float(depth_beta), device=dev)
         self.depth_tau = torch.tensor(float(depth_tau), device=dev)
         self.softz_beta = torch.tensor(float(softz_beta), device=dev)
+        self.color_rest = None
+        if color_rest is not None:
+            cr = torch.as_tensor(color_rest, dtype=torch.float32, device=dev)
+            if tuple(cr.shape) != (self.params.shape[0], 15, 3):
+                raise ValueError(f"color_rest must be [G,15,3], got {tuple(cr.shape)}")
+            self.color_rest = cr.contiguous()
 
     @classmethod
     def from_reference(cls, model, device="cuda"):
         """Pack a spike-style model (separate tensors) into the [G,14] block."""
         P = torch.cat([model.means3d.detach(), model.quats.detach(), model.log_scales.detach(),
                        model.color_dc.detach(), model.opacity_raw.detach().reshape(-1, 1)], 1)
-        return cls(P.to(device), float(model.w_b_raw), model.c_b.detach().cpu())
+        rest = getattr(model, "color_rest", None)
+        return cls(P.to(device), float(model.w_b_raw), model.c_b.detach().cpu(),
+                   color_rest=None if rest is None else rest.detach().to(device))
 
     @property
     def G(self):

@@ -60,7 +60,12 @@ class TrainStep:
     step (learning rate lr_bt) after every step; tau0 = None uses the median camera depth of
     the gaussians camera 0 keeps, as the reference refines it at warm-up.
     keep_grad = True (batch = 1): the fused backward also stores each step's dL/dparams [G,14]
-    in self.gparams (the gradient Adam was given)."""
+    in self.gparams (the gradient Adam was given).
+    bin_every = N (batch = 1): the reference trainer's bin cadence (--bin-every, default 5 there,
+    tools/resident_traced.py:103,683): step() rebins only on steps whose running count is a
+    multiple of N (and on the step after an MCMC relocation); the other steps run geometry,
+    splat, loss, backward and Adam on the bins last computed -- one bin table for all cameras,
+    as in that trainer.  Each camera gets a graph with and one without the binning kernels."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
@@ -69,7 +74,7 @@ class TrainStep:
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
                  dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None,
-                 depth_weight=None, keep_grad=False):
+                 depth_weight=None, keep_grad=False, bin_every=1):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -161,6 +166,12 @@ class TrainStep:
         self.gparams = torch.zeros(G, 14, device=dev, dtype=F32) if keep_grad else None
         self.gacc_sh = (torch.zeros_like(self.sh) if self.batch > 1 and self.sh_degree > 0
                         else None)
+        self.bin_every = int(bin_every)
+        if self.bin_every < 1:
+            raise ValueError(f"bin_every must be >= 1, got {bin_every}")
+        if self.bin_every > 1 and self.batch > 1:
+            raise ValueError("bin_every > 1 reuses one bin table across steps: batch must be 1")
+        self._force_rebin = False
         self.graphs = {}
 
     @property
@@ -169,15 +180,17 @@ class TrainStep:
         return None if self.sh is None else kernels.sh_rest_model(self.sh)
 
     # ---------------------------------------------------------------------------------
-    def forward(self, ci=0, advance=False):
+    def forward(self, ci=0, advance=False, rebin=True):
         """Geometry + binning + fused splat for camera ci into self.image.  advance=True: the
-        geometry launch also advances the Adam step block (a training step's first kernel)."""
+        geometry launch also advances the Adam step block (a training step's first kernel).
+        rebin=False: the bins last computed are reused (the binning kernels are not run)."""
         kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep, sh_rest=self.sh,
                          sh_degree=self.sh_degree, depth_bt=self.dw,
                          advance=self.step_block if advance else None)
-        kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
-                            self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
-                            self.ncand, self.inv, self.order)
+        if rebin:
+            kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
+                                self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
+                                self.ncand, self.inv, self.order)
         if self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
@@ -191,21 +204,22 @@ class TrainStep:
         """Number of distinct steps (views for batch = 1, batches otherwise)."""
         return len(self.cams) // self.batch
 
-    def _view_backward(self, ci, advance=False):
+    def _view_backward(self, ci, advance=False, rebin=True):
         """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
-        self.forward(ci, advance)
+        self.forward(ci, advance, rebin)
         kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
                           self.loss_ws)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                           self.k, self.image, self.den, self.gimage, self.gslot,
                           order=self.order)
 
-    def enqueue(self, i=0):
-        """Enqueue training step i (camera i, or batch i) on the current stream."""
+    def enqueue(self, i=0, rebin=True):
+        """Enqueue training step i (camera i, or batch i) on the current stream; rebin=False
+        reuses the bins last computed (batch = 1 only)."""
         sh = dict(sh_rest=self.sh, sh_degree=self.sh_degree)
         mc = self.mc
         if self.batch == 1:
-            self._view_backward(i, advance=True)   # the step advance rides on geom_fwd
+            self._view_backward(i, advance=True, rebin=rebin)   # step advance rides on geom_fwd
             kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
                                   self.lr, self.step_block, gparams=self.gparams,
                                   sh_m=self.sh_m, sh_v=self.sh_v,
@@ -255,11 +269,13 @@ class TrainStep:
         if self.dw is not None:
             live += [self.dw, self.dw_state, self.gdw]
         state = [t.clone() for t in live]
+        variants = (True, False) if self.bin_every > 1 else (True,)
         side = torch.cuda.Stream(device=self.dev)
         side.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(side):
             for ci in cams:
-                self.enqueue(ci)
+                for rebin in variants:
+                    self.enqueue(ci, rebin)
             if self.mc["relocate_every"]:
                 self.enqueue_relocate()
         torch.cuda.current_stream(self.dev).wait_stream(side)
@@ -269,10 +285,11 @@ class TrainStep:
             self.relocations.zero_()
         torch.cuda.synchronize(self.dev)
         for ci in cams:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                self.enqueue(ci)
-            self.graphs[ci] = g
+            for rebin in variants:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self.enqueue(ci, rebin)
+                self.graphs[(ci, rebin)] = g
         if self.mc["relocate_every"]:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -281,18 +298,23 @@ class TrainStep:
         torch.cuda.synchronize(self.dev)
 
     def step(self, ci=0):
-        """Training step ci: camera ci, or batch ci (graph replay when captured, else eager)."""
-        g = self.graphs.get(ci)
+        """Training step ci: camera ci, or batch ci (graph replay when captured, else eager).
+        With bin_every = N the bins are recomputed on every N-th step() call (counting from the
+        first) and after a relocation, and reused otherwise."""
+        rebin = self._it % self.bin_every == 0 or self._force_rebin
+        self._force_rebin = False
+        g = self.graphs.get((ci, rebin))
         if g is not None:
             g.replay()
         else:
-            self.enqueue(ci)
+            self.enqueue(ci, rebin)
         every = self.mc["relocate_every"]
         if every and self._it > 0 and self._it % every == 0:
             if self.reloc_graph is not None:
                 self.reloc_graph.replay()
             else:
                 self.enqueue_relocate()
+            self._force_rebin = True     # relocated gaussians move: the next step rebins
         self._it += 1
 
     def loss(self):

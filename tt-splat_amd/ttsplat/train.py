@@ -43,6 +43,9 @@ class _Fitted:
                                          dtype=F32).detach().to(P.device).reshape(())
         self.softz_beta = torch.as_tensor(getattr(model, "softz_beta", 4.0),
                                           dtype=F32).detach().to(P.device).reshape(())
+        rest = getattr(model, "color_rest", None)   # SH rest coefficients [G,15,3] or None
+        self.color_rest = (None if rest is None
+                           else rest.detach().to(P.device, F32).contiguous().clone())
 
 
 def _write_back(model, st):
@@ -56,6 +59,8 @@ def _write_back(model, st):
             model.log_scales.copy_(P[:, 7:10])
             model.color_dc.copy_(P[:, 10:13])
             model.opacity_raw.copy_(P[:, 13].reshape(model.opacity_raw.shape))
+        if st.color_rest is not None and torch.is_tensor(getattr(model, "color_rest", None)):
+            model.color_rest.copy_(st.color_rest.reshape(model.color_rest.shape))
         if torch.is_tensor(model.w_b_raw):
             model.w_b_raw.copy_(st.w_b_raw.reshape(model.w_b_raw.shape))
         else:
@@ -89,6 +94,12 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
     mw, vw = torch.zeros_like(wrow), torch.zeros_like(wrow)
     step = kernels.adam_state(dev)
     gts = [g.to(dev).float().contiguous() for g in gt_images]
+    # view-dependent colour: the rest coefficients take Adam at lr color_rest (spike/model.py:91)
+    use_sh = int(sh_degree) > 0 and st.color_rest is not None
+    if use_sh:
+        mr, vr = torch.zeros_like(st.color_rest), torch.zeros_like(st.color_rest)
+        lr_rest = torch.tensor([float(lr.get("color_rest", lr["color"] / 20.0))], dtype=F32,
+                               device=dev)
 
     class _View:                     # the duck-typed model render() reads
         pass
@@ -107,14 +118,19 @@ def fit(model, cameras, gt_images, arm, iters=800, lambda_ssim=0.2, lr=None, k=4
         if arm == "SZ":
             view.softz_beta = st.softz_beta.clone().requires_grad_(True)
             leaves += [view.softz_beta]
+        if use_sh:
+            view.color_rest = st.color_rest.clone().requires_grad_(True)
+            leaves += [view.color_rest]
         total = 0.0
         for cam, gt in zip(cameras, gts):
-            img = render(view, cam, arm, k=k, blur_eps=blur_eps, near=near)
+            img = render(view, cam, arm, k=k, blur_eps=blur_eps, near=near, sh_degree=sh_degree)
             total = total + loss_fn(img, gt, lambda_ssim)
         total = total / len(cameras)
         grads = torch.autograd.grad(total, leaves)
         kernels.adam_advance(step)
         kernels.adam(st.params, m, v, grads[0].contiguous(), lrv, step)
+        if use_sh:
+            kernels.adam_flat(st.color_rest, mr, vr, grads[-1].contiguous(), lr_rest, step)
         wrow[0, 0] = st.w_b_raw
         gwrow = torch.zeros_like(wrow)
         gwrow[0, 0] = grads[1]
