@@ -218,8 +218,8 @@ def time_kernels(ts, reps, torch, kernels):
         if ts.dtype == "bf16" else
         (lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S, ts.k,
                                    ts.image, ts.den, ts.order)),
-        "loss_grad": lambda: kernels.loss_grad(ts.image, ts.targets[0], ts.lam, ts.gimage,
-                                               ts.partials, ts.loss_ws),
+        "loss_grad": lambda: kernels.loss_grad_stats(ts.image, ts.targets[0], ts.target_stats[0],
+                                                     ts.lam, ts.gimage, ts.partials),
         "splat_bwd": lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
                                                ts.S, ts.k, ts.image, ts.den, ts.gimage,
                                                ts.gslot, order=ts.order),

@@ -207,21 +207,36 @@ int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* vali
 
 /* -------------------------------------------------------------------- loss ---------- */
 
-/* Bytes of scratch tts_loss_grad needs for an H x W image: the SSIM partial maps, 9 planes of
- * (H-10) x (W-10) floats (no initialisation needed). */
+/* Bytes of the target statistics of an H x W target: mu_y and s_y = G*y^2 - mu_y^2 of each
+ * channel on the (H-10) x (W-10) valid SSIM map, six planes of floats. */
+size_t tts_loss_stats_bytes(int H, int W);
+
+/* Bytes of scratch tts_loss_grad needs: the target statistics (tts_loss_stats_bytes). */
 size_t tts_loss_workspace_bytes(int H, int W);
 
-/* Number of fp32 partial sums tts_loss_grad writes.  The first *n_ssim are sums of the SSIM
- * map, the rest are sums of |x-y|:
+/* Number of fp32 partial sums tts_loss_grad / tts_loss_grad_stats write.  The first *n_ssim are
+ * sums of the SSIM map, the rest are sums of |x-y|:
  *   loss = (1-l) * sum|x-y| / (3HW) + l * (1 - sumS / (3 (H-10)(W-10))). */
 int tts_loss_partials_count(int H, int W, int* n_ssim);
 
+/* The target's SSIM statistics (stats: tts_loss_stats_bytes bytes, written whole), computed
+ * once per target: the per-view target maps muy/sy of tools/resident_traced.py:431-464.
+ * Size limits as tts_loss_grad. */
+int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream);
+
 /* dL/dimage of L = (1-lambda)*mean|x-y| + lambda*(1 - mean SSIM(clamp(x,0,1), clamp(y,0,1))),
- * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4.
- * Replaces spike/metrics.py:26-28 (loss_fn, differentiated by autograd), the manual gradient
- * tools/loss_manual.py:76-103 and the device loss tools/resident_traced.py:431-464.
- * image, target, gimage: [H,W,3]; H, W >= 11 and H*W*36 <= 2^31-1 (TTS_EINVAL otherwise: the
- * kernels address with 32-bit buffer offsets; 7680x4320 fits).  partials may be NULL. */
+ * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4, with the target's
+ * statistics from tts_loss_target_stats: one kernel, no workspace.  Replaces the device loss of
+ * tools/resident_traced.py:431-464 (its filt/filt_T banded matmuls over precomputed target
+ * maps).  image, target, gimage: [H,W,3]; H, W >= 11 and H*W*24 <= 2^31-17 (TTS_EINVAL
+ * otherwise: the kernels address with 32-bit buffer offsets; 7680x4320 fits).  partials (NULL
+ * or tts_loss_partials_count floats) receives the partial sums. */
+int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
+                        int W, float lambda, float* gimage, float* partials, hipStream_t stream);
+
+/* tts_loss_target_stats into the workspace, then tts_loss_grad_stats.  Replaces
+ * spike/metrics.py:26-28 (loss_fn, differentiated by autograd) and the manual gradient
+ * tools/loss_manual.py:76-103. */
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);

@@ -86,13 +86,16 @@ def test_splat_rejects_bad_tile(lib):
 
 
 def test_loss_grad_size_limit(lib):
-    """The loss kernels address with 32-bit buffer offsets: images whose nine map planes
-    (H*W*36 bytes) exceed 2^31-1 are refused before launch; 7680x4320 passes the check (and
-    then stops at the missing workspace)."""
+    """The loss kernels address with 32-bit buffer offsets: images whose statistics planes
+    (about H*W*24 bytes) would pass 2^31 are refused before launch; 7680x4320 passes the check
+    (and then stops at the missing workspace)."""
     buf = ctypes.create_string_buffer(64)
     p = ctypes.cast(buf, ctypes.c_void_p)
-    assert lib.tts_loss_grad(p, p, 8000, 8000, 0.2, p, None, None, 0, None) == -1
+    assert lib.tts_loss_grad(p, p, 10000, 10000, 0.2, p, None, None, 0, None) == -1
+    assert lib.tts_loss_grad_stats(p, p, p, 10000, 10000, 0.2, p, None, None) == -1
+    assert lib.tts_loss_target_stats(p, 10000, 10000, p, None) == -1
     assert lib.tts_loss_grad(p, p, 4320, 7680, 0.2, p, None, None, 0, None) == -4
+    assert lib.tts_loss_stats_bytes(4320, 7680) == 24 * 4310 * 7670
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -56,9 +56,9 @@ def test_loss_grad(H, W):
 
 @pytest.mark.parametrize("H,W", [(11, 11), (33, 75), (96, 130), (200, 300)])
 def test_loss_grad_ragged_sizes(H, W):
-    """Sizes that do not divide the 32 x 16 tiles (ragged tiles, the 11 x 11 minimum), with x
+    """Sizes that do not divide the 34 x 64 tiles (ragged tiles, the 11 x 11 minimum), with x
     outside [0, 1] in places (the clamp gate), against the oracle; a second call into the same
-    workspace (stale maps from the first) gives the same result."""
+    workspace gives the same result."""
     g = torch.Generator().manual_seed(H * W)
     x = (torch.rand(H, W, 3, generator=g) * 1.2 - 0.1).cuda()
     y = torch.rand(H, W, 3, generator=g).cuda()
@@ -72,6 +72,37 @@ def test_loss_grad_ragged_sizes(H, W):
     rl, rg = oloss.loss_and_grad(x.cpu().double(), y.cpu().double(), 0.2)
     assert abs(float(kernels.loss_from_partials(pb, H, W, 0.2)) - float(rl)) <= 1e-5
     assert rel_l2(gb, rg) <= 1e-4
+
+
+@pytest.mark.parametrize("H,W", [(11, 13), (37, 75), (200, 300)])
+def test_loss_target_stats(H, W):
+    """Target statistics against the oracle's window sums of the clamped target: mu_y and
+    s_y = G*y^2 - mu_y^2 per channel, each channel's planes column-major [Wo][Ho]."""
+    g = torch.Generator().manual_seed(3 * H + W)
+    y = torch.rand(H, W, 3, generator=g) * 1.2 - 0.1          # some values outside [0,1]
+    st = kernels.loss_stats(y.cuda()).cpu().view(2, 3, W - 10, H - 10).double()
+    yc = y.double().clamp(0, 1).permute(2, 0, 1)
+    gw = oloss.gauss_1d()
+    mu = oloss.gaussian_filter(yc, gw)
+    sy = oloss.gaussian_filter(yc * yc, gw) - mu * mu
+    assert max_abs(st[0].transpose(1, 2), mu) <= 1e-6
+    assert max_abs(st[1].transpose(1, 2), sy) <= 1e-6
+
+
+@pytest.mark.parametrize("H,W", [(11, 11), (45, 70), (832, 1264)])
+def test_loss_grad_stats_equals_combined(H, W):
+    """The one-kernel entry on precomputed target statistics gives exactly what the combined
+    entry (statistics into its workspace, then the same kernel) gives, call after call."""
+    g = torch.Generator().manual_seed(H + 7 * W)
+    x = (torch.rand(H, W, 3, generator=g) * 1.2 - 0.1).cuda()
+    y = torch.rand(H, W, 3, generator=g).cuda()
+    n, _ = kernels.loss_partials_count(H, W)
+    pa, pb = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    ga = kernels.loss_grad(x, y, 0.2, partials=pa)
+    st = kernels.loss_stats(y)
+    for _ in range(2):
+        gb = kernels.loss_grad_stats(x, y, st, 0.2, partials=pb)
+        assert torch.equal(ga, gb) and torch.equal(pa, pb)
 
 
 def test_loss_identity():

@@ -2,17 +2,26 @@
 // SSIM: 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4
 // (spike/metrics.py:6-28; the manual gradient of tools/loss_manual.py:76-103).
 //
-// Two kernels, one colour channel per block, separable filters with register blocking (each
-// value read from LDS once per pass instead of once per tap):
-//   k_ssim_maps   per OUTPUT pixel of the valid SSIM map: the five filtered moments mu_x,
-//                 E[x^2], E[xy], mu_y, E[y^2], S and its partials dS/dmu_x, dS/dE[x^2],
-//                 dS/dE[xy] -> maps[3][3][Ho][Wo], the tile's sum of S.  The target's moments
-//                 are filtered in the same passes rather than read from a precomputed buffer:
-//                 in a training step the target arrives from HBM, and its two statistics planes
-//                 per channel would cost twice its own bytes again.
-//   k_ssim_grad   per INPUT pixel: the transposed filter (zero outside the valid map) of the
-//                 three maps, combined as  dmeanS/dx = (F'(A) + 2 x F'(B) + y F'(Cxy)) / Ns,
-//                 gated by 0 <= x <= 1 (the clamp), plus the L1 term (1-l) sign(x-y) / N.
+// The target's statistics mu_y = G*y and s_y = G*y^2 - mu_y^2 depend on the target only: a
+// training loop computes them once per view (k_loss_target_stats), as the reference's resident
+// trainer keeps muy/sy per view (tools/resident_traced.py:431-464).  The step kernel then
+// filters x, x^2 and xy only.
+//
+// k_loss_fused: a block owns a TH x 64 tile of gradient pixels of one colour channel and runs
+// the whole chain on it, the SSIM map region it needs (the tile plus the 10-pixel halo above and
+// left of it) recomputed rather than exchanged through memory:
+//   1 vertical filter of x, x^2, xy straight from global memory (a thread = one input column,
+//     a run of map rows; its loads in flight together)            -> V[3][TH+10][84]  (LDS)
+//   2 horizontal filter, S and its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] (a thread = a run
+//     of map columns on one map row)                              -> D[3][TH+10][74]  (LDS)
+//   3 transposed horizontal filter of the partials               -> T[3][TH+10][64]  (LDS)
+//   4 transposed vertical filter (a thread = one gradient column, a run of rows, so its image
+//     loads and gradient stores are coalesced), combined as dmeanS/dx = (T'A + 2 x T'B +
+//     y T'C) / Ns, gated by 0 <= x <= 1 (the clamp), plus the L1 term (1-l) sign(x-y) / N.
+// V, D and T share one 45 KB LDS buffer (each written after a barrier that ends the reads of
+// the one before; three blocks fit a CU); the loads a phase needs from global memory are issued
+// a phase ahead.  Each block also sums S over the map pixels of its tile and |x - y| over its
+// pixels.  Nothing is exchanged between blocks: the kernel needs no workspace.
 
 #include "tts_common.h"
 
@@ -20,12 +29,14 @@ namespace tts {
 
 constexpr int kWin = 11;
 constexpr int kHalo = kWin - 1;
-constexpr int kTW = 32;            // tile width (outputs of a pass)
-constexpr int kTH = 16;            // tile height
-constexpr int kRW = kTW + kHalo;   // 42: region width
-constexpr int kRH = kTH + kHalo;   // 26: region height
-constexpr int kVRows = 4;          // vertical pass: output rows per thread
-constexpr int kHCols = 2;          // horizontal pass: outputs per thread
+constexpr int kTW = 64;                 // gradient tile width
+constexpr int kMC = kTW + kHalo;        // 74 map columns
+constexpr int kIC = kTW + 2 * kHalo;    // 84 input columns
+constexpr int kVS = kIC + 1;            // LDS row strides (odd: column walks spread over banks)
+constexpr int kDS = kMC + 1;
+constexpr int kHC = 15;                 // phase 2: map columns per thread (5 runs cover 74)
+constexpr int kHC3 = 13;                // phase 3: gradient columns per thread (5 runs cover 64)
+constexpr int kTS = kTW + 1;
 constexpr float kC1 = 1e-4f;
 constexpr float kC2 = 9e-4f;
 
@@ -33,289 +44,354 @@ struct Taps {
   float g[kWin];
 };
 
-// Work item of a 1-D grid of gx * gy * 3 blocks: (tile column, tile row, channel), channels
-// innermost and tiles row-major, renumbered so that each XCD sweeps one contiguous band of tiles.
-struct TileItem {
-  int tx, ty, ch;
-};
-__device__ __forceinline__ TileItem tile_item(int gx, int gy) {
-  const int n = gx * gy * 3;
-  const int w = xcd_item(blockIdx.x, n);
-  const int t = w / 3;
-  return {t % gx, t / gx, w - 3 * t};
-}
-
 __device__ __forceinline__ float clamp01(float v) { return fminf(fmaxf(v, 0.f), 1.f); }
 
-// Buffer-resource addressing: a wave-uniform base (scalar offset: row, plane) plus a 32-bit
-// per-lane byte offset (column), so no lane forms a 64-bit address.  Every buffer handed to
-// these kernels is under 2^31 bytes (the entry point checks); a resource's size is its bound,
-// and the indices are clamped inside it as well.
+// Buffer-resource addressing: one 32-bit byte offset per lane.  A resource's size is its bound:
+// a load at an offset at or past it reads 0.  Images are under 2^31 bytes (the entry points
+// check), so an offset computed from a row above the image (negative, taken as unsigned) or
+// kOOB plus any in-image offset stays past the bound.
 typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr unsigned kOOB = 0x80000000u;
 __device__ __forceinline__ Rsrc rsrc(const float* p, size_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, (int)bytes, 0x00020000);
 }
-__device__ __forceinline__ float bld(Rsrc r, unsigned voff, unsigned soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+__device__ __forceinline__ float bld(Rsrc r, unsigned voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
 }
-__device__ __forceinline__ void bst(Rsrc r, unsigned voff, unsigned soff, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 0);
+__device__ __forceinline__ void bst(Rsrc r, unsigned voff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, 0, 0);
 }
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
-// Map kernel: per output pixel of the valid SSIM map, the moments mu_x, E[x^2], E[xy], mu_y,
-// E[y^2] (five filtered images), S and its partials dS/dmu_x, dS/dE[x^2], dS/dE[xy] ->
-// maps[3][3][Ho][Wo]; the tile's sum of S.
-__global__ __launch_bounds__(256) void k_ssim_maps(const float* __restrict__ x,
-                                                   const float* __restrict__ y, int H, int W,
-                                                   Taps taps, float* __restrict__ maps,
-                                                   float* __restrict__ partials) {
+// ------------------------------------------------------------------ target statistics ------
+// One block per (64 x 16 tile of the valid map, channel): mu_y and s_y of the clamped target ->
+// stats[2][3][Wo][Ho], each channel's planes column-major (the step kernel reads them along map
+// rows per lane).
+constexpr int kSW = 64, kSH = 16, kSR = 6;   // tile, vertical run (3 runs cover 16 rows)
+__global__ __launch_bounds__(256) void k_loss_target_stats(const float* __restrict__ y, int H,
+                                                           int W, int tiles_x, Taps taps,
+                                                           float* __restrict__ stats) {
+  __shared__ float V[2][kSH][kSW + kHalo + 1];
   const int Ho = H - kHalo, Wo = W - kHalo;
-  const TileItem it = tile_item((Wo + kTW - 1) / kTW, (Ho + kTH - 1) / kTH);
-  const int ox0 = it.tx * kTW, oy0 = it.ty * kTH, ch = it.ch;
-  __shared__ float sx[kRH][kRW + 1], sy[kRH][kRW + 1];
-  __shared__ float v[5][kTH][kRW + 1];
-  __shared__ float s_ftmp[4];
+  const int t = blockIdx.x / 3, ch = blockIdx.x - 3 * t;
+  const int R0 = (t / tiles_x) * kSH, C0 = (t % tiles_x) * kSW;
   const int tid = threadIdx.x;
-  const unsigned plane = (unsigned)(Ho * Wo);
-  {  // region rows [oy0, oy0+26), cols [ox0, ox0+42): lane = column, wave w takes rows w, w+4, ...
-    constexpr int NI = (kRH + 3) / 4;
-    const Rsrc xs = rsrc(x, (size_t)H * W * 12), ys = rsrc(y, (size_t)H * W * 12);
-    const int lane = tid & 63, wv = wave_id();
-    const unsigned coff = ((unsigned)min(ox0 + lane, W - 1) * 3u + (unsigned)ch) * 4u;
-    float a[NI], b[NI];
+  const Rsrc ys = rsrc(y, (size_t)H * W * 12);
+  if (tid < 3 * (kSW + kHalo)) {
+    const int j = tid % (kSW + kHalo), m0 = (tid / (kSW + kHalo)) * kSR;
+    const int gc = C0 + j;
+    const unsigned base = gc < W ? (unsigned)((((R0 + m0) * W + gc) * 3 + ch) * 4) : kOOB;
+    float v[kSR + kHalo];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int gr = min(oy0 + wv + 4 * i, H - 1);
-      a[i] = bld(xs, coff, (unsigned)(gr * W) * 12u);
-      b[i] = bld(ys, coff, (unsigned)(gr * W) * 12u);
+    for (int k = 0; k < kSR + kHalo; ++k) v[k] = clamp01(bld(ys, base + (unsigned)k * W * 12u));
+    float a[2][kSR];
+#pragma unroll
+    for (int o = 0; o < kSR; ++o) a[0][o] = a[1][o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSR + kHalo; ++k) {
+      const float b = v[k], bb = b * b;
+#pragma unroll
+      for (int o = 0; o < kSR; ++o) {
+        const int tap = k - o;
+        if (tap >= 0 && tap < kWin) {
+          a[0][o] += taps.g[tap] * b;
+          a[1][o] += taps.g[tap] * bb;
+        }
+      }
     }
-    const bool col_ok = lane < kRW && ox0 + lane < W;
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int r = wv + 4 * i;
-      if (r < kRH && lane < kRW) {
-        const bool in = col_ok && oy0 + r < H;
-        sx[r][lane] = in ? clamp01(a[i]) : 0.f;
-        sy[r][lane] = in ? clamp01(b[i]) : 0.f;
+    for (int o = 0; o < kSR; ++o) {
+      if (m0 + o < kSH) {
+        V[0][m0 + o][j] = a[0][o];
+        V[1][m0 + o][j] = a[1][o];
       }
     }
   }
-  // this thread's output pixels in the horizontal pass
-  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
-  const int orow = oy0 + r;
   __syncthreads();
-  // vertical: thread = (column c, chunk of kVRows output rows)
-  if (tid < kRW * (kTH / kVRows)) {
-    const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
-    float acc[5][kVRows];
+  const int m = tid >> 4, q0 = (tid & 15) * 4;
+  float f[2][4];
 #pragma unroll
-    for (int m = 0; m < 5; ++m)
+  for (int o = 0; o < 4; ++o) f[0][o] = f[1][o] = 0.f;
 #pragma unroll
-      for (int o = 0; o < kVRows; ++o) acc[m][o] = 0.f;
+  for (int k = 0; k < 4 + kHalo; ++k) {
+    const float a = V[0][m][q0 + k], b = V[1][m][q0 + k];
 #pragma unroll
-    for (int k = 0; k < kVRows + kHalo; ++k) {
-      const float xv = sx[r0 + k][c], yv = sy[r0 + k][c];
-      const float xx = xv * xv, xy = xv * yv, yy = yv * yv;
+    for (int o = 0; o < 4; ++o) {
+      const int tap = k - o;
+      if (tap >= 0 && tap < kWin) {
+        f[0][o] += taps.g[tap] * a;
+        f[1][o] += taps.g[tap] * b;
+      }
+    }
+  }
+  const int gm = R0 + m;
+  const size_t plane = (size_t)Ho * Wo;
 #pragma unroll
-      for (int o = 0; o < kVRows; ++o) {
+  for (int o = 0; o < 4; ++o) {
+    const int gq = C0 + q0 + o;
+    if (gm < Ho && gq < Wo) {
+      const size_t i = (size_t)gq * Ho + gm;   // column-major: a column's rows are contiguous
+      stats[(size_t)ch * plane + i] = f[0][o];
+      stats[(size_t)(3 + ch) * plane + i] = f[1][o] - f[0][o] * f[0][o];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ fused step kernel ------
+template <int TH>
+struct FGeo {
+  static constexpr int MR = TH + kHalo;              // map rows of the region
+  static constexpr int VR = (MR + 2) / 3;            // phase 1: map rows per thread (3 runs)
+  static constexpr int TR4 = (TH + 3) / 4;           // phase 4: gradient rows per thread
+  static constexpr int N2 = 5 * MR;                  // phase 2 and 3 threads
+  static constexpr int TP = 4 * TR4 + kHalo;         // T rows per plane (phase 4 reads past MR)
+  static constexpr int kV = 3 * MR * kVS;            // floats of V
+  static_assert(3 * MR * kDS + kDS <= kV && 3 * TP * kTS <= kV, "D and T reuse V's space");
+  static_assert(3 * kIC <= 256 && N2 <= 256, "one pass each");
+  static_assert(5 * kHC >= kMC && 5 * kHC3 >= kTW && 3 * VR >= MR && 4 * TR4 >= TH, "cover");
+  static constexpr size_t lds_bytes = sizeof(float) * (size_t)kV;
+};
+
+template <int TH>
+__global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
+                                                    const float* __restrict__ y,
+                                                    const float* __restrict__ stats, int H,
+                                                    int W, int tiles_x, int n_items, Taps taps,
+                                                    float lambda, float inv_n, float inv_ns,
+                                                    float* __restrict__ gout,
+                                                    float* __restrict__ partials) {
+  using G = FGeo<TH>;
+  extern __shared__ float s_lds[];
+  float* V = s_lds;
+  float* D = s_lds;
+  float* T = s_lds;
+  __shared__ float s_ftmp[4];
+  // items: (tile, channel), channels innermost so a tile's three blocks share cache lines
+  const int item = xcd_item(blockIdx.x, n_items);
+  const int tile = item / 3, ch = item - 3 * tile;
+  const int R0 = (tile / tiles_x) * TH, C0 = (tile % tiles_x) * kTW;
+  const int Ho = H - kHalo, Wo = W - kHalo;
+  const int tid = threadIdx.x;
+  const size_t ibytes = (size_t)H * W * 12;
+  const Rsrc xs = rsrc(x, ibytes), ys = rsrc(y, ibytes), gs_out = rsrc(gout, ibytes);
+  const Rsrc ss = rsrc(stats, (size_t)Ho * Wo * 24);
+  const unsigned plane4 = (unsigned)(Ho * Wo) * 4u;
+  // phase-2 role: map row m2, columns [q2, q2 + 15); its target statistics loaded up front
+  const int m2 = tid % G::MR, q2 = (tid / G::MR) * kHC;
+  const bool act2 = tid < G::N2;
+  const int gm2 = R0 - kHalo + m2;
+  float smu[kHC], ssy[kHC];
+  auto load_stats = [&]() {
+    const unsigned row = (unsigned)min(max(gm2, 0), Ho - 1);
+#pragma unroll
+    for (int o = 0; o < kHC; ++o) {
+      const unsigned col = (unsigned)min(max(C0 - kHalo + q2 + o, 0), Wo - 1);
+      const unsigned off = (col * (unsigned)Ho + row) * 4u + (unsigned)ch * plane4;
+      smu[o] = bld(ss, off);
+      ssy[o] = bld(ss, off + 3u * plane4);
+    }
+  };
+  // ---- phase 1: vertical filter of x, x^2, xy; thread = (input column j, run of VR map rows)
+  if (tid < 3 * kIC) {
+    const int j = tid % kIC, m0 = (tid / kIC) * G::VR;
+    const int gc = C0 - kHalo + j;
+    // rows outside the image fall past the bound (negative or >= H rows); columns outside it
+    // would alias a neighbouring row, so their lanes start at kOOB
+    const unsigned base = (gc >= 0 && gc < W)
+                              ? (unsigned)((((R0 - kHalo + m0) * W + gc) * 3 + ch) * 4)
+                              : kOOB;
+    const unsigned rstep = (unsigned)W * 12u;
+    float xv[G::VR + kHalo], yv[G::VR + kHalo];
+#pragma unroll
+    for (int k = 0; k < G::VR + kHalo; ++k) {
+      xv[k] = bld(xs, base + (unsigned)k * rstep);
+      yv[k] = bld(ys, base + (unsigned)k * rstep);
+    }
+    // the target statistics phase 2 needs, issued after the loads phase 1 waits on
+    load_stats();
+    float acc[3][G::VR];
+#pragma unroll
+    for (int o = 0; o < G::VR; ++o) acc[0][o] = acc[1][o] = acc[2][o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < G::VR + kHalo; ++k) {
+      const float a = clamp01(xv[k]), b = clamp01(yv[k]), aa = a * a, ab = a * b;
+#pragma unroll
+      for (int o = 0; o < G::VR; ++o) {
         const int tap = k - o;
         if (tap >= 0 && tap < kWin) {
           const float gk = taps.g[tap];
-          acc[0][o] += gk * xv;
-          acc[1][o] += gk * xx;
-          acc[2][o] += gk * xy;
-          acc[3][o] += gk * yv;
-          acc[4][o] += gk * yy;
+          acc[0][o] += gk * a;
+          acc[1][o] += gk * aa;
+          acc[2][o] += gk * ab;
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < 5; ++m)
+    for (int o = 0; o < G::VR; ++o) {
+      const int m = m0 + o;
+      if (m < G::MR) {
 #pragma unroll
-      for (int o = 0; o < kVRows; ++o) v[m][r0 + o][c] = acc[m][o];
-  }
-  __syncthreads();
-  // horizontal: thread = (output row r, chunk of kHCols outputs)
-  float f[5][kHCols];
-#pragma unroll
-  for (int m = 0; m < 5; ++m)
-#pragma unroll
-    for (int o = 0; o < kHCols; ++o) f[m][o] = 0.f;
-#pragma unroll
-  for (int k = 0; k < kHCols + kHalo; ++k) {
-    float vv[5];
-#pragma unroll
-    for (int m = 0; m < 5; ++m) vv[m] = v[m][r][c0 + k];
-#pragma unroll
-    for (int o = 0; o < kHCols; ++o) {
-      const int tap = k - o;
-      if (tap >= 0 && tap < kWin) {
-        const float gk = taps.g[tap];
-#pragma unroll
-        for (int m = 0; m < 5; ++m) f[m][o] += gk * vv[m];
+        for (int qn = 0; qn < 3; ++qn) V[(qn * G::MR + m) * kVS + j] = acc[qn][o];
       }
     }
   }
-  float ssum = 0.0f;
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) {
-    const int ocol = ox0 + c0 + o;
-    if (orow < Ho && ocol < Wo) {
-      const float mx = f[0][o], my = f[3][o];
-      const float A1 = 2.f * mx * my + kC1;
-      const float A2 = 2.f * (f[2][o] - mx * my) + kC2;
-      const float B1 = mx * mx + my * my + kC1;
-      const float B2 = (f[1][o] - mx * mx) + (f[4][o] - my * my) + kC2;
-      // hardware reciprocal (1 ulp): B1 >= C1 and B2 >= C2 - rounding, so B1*B2 is normal
-      const float inv_d = __builtin_amdgcn_rcpf(B1 * B2);
-      const float Sv = A1 * A2 * inv_d;
-      const unsigned oi = (unsigned)(orow * Wo + ocol) * 4u;
-      const Rsrc mp = rsrc(maps, (size_t)plane * 36);
-      bst(mp, oi, ch * plane * 4u, 2.f * inv_d * (my * (A2 - A1) - Sv * mx * (B2 - B1)));
-      bst(mp, oi, (3 + ch) * plane * 4u, -Sv * B1 * inv_d);
-      bst(mp, oi, (6 + ch) * plane * 4u, 2.f * A1 * inv_d);
-      ssum += Sv;
-    }
-  }
-  const float tot = block_sum256(ssum, s_ftmp);
-  if (partials && tid == 0)
-    partials[blockIdx.x] = tot;
-}
-
-__global__ __launch_bounds__(256) void k_ssim_grad(const float* __restrict__ x,
-                                                   const float* __restrict__ y, int H, int W,
-                                                   Taps taps, const float* __restrict__ maps,
-                                                   float lambda, float inv_n, float inv_ns,
-                                                   float* __restrict__ gout,
-                                                   float* __restrict__ partials) {
-  const int Ho = H - kHalo, Wo = W - kHalo;
-  const TileItem it = tile_item((W + kTW - 1) / kTW, (H + kTH - 1) / kTH);
-  const int ix0 = it.tx * kTW, iy0 = it.ty * kTH, ch = it.ch;
-  __shared__ float sm[3][kRH][kRW + 1];
-  __shared__ float v[3][kTH][kRW + 1];
-  __shared__ float s_ftmp[4];
-  const int tid = threadIdx.x;
-  const unsigned plane = (unsigned)(Ho * Wo);
-  const int lane = tid & 63, wv = wave_id();
-  // map rows [iy0-10, iy0+16), cols [ix0-10, ix0+32); zero outside the valid map.
-  // lane = column, wave w takes rows w, w+4, ...
-  {
-    constexpr int NI = (kRH + 3) / 4;
-    const Rsrc ms = rsrc(maps, (size_t)plane * 36);
-    const int mc = ix0 - kHalo + lane;
-    const unsigned coff = (unsigned)min(max(mc, 0), Wo - 1) * 4u;
-    float mv[3][NI];
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {  // every load in flight before any is used
-      const int mr = min(max(iy0 - kHalo + wv + 4 * i, 0), Ho - 1);
-#pragma unroll
-      for (int m = 0; m < 3; ++m)
-        mv[m][i] = bld(ms, coff, ((unsigned)(m * 3 + ch) * plane + (unsigned)(mr * Wo)) * 4u);
-    }
-    const bool col_ok = lane < kRW && mc >= 0 && mc < Wo;
-#pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      const int r = wv + 4 * i, mr = iy0 - kHalo + r;
-      if (r < kRH && lane < kRW) {
-        const bool ok = col_ok && mr >= 0 && mr < Ho;
-#pragma unroll
-        for (int m = 0; m < 3; ++m) sm[m][r][lane] = ok ? mv[m][i] : 0.f;
-      }
-    }
-  }
-  // this thread's pixels (loaded ahead of the filtering)
-  const int r = tid / (kTW / kHCols), c0 = (tid % (kTW / kHCols)) * kHCols;
-  const int gr = iy0 + r;
-  const Rsrc xs = rsrc(x, (size_t)H * W * 12), ys = rsrc(y, (size_t)H * W * 12);
-  const unsigned roff = (unsigned)(min(gr, H - 1) * W) * 12u;  // per lane: 4 rows per wave
-  float xv[kHCols], yv[kHCols];
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) {
-    const unsigned po = ((unsigned)min(ix0 + c0 + o, W - 1) * 3u + (unsigned)ch) * 4u;
-    xv[o] = bld(xs, roff + po, 0);
-    yv[o] = bld(ys, roff + po, 0);
+  else {
+    load_stats();
   }
   __syncthreads();
-  // transposed vertical: input row r receives sum_k g[k] * map[r + 10 - k]
-  if (tid < kRW * (kTH / kVRows)) {
-    const int c = tid % kRW, r0 = (tid / kRW) * kVRows;
-    float acc[3][kVRows];
+  // ---- phase 2: horizontal filter + SSIM partials
+  float ssum = 0.f, l1sum = 0.f;
+  float dv[3][kHC];
+  if (act2) {
 #pragma unroll
-    for (int m = 0; m < 3; ++m)
+    for (int o = 0; o < kHC; ++o) dv[0][o] = dv[1][o] = dv[2][o] = 0.f;
 #pragma unroll
-      for (int o = 0; o < kVRows; ++o) acc[m][o] = 0.f;
+    for (int k = 0; k < kHC + kHalo; ++k) {
+      const int c = q2 + k;   // <= 84 < kVS: the row padding, feeding only dropped columns
+      float vv[3];
 #pragma unroll
-    for (int k = 0; k < kVRows + kHalo; ++k) {
-      float mv[3];
+      for (int qn = 0; qn < 3; ++qn) vv[qn] = V[(qn * G::MR + m2) * kVS + c];
 #pragma unroll
-      for (int m = 0; m < 3; ++m) mv[m] = sm[m][r0 + k][c];
-#pragma unroll
-      for (int o = 0; o < kVRows; ++o) {
-        const int tap = kHalo - (k - o);  // map row r0+k feeds input row r0+o through tap 10-(k-o)
+      for (int o = 0; o < kHC; ++o) {
+        const int tap = k - o;
         if (tap >= 0 && tap < kWin) {
           const float gk = taps.g[tap];
 #pragma unroll
-          for (int m = 0; m < 3; ++m) acc[m][o] += gk * mv[m];
+          for (int qn = 0; qn < 3; ++qn) dv[qn][o] += gk * vv[qn];
+        }
+      }
+    }
+    const bool row_ok = gm2 >= 0 && gm2 < Ho;
+#pragma unroll
+    for (int o = 0; o < kHC; ++o) {
+      const int gq = C0 - kHalo + q2 + o;
+      float d0 = 0.f, d1 = 0.f, d2 = 0.f;
+      if (row_ok && gq >= 0 && gq < Wo && q2 + o < kMC) {
+        const float mx = dv[0][o], my = smu[o];
+        const float A1 = 2.f * mx * my + kC1;
+        const float A2 = 2.f * (dv[2][o] - mx * my) + kC2;
+        const float B1 = mx * mx + my * my + kC1;
+        const float B2 = (dv[1][o] - mx * mx) + ssy[o] + kC2;
+        // hardware reciprocal (1 ulp): B1 >= C1 and B2 >= C2 - rounding, so B1*B2 is normal
+        const float inv_d = __builtin_amdgcn_rcpf(B1 * B2);
+        const float Sv = A1 * A2 * inv_d;
+        d0 = 2.f * inv_d * (my * (A2 - A1) - Sv * mx * (B2 - B1));
+        d1 = -Sv * B1 * inv_d;
+        d2 = 2.f * A1 * inv_d;
+        if (m2 >= kHalo && q2 + o >= kHalo) ssum += Sv;   // map pixels of this tile
+      }
+      dv[0][o] = d0;
+      dv[1][o] = d1;
+      dv[2][o] = d2;
+    }
+  }
+  __syncthreads();   // every read of V done: D overwrites it
+  if (act2) {
+#pragma unroll
+    for (int o = 0; o < kHC; ++o) {
+      if (q2 + o < kMC) {
+#pragma unroll
+        for (int qn = 0; qn < 3; ++qn) D[(qn * G::MR + m2) * kDS + q2 + o] = dv[qn][o];
+      }
+    }
+  }
+  // phase-4 role: gradient column c4, rows [p4, p4 + TR4); its pixels loaded two phases ahead
+  const int c4 = tid & 63, p4 = (tid >> 6) * G::TR4;
+  const int gc4 = C0 + c4;
+  const bool col4_ok = gc4 < W;
+  const unsigned off4 = (unsigned)((((R0 + p4) * W + gc4) * 3 + ch) * 4);
+  const unsigned rstep4 = (unsigned)W * 12u;
+  float xr[G::TR4], yr[G::TR4];
+#pragma unroll
+  for (int o = 0; o < G::TR4; ++o) {
+    xr[o] = bld(xs, col4_ok ? off4 + (unsigned)o * rstep4 : kOOB);
+    yr[o] = bld(ys, col4_ok ? off4 + (unsigned)o * rstep4 : kOOB);
+  }
+  __syncthreads();
+  // ---- phase 3: transposed horizontal, thread = (map row m3, run of kHC3 gradient columns):
+  //      gradient column c receives map columns c..c+10 through tap 10 - (q - c)
+  float ta[3][kHC3];
+  const int m3 = tid % G::MR, c3 = (tid / G::MR) * kHC3;
+  const bool act3 = tid < 5 * G::MR;
+  if (act3) {
+#pragma unroll
+    for (int o = 0; o < kHC3; ++o) ta[0][o] = ta[1][o] = ta[2][o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kHC3 + kHalo; ++k) {
+      const int q = c3 + k;   // <= 74 < kDS: the row padding, feeding only dropped columns
+      float dd[3];
+#pragma unroll
+      for (int qn = 0; qn < 3; ++qn) dd[qn] = D[(qn * G::MR + m3) * kDS + q];
+#pragma unroll
+      for (int o = 0; o < kHC3; ++o) {
+        const int tap = kHalo - (k - o);
+        if (tap >= 0 && tap < kWin) {
+          const float gk = taps.g[tap];
+#pragma unroll
+          for (int qn = 0; qn < 3; ++qn) ta[qn][o] += gk * dd[qn];
+        }
+      }
+    }
+  }
+  __syncthreads();   // every read of D done: T overwrites it
+  if (act3) {
+#pragma unroll
+    for (int o = 0; o < kHC3; ++o) {
+      const int c = c3 + o;
+      if (c < kTW) {
+#pragma unroll
+        for (int qn = 0; qn < 3; ++qn) T[(qn * G::TP + m3) * kTS + c] = ta[qn][o];
+      }
+    }
+  }
+  __syncthreads();
+  // ---- phase 4: transposed vertical + gradient, thread = (gradient column c4, run of rows):
+  //      gradient row p receives map rows p..p+10 through tap 10 - (m - p)
+  {
+    float t[3][G::TR4];
+#pragma unroll
+    for (int o = 0; o < G::TR4; ++o) t[0][o] = t[1][o] = t[2][o] = 0.f;
+#pragma unroll
+    for (int k = 0; k < G::TR4 + kHalo; ++k) {
+      const int m = p4 + k;   // rows past MR feed only dropped rows; T has room for them
+      float tt[3];
+#pragma unroll
+      for (int qn = 0; qn < 3; ++qn) tt[qn] = T[(qn * G::TP + m) * kTS + c4];
+#pragma unroll
+      for (int o = 0; o < G::TR4; ++o) {
+        const int tap = kHalo - (k - o);
+        if (tap >= 0 && tap < kWin) {
+          const float gk = taps.g[tap];
+#pragma unroll
+          for (int qn = 0; qn < 3; ++qn) t[qn][o] += gk * tt[qn];
         }
       }
     }
 #pragma unroll
-    for (int m = 0; m < 3; ++m)
-#pragma unroll
-      for (int o = 0; o < kVRows; ++o) v[m][r0 + o][c] = acc[m][o];
-  }
-  __syncthreads();
-  float t[3][kHCols];
-#pragma unroll
-  for (int m = 0; m < 3; ++m)
-#pragma unroll
-    for (int o = 0; o < kHCols; ++o) t[m][o] = 0.f;
-#pragma unroll
-  for (int k = 0; k < kHCols + kHalo; ++k) {
-    float vv[3];
-#pragma unroll
-    for (int m = 0; m < 3; ++m) vv[m] = v[m][r][c0 + k];
-#pragma unroll
-    for (int o = 0; o < kHCols; ++o) {
-      const int tap = kHalo - (k - o);
-      if (tap >= 0 && tap < kWin) {
-        const float gk = taps.g[tap];
-#pragma unroll
-        for (int m = 0; m < 3; ++m) t[m][o] += gk * vv[m];
+    for (int o = 0; o < G::TR4; ++o) {
+      const float xo = xr[o], yo = yr[o];
+      const float d = xo - yo;
+      const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
+      const bool pass = xo >= 0.f && xo <= 1.f;
+      const float gs =
+          pass ? (t[0][o] + 2.f * clamp01(xo) * t[1][o] + clamp01(yo) * t[2][o]) * inv_ns : 0.f;
+      if (col4_ok && p4 + o < TH && R0 + p4 + o < H) {
+        bst(gs_out, off4 + (unsigned)o * rstep4, (1.f - lambda) * sgn * inv_n - lambda * gs);
+        l1sum += fabsf(d);
       }
     }
   }
-  const Rsrc gs_out = rsrc(gout, (size_t)H * W * 12);
-  float l1sum = 0.0f;
-#pragma unroll
-  for (int o = 0; o < kHCols; ++o) {
-    const int gc = ix0 + c0 + o;
-    if (gr < H && gc < W) {
-      const float xr = xv[o], yr = yv[o];
-      const float d = xr - yr;
-      const float sgn = d > 0.f ? 1.f : (d < 0.f ? -1.f : 0.f);
-      const bool pass = xr >= 0.f && xr <= 1.f;
-      const float gs = pass ? (t[0][o] + 2.f * clamp01(xr) * t[1][o] + clamp01(yr) * t[2][o]) * inv_ns
-                            : 0.f;
-      bst(gs_out, roff + ((unsigned)gc * 3u + (unsigned)ch) * 4u, 0,
-          (1.f - lambda) * sgn * inv_n - lambda * gs);
-      l1sum += fabsf(d);
-    }
+  const float st = block_sum256(ssum, s_ftmp);
+  const float lt = block_sum256(l1sum, s_ftmp);
+  if (partials && tid == 0) {
+    partials[blockIdx.x] = st;
+    partials[gridDim.x + blockIdx.x] = lt;
   }
-  const float tot = block_sum256(l1sum, s_ftmp);
-  if (partials && tid == 0)
-    partials[blockIdx.x] = tot;
 }
 
-// 1-D grids (see tile_item): one block per (tile, channel)
-inline int maps_grid(int H, int W) {
-  const int Ho = H - kHalo, Wo = W - kHalo;
-  return ((Wo + kTW - 1) / kTW) * ((Ho + kTH - 1) / kTH) * 3;
-}
-inline int grad_grid(int H, int W) {
-  return ((W + kTW - 1) / kTW) * ((H + kTH - 1) / kTH) * 3;
-}
+constexpr int kTH = 34;
+
+inline int fused_tiles_x(int W) { return (W + kTW - 1) / kTW; }
+inline int fused_items(int H, int W) { return 3 * fused_tiles_x(W) * ((H + kTH - 1) / kTH); }
 
 inline Taps make_taps() {
   Taps taps;
@@ -329,42 +405,63 @@ inline Taps make_taps() {
   return taps;
 }
 
+inline bool loss_size_ok(int H, int W) {
+  // buffer offsets are 32-bit: the statistics planes (24 bytes per map pixel) and the images
+  // (12 bytes per pixel) stay below 2^31 bytes, and an out-of-image offset past the image's bound
+  return H >= kWin && W >= kWin && (int64_t)H * W * 24 <= (int64_t)INT32_MAX - 16;
+}
+
 }  // namespace tts
 
 using namespace tts;
 
 extern "C" {
 
-size_t tts_loss_workspace_bytes(int H, int W) {
-  // the SSIM partial maps: [3][3] planes of (H-10) x (W-10)
+size_t tts_loss_stats_bytes(int H, int W) {
   if (H < kWin || W < kWin) return 0;
-  return sizeof(float) * 9 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
+  return sizeof(float) * 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
 }
+
+size_t tts_loss_workspace_bytes(int H, int W) { return tts_loss_stats_bytes(H, W); }
 
 int tts_loss_partials_count(int H, int W, int* n_ssim) {
   if (H < kWin || W < kWin) return 0;
-  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
-  if (n_ssim) *n_ssim = gm;
-  return gm + gg;
+  const int nb = fused_items(H, W);
+  if (n_ssim) *n_ssim = nb;
+  return 2 * nb;
+}
+
+int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream) {
+  if (!target || !stats) return TTS_EINVAL;
+  if (!loss_size_ok(H, W)) return TTS_EINVAL;
+  const int tx = (W - kHalo + kSW - 1) / kSW, ty = (H - kHalo + kSH - 1) / kSH;
+  k_loss_target_stats<<<tx * ty * 3, 256, 0, stream>>>(target, H, W, tx, make_taps(), stats);
+  return launch_status();
+}
+
+int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,
+                        int W, float lambda, float* gimage, float* partials,
+                        hipStream_t stream) {
+  if (!image || !target || !stats || !gimage) return TTS_EINVAL;
+  if (!loss_size_ok(H, W)) return TTS_EINVAL;
+  const int tx = fused_tiles_x(W), ni = fused_items(H, W);
+  const float inv_n = 1.0f / (3.0f * (float)H * (float)W);
+  const float inv_ns = 1.0f / (3.0f * (float)(H - kHalo) * (float)(W - kHalo));
+  k_loss_fused<kTH><<<ni, 256, FGeo<kTH>::lds_bytes, stream>>>(
+      image, target, stats, H, W, tx, ni, make_taps(), lambda, inv_n, inv_ns, gimage, partials);
+  return launch_status();
 }
 
 int tts_loss_grad(const float* image, const float* target, int H, int W, float lambda,
                   float* gimage, float* partials, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
   if (!image || !target || !gimage) return TTS_EINVAL;
-  if (H < kWin || W < kWin) return TTS_EINVAL;
-  // buffer resources take 32-bit sizes: the 9 map planes (the largest buffer) stay below 2^31 B
-  if ((int64_t)H * W * 36 > INT32_MAX) return TTS_EINVAL;
+  if (!loss_size_ok(H, W)) return TTS_EINVAL;
   if (!workspace || workspace_bytes < tts_loss_workspace_bytes(H, W)) return TTS_EWORKSPACE;
-  const Taps taps = make_taps();
-  const int gm = maps_grid(H, W), gg = grad_grid(H, W);
-  const float inv_n = 1.0f / (3.0f * (float)H * (float)W);
-  const float inv_ns = 1.0f / (3.0f * (float)(H - kHalo) * (float)(W - kHalo));
-  float* maps = static_cast<float*>(workspace);
-  k_ssim_maps<<<gm, 256, 0, stream>>>(image, target, H, W, taps, maps, partials);
-  k_ssim_grad<<<gg, 256, 0, stream>>>(image, target, H, W, taps, maps, lambda, inv_n, inv_ns,
-                                      gimage, partials ? partials + gm : nullptr);
-  return launch_status();
+  float* stats = static_cast<float*>(workspace);
+  const int e = tts_loss_target_stats(target, H, W, stats, stream);
+  if (e) return e;
+  return tts_loss_grad_stats(image, target, stats, H, W, lambda, gimage, partials, stream);
 }
 
 }  // extern "C"

@@ -361,6 +361,36 @@ def loss_grad(image, target, lam=0.2, gimage=None, partials=None, workspace=None
     return gimage
 
 
+def loss_stats(target, stats=None):
+    """The target's SSIM statistics (mu_y, s_y per channel on the valid map), computed once per
+    target and read by loss_grad_stats."""
+    H, W = target.shape[0], target.shape[1]
+    require(target, "target", F32, (H, W, 3))
+    n = _lib.load().tts_loss_stats_bytes(H, W)
+    if n == 0:
+        raise ValueError(f"image {H}x{W} is smaller than the 11x11 SSIM window")
+    stats = torch.empty(n // 4, device=target.device, dtype=F32) if stats is None else stats
+    require(stats, "stats", F32, (n // 4,), target.device)
+    call("tts_loss_target_stats", ptr(target), H, W, ptr(stats), stream())
+    return stats
+
+
+def loss_grad_stats(image, target, stats, lam=0.2, gimage=None, partials=None):
+    """loss_grad with the target's statistics from loss_stats: one kernel."""
+    H, W = image.shape[0], image.shape[1]
+    dev = image.device
+    require(image, "image", F32, (H, W, 3))
+    require(target, "target", F32, (H, W, 3), dev)
+    require(stats, "stats", F32, (_lib.load().tts_loss_stats_bytes(H, W) // 4,), dev)
+    gimage = torch.empty_like(image) if gimage is None else gimage
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    if partials is not None:
+        require(partials, "partials", F32, (loss_partials_count(H, W)[0],), dev)
+    call("tts_loss_grad_stats", ptr(image), ptr(target), ptr(stats), H, W, float(lam),
+         ptr(gimage), ptr(partials), stream())
+    return gimage
+
+
 def loss_from_partials(partials, H, W, lam=0.2):
     """Loss value from the partial sums written by loss_grad (a device scalar)."""
     _, ns = loss_partials_count(H, W)

@@ -6,7 +6,7 @@ host binning/loss/scatter round trips in between.  Here one step is, on one stre
 host round trip:
 
     geom_fwd (+ Adam step advance) -> assign_bins (5 kernels, + inverse table and tile order)
-             -> splat_fwd -> loss_grad (2 kernels) -> splat_bwd (theta bwd, per-slot gradients)
+             -> splat_fwd -> loss_grad_stats (1 kernel) -> splat_bwd (theta bwd, per-slot gradients)
              -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
 captured once per camera into a HIP graph (torch.cuda.CUDAGraph) and replayed.  The step
@@ -140,6 +140,9 @@ class TrainStep:
         self.targets = [t.to(dev, F32).contiguous() for t in targets]
         if len(self.targets) != len(self.cams):
             raise ValueError("one target image per camera is required")
+        # each target's SSIM statistics, computed once (tools/resident_traced.py:431-464 keeps
+        # its target maps per view the same way)
+        self.target_stats = [kernels.loss_stats(t) for t in self.targets]
         # work buffers
         self.proj = torch.empty(G, 12, device=dev, dtype=F32)
         self.keep = torch.empty(G, device=dev, dtype=U8)
@@ -154,7 +157,6 @@ class TrainStep:
         self.image = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.den = torch.empty(H, W, device=dev, dtype=F32)
         self.gimage = torch.empty(H, W, 3, device=dev, dtype=F32)
-        self.loss_ws = kernels.loss_workspace(H, W, dev)
         self.partials = torch.empty(kernels.loss_partials_count(H, W)[0], device=dev, dtype=F32)
         self.batch = int(batch)
         if self.batch < 1 or len(self.cams) % self.batch:
@@ -207,8 +209,8 @@ class TrainStep:
     def _view_backward(self, ci, advance=False, rebin=True):
         """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
         self.forward(ci, advance, rebin)
-        kernels.loss_grad(self.image, self.targets[ci], self.lam, self.gimage, self.partials,
-                          self.loss_ws)
+        kernels.loss_grad_stats(self.image, self.targets[ci], self.target_stats[ci], self.lam,
+                                self.gimage, self.partials)
         kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                           self.k, self.image, self.den, self.gimage, self.gslot,
                           order=self.order)
