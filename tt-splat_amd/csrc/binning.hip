@@ -14,21 +14,22 @@
 // far gaussians are stored apart (their ids only) and tiles count them from the cell totals;
 // only the selection among saturated ties ever reads them, and then only one cell's list.
 //
-// Passes (stream-ordered, no host round trip):
-//   1. k_bin_count      cell and far flag of each gaussian; per-block LDS histograms, one global
-//                       atomic per non-zero cell; each regular gaussian's rank in its cell,
-//                       each far gaussian's rank among its block's far gaussians of the cell,
-//                       in g order.
-//   2. k_far_colscan    per border cell, exclusive scan of the far counts over count blocks.
-//   3. k_bin_scan       one block: copy offsets and exclusive scans -> cell_start[T+1],
-//                       far_start[T+1]; resets the counters for the next call.  When the tile
-//                       grid fits its LDS (T <= 8192) it also classifies the tiles (a tile's
-//                       candidates are the 3x3 box sum of the cell totals, formed as row
-//                       3-sums then column 3-sums) and writes the heaviest-first tile order;
-//                       larger grids run k_tile_classify / k_tile_order instead.
-//   4. k_bin_scatter    regular gaussians -> (g, mu_x, mu_y) records, far -> g at their ranks:
-//                       every cell's far ids end up ascending.
-//   5. k_bin_select     one block per tile (below).
+// Passes (stream-ordered, no host round trip, no global atomics):
+//   1. k_bin_count      cell and far flag of each gaussian; per-block LDS histograms written as
+//                       one row per block of a count matrix [block][cell | border cell]; each
+//                       regular gaussian's rank in its cell inside the block, each far
+//                       gaussian's rank among its block's far gaussians of the cell, in g order.
+//   2. k_bin_colscan    per column of the matrix, the exclusive scan over blocks (each block's
+//                       base in the cell) and the column total; totals' prefix inside 64-cell
+//                       chunks and the chunk totals.
+//   3. k_bin_scatter    cell_start[T+1], far_start[T+1] from the chunk prefixes; regular
+//                       gaussians -> (g, mu_x, mu_y) records, far -> g at their ranks: every
+//                       cell's far ids end up ascending.  Its first blocks classify the tiles (a
+//                       tile's candidates are the 3x3 box sum of the cell totals) into the heavy
+//                       and light lists, and record per block how many tiles take each order
+//                       key (K - kept count) and each tile's rank among them.
+//   4. k_bin_select     one block per tile (below); it also writes the tile's slot of the
+//                       heaviest-first order, from those per-block key counts.
 // The result does not depend on the order atomics land in.
 
 #include <mutex>
@@ -169,43 +170,56 @@ __device__ __forceinline__ void hist_add(unsigned* h, unsigned b) {
   }
 }
 
-// Count pass.  Each block takes kCountBlock consecutive gaussians; wave w owns the contiguous
-// range [w * kWaveSpan, (w + 1) * kWaveSpan) of them, kCountPerLane rounds of 64 (so the block
-// order (wave, round, lane) is g order).  Every round's loads are issued up front.
-// Regular gaussians: per-cell counts in LDS (REG_LDS) or global atomics, and the gaussian's rank
-// in its cell (any order); the cells the block touched are listed as they are first counted, and
-// each gets one global atomic at the end.
-// Far gaussians: a rank that is stable in g order inside the block: lanes in order through
+// Count pass.  A block of NT threads takes NT/64 * 64 * PER consecutive gaussians; wave w owns
+// the contiguous range [w * 64 * PER, (w + 1) * 64 * PER), PER rounds of 64 (so the block order
+// (wave, round, lane) is g order).  Every round's loads are issued up front.
+// Regular gaussians: per-cell counts in an LDS histogram and each gaussian's rank in its cell
+// inside the block, in LDS-atomic order (any order serves: the select pass orders by key).
+// Far gaussians: a rank inside the block that is stable in g order: lanes in order through
 // ballots, rounds in order through a running per-cell count private to the wave, waves in order
-// through the waves' totals (one block barrier).  The block's per-border-cell totals go to
-// far_blk[b][block]; a column scan over blocks (k_far_colscan) then makes every cell's far list
-// ascending in g.
-constexpr int kCountPerLane = 2;
-constexpr int kWaveSpan = 64 * kCountPerLane;
-constexpr int kCountBlock = 4 * kWaveSpan;
-constexpr int kMaxLdsCells = 12288;
-constexpr int kMaxBorder = 1024;   // far handling needs 4 * NB ints of LDS
+// through the earlier waves' totals (one block barrier).
+// The block writes its row of the count matrix mat[block][Tpad + NB]: the regular counts of the
+// Tpad cells, then the far counts of the NB border cells.  No global atomics: k_bin_colscan
+// turns the rows into per-block bases.
+constexpr int kMaxLdsInts = 38912;   // count-pass LDS (Tpad + waves * NB ints, 152 KB)
+constexpr int kMaxCountWaves = 16;
+constexpr int kMaxBorder = 1024;     // border cells with far handling (one per scatter thread)
+constexpr int kChunk = 64;           // column-scan chunk (cells)
+constexpr int kMaxCountRows = 256;   // count blocks: small blocks while the matrix stays short
 
-template <bool REG_LDS>
-__global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2d, int mu_stride,
-                                                   const uint8_t* __restrict__ keep,
-                                                   int keep_stride, int G, int ntx, int nty,
-                                                   float S, int span, int NB,
-                                                   int* __restrict__ reg_cnt,
-                                                   int* __restrict__ far_blk, int nblk,
-                                                   int2* __restrict__ cell_slot) {
+// Count-pass geometry: NT threads, PER rounds of 64 per wave.  Small blocks (256 x 2) spread a
+// small G over many CUs; once that would make the count matrix longer than kMaxCountRows rows,
+// large blocks (1024 x 4) keep it short.
+template <int NT, int PER>
+struct CountGeo {
+  static constexpr int kWaves = NT / 64;
+  static constexpr int kWaveSpan = 64 * PER;
+  static constexpr int kBlock = kWaves * kWaveSpan;
+};
+using CountSmall = CountGeo<256, 2>;
+using CountLarge = CountGeo<1024, 4>;
+inline int count_block(int G) {
+  return (G + CountSmall::kBlock - 1) / CountSmall::kBlock <= kMaxCountRows ? CountSmall::kBlock
+                                                                            : CountLarge::kBlock;
+}
+
+__host__ __device__ __forceinline__ int pad_cells(int T) { return (T + kChunk - 1) / kChunk * kChunk; }
+
+template <int NT, int PER>
+__global__ __launch_bounds__(NT) void k_bin_count(
+    const float* __restrict__ mu2d, int mu_stride, const uint8_t* __restrict__ keep,
+    int keep_stride, int G, int ntx, int nty, float S, int span, int NB, int Tpad,
+    int* __restrict__ mat, int2* __restrict__ cell_slot) {
+  using C = CountGeo<NT, PER>;
+  constexpr int kCountPerLane = PER;
   extern __shared__ int s_lds[];
-  __shared__ int s_touched[kCountBlock];
-  __shared__ int s_ntouched;
-  const int T = ntx * nty;
-  int* s_wrun = s_lds;            // [4][NB] far count per wave (running, then the wave total)
-  int* s_reg = s_lds + 4 * NB;    // [T] (REG_LDS)
-  const int nl = 4 * NB + (REG_LDS ? T : 0);
-  for (int c = threadIdx.x; c < nl; c += blockDim.x) s_lds[c] = 0;
-  if (threadIdx.x == 0) s_ntouched = 0;
+  int* s_reg = s_lds;            // [Tpad] regular count per cell
+  int* s_wrun = s_lds + Tpad;    // [waves][NB] far count per wave (running, then total)
+  const int nl = Tpad + C::kWaves * NB;
+  for (int c = threadIdx.x; c < nl; c += NT) s_lds[c] = 0;
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = lane_id();
-  const int g0 = blockIdx.x * kCountBlock + wave * kWaveSpan + lane;
+  const int g0 = blockIdx.x * C::kBlock + wave * C::kWaveSpan + lane;
   // loads from clamped indices, unconditionally, so that all of them are in flight at once
   float mx[kCountPerLane], my[kCountPerLane];
   uint8_t kv[kCountPerLane];
@@ -216,17 +230,13 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
     mx[i] = mu2d[(int64_t)gc * mu_stride];
     my[i] = mu2d[(int64_t)gc * mu_stride + 1];
   }
-  bool kp[kCountPerLane];
-#pragma unroll
-  for (int i = 0; i < kCountPerLane; ++i) kp[i] = (g0 + 64 * i < G) && kv[i] != 0;
   int cell[kCountPerLane], rank[kCountPerLane];
   bool farv[kCountPerLane];
-  // classification (ALU only)
 #pragma unroll
   for (int i = 0; i < kCountPerLane; ++i) {
     int c = -1;
     bool far = false;
-    if (kp[i]) {
+    if (g0 + 64 * i < G && kv[i] != 0) {
       c = classify(mx[i], my[i], S, ntx, nty, span, &far);
       far = far && NB > 0;
     }
@@ -234,36 +244,9 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
     farv[i] = far;
     rank[i] = 0;
   }
-  // regular ranks: plain LDS atomics, all rounds in flight
-  if (REG_LDS) {
 #pragma unroll
-    for (int i = 0; i < kCountPerLane; ++i)
-      if (cell[i] >= 0 && !farv[i]) rank[i] = atomicAdd(&s_reg[cell[i]], 1);
-    // a cell counted first by this lane goes on the block's touched list
-#pragma unroll
-    for (int i = 0; i < kCountPerLane; ++i) {
-      const int p = wave_append(&s_ntouched, cell[i] >= 0 && !farv[i] && rank[i] == 0);
-      if (p >= 0) s_touched[p] = cell[i];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < kCountPerLane; ++i)
-      if (cell[i] >= 0 && !farv[i]) rank[i] = atomicAdd(&reg_cnt[cell[i]], 1);
-  }
-  // REG_LDS: once the block's regular counts are final, one global atomic per touched cell
-  // (at most kCountBlock of them, two per thread) takes the block's base in the cell.  They are
-  // issued here and their results used only after the far ranks, which they do not touch, so
-  // the round trip overlaps that work.
-  static_assert(kCountBlock <= 2 * 256, "two touched cells per thread");
-  int tc0 = -1, tc1 = -1, tb0, tb1;  // tbK is set and read only when tcK >= 0
-  if (REG_LDS) {
-    __syncthreads();
-    const int nt = s_ntouched;
-    if ((int)threadIdx.x < nt) tc0 = s_touched[threadIdx.x];
-    if ((int)threadIdx.x + 256 < nt) tc1 = s_touched[threadIdx.x + 256];
-    if (tc0 >= 0) tb0 = atomicAdd(&reg_cnt[tc0], s_reg[tc0]);
-    if (tc1 >= 0) tb1 = atomicAdd(&reg_cnt[tc1], s_reg[tc1]);
-  }
+  for (int i = 0; i < kCountPerLane; ++i)
+    if (cell[i] >= 0 && !farv[i]) rank[i] = atomicAdd(&s_reg[cell[i]], 1);
   // far ranks inside the wave's range: per round, lanes of one cell are grouped by ballots
   // (registers only); each group's leader then adds the group to the wave's running count of
   // the cell with one LDS atomic, and the lanes take the returned base from their leader.
@@ -305,240 +288,223 @@ __global__ __launch_bounds__(256) void k_bin_count(const float* __restrict__ mu2
         for (int w = 0; w < wave; ++w) rank[i] += s_wrun[w * NB + b];
       }
     }
-    for (int b = threadIdx.x; b < NB; b += blockDim.x)
-      far_blk[(int64_t)b * nblk + blockIdx.x] =
-          s_wrun[b] + s_wrun[NB + b] + s_wrun[2 * NB + b] + s_wrun[3 * NB + b];
   }
-  if (REG_LDS) {
-    // each touched cell is listed once: this thread alone rewrites its entry with the base
-    if (tc0 >= 0) s_reg[tc0] = tb0;
-    if (tc1 >= 0) s_reg[tc1] = tb1;
-    __syncthreads();
+  int* row = mat + (int64_t)blockIdx.x * (Tpad + NB);
+  for (int c = threadIdx.x; c < Tpad; c += NT) row[c] = s_reg[c];
+  for (int b = threadIdx.x; b < NB; b += NT) {
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < C::kWaves; ++w) s += s_wrun[w * NB + b];
+    row[Tpad + b] = s;
   }
 #pragma unroll
   for (int i = 0; i < kCountPerLane; ++i) {
     const int g = g0 + 64 * i;
-    if (g >= G) continue;
-    int2 cs = make_int2(-1, 0);
-    if (cell[i] >= 0) {
-      const bool far = (cell[i] >> kFarBit) & 1;
-      cs = make_int2(cell[i], (REG_LDS && !far) ? s_reg[cell[i]] + rank[i] : rank[i]);
-    }
-    cell_slot[g] = cs;
+    if (g < G) cell_slot[g] = cell[i] >= 0 ? make_int2(cell[i], rank[i]) : make_int2(-1, 0);
   }
 }
 
-// Exclusive scan of far_blk[b][0..nblk) for each border cell b (one block per cell); the total
-// is the cell's far count.
-__global__ __launch_bounds__(256) void k_far_colscan(int* __restrict__ far_blk, int nblk,
-                                                     int ntx, int nty,
-                                                     int* __restrict__ far_cnt) {
-  __shared__ int s_tmp[4];
-  int* row = far_blk + (int64_t)blockIdx.x * nblk;
-  int carry = 0;
-  for (int b0 = 0; b0 < nblk; b0 += 256) {
-    const int i = b0 + threadIdx.x;
-    const int v = i < nblk ? row[i] : 0;
-    int total;
-    const int ex = block_excl_scan256(v, s_tmp, &total);
-    if (i < nblk) row[i] = carry + ex;
-    carry += total;
+// Column scan of the count matrix, one block per chunk of 64 columns: 16 segments of rows per
+// column summed in parallel, the segment sums scanned, the rows rewritten in place with their
+// exclusive prefix over count blocks (a block's base in the cell).  Also the column totals
+// tot[x], their exclusive prefix inside the chunk within[x], and the chunk's total.  Block 0
+// also zeroes the counters the scatter pass's classification blocks accumulate into.
+__global__ __launch_bounds__(1024) void k_bin_colscan(int* __restrict__ mat, int nblk, int X,
+                                                      int* __restrict__ tot,
+                                                      int* __restrict__ within,
+                                                      int* __restrict__ chunk_tot,
+                                                      int* __restrict__ cls_ctr, int n_ctr) {
+  __shared__ int s_seg[16][kChunk];
+  // the scatter pass's list counters start from zero
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i < n_ctr; i += 1024) cls_ctr[i] = 0;
+  const int col = threadIdx.x & (kChunk - 1), seg = threadIdx.x >> 6;
+  const int x = blockIdx.x * kChunk + col;
+  const int rows = (nblk + 15) / 16;
+  const int r0 = min(seg * rows, nblk), r1 = min(r0 + rows, nblk);
+  int sum = 0;
+  if (x < X) {
+    for (int rb = r0; rb < r1; rb += 16) {
+      int v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = rb + k < r1 ? mat[(int64_t)(rb + k) * X + x] : 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sum += v[k];
+    }
   }
-  if (threadIdx.x == 0) far_cnt[border_cell(blockIdx.x, ntx, nty)] = carry;
+  s_seg[seg][col] = sum;
+  __syncthreads();
+  int total = 0;
+  if (seg == 0) {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      const int v = s_seg[s][col];
+      s_seg[s][col] = total;
+      total += v;
+    }
+  }
+  __syncthreads();
+  if (x < X) {
+    int base = s_seg[seg][col];
+    for (int rb = r0; rb < r1; rb += 16) {
+      int v[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) v[k] = rb + k < r1 ? mat[(int64_t)(rb + k) * X + x] : 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (rb + k < r1) mat[(int64_t)(rb + k) * X + x] = base;
+        base += v[k];
+      }
+    }
+  }
+  if (seg == 0) {  // wave 0: the chunk's 64 columns
+    const int incl = wave_incl_scan(total);
+    if (x < X) {
+      tot[x] = total;
+      within[x] = incl - total;
+    }
+    if (col == kChunk - 1) chunk_tot[blockIdx.x] = incl;
+  }
 }
 
-// Cell offsets, one block: exclusive scans of the regular and far counts -> cell_start[T+1],
-// far_start[T+1]; both counters are reset to zero for the next call.  Values are staged
-// through LDS so every global access is coalesced.
-//
-// When the whole grid fits one chunk (T <= kScanChunk) the same block also classifies the tiles
-// from the starts still in LDS (what k_tile_classify does otherwise): tiles with more than K
-// candidates go to lists[0..nlist[0]), the others to lists[T-1], lists[T-2], ...; and, when
-// `order` is given, it writes the tiles ordered by kept count min(candidates, K), heaviest first
-// (a counting sort; the splat kernels' block -> tile map), so no separate order pass runs.
-constexpr int kScanChunk = 8192;
+// Rank of border index b in cell order (top row, then left and right cell of each inner row,
+// then the bottom row).
+__device__ __forceinline__ int border_rank(int b, int ntx, int nty) {
+  if (nty == 1 || ntx == 1) return b;
+  if (b < ntx) return b;
+  if (b < 2 * ntx) return ntx + 2 * (nty - 2) + (b - ntx);
+  if (b < 2 * ntx + (nty - 2)) return ntx + 2 * (b - 2 * ntx);
+  return ntx + 2 * (b - 2 * ntx - (nty - 2)) + 1;
+}
 
-__global__ __launch_bounds__(1024) void k_bin_scan(int* __restrict__ reg_cnt,
-                                                   int* __restrict__ far_cnt,
-                                                   int* __restrict__ cell_start,
-                                                   int* __restrict__ far_start, int ntx, int nty,
-                                                   int K, int fuse, int* __restrict__ lists,
-                                                   int* __restrict__ nlist,
-                                                   int32_t* __restrict__ order) {
-  __shared__ int s_v[2][kScanChunk];
-  __shared__ int s_tmp[32];
-  __shared__ int s_n[kScanChunk];     // fused: cell totals, then their row 3-sums
-  __shared__ int s_bins[kMaxK + 2];   // fused: counting-sort buckets
-  const int T = ntx * nty;
-  if (fuse) {
-    // ---- T <= kScanChunk: counts, starts and the tile classification all in LDS ----
-    int* s_r = s_v[0];
-    int* s_f = s_v[1];
-    for (int i = threadIdx.x; i < T; i += 1024) {
-      const int r = reg_cnt[i], f = far_cnt[i];
-      s_r[i] = r;
-      s_f[i] = f;
-      s_n[i] = r + f;
-      reg_cnt[i] = 0;
-      far_cnt[i] = 0;
-    }
-    for (int c = threadIdx.x; c <= K + 1; c += 1024) s_bins[c] = 0;
-    __syncthreads();
-    // thread = tiles [lo, lo + per): its partial sums of both counts, and the row 3-sums of the
-    // cell totals (a tile's candidates are the 3x3 box sum of the totals around its cell)
-    constexpr int kPer = kScanChunk / 1024;
-    const int per = (T + 1023) / 1024;
-    const int lo = threadIdx.x * per;
-    int sr = 0, sf = 0, hs[kPer];
+struct ScatterArgs {
+  const float* mu2d;
+  int mu_stride, G, ntx, nty, NB, Tpad, K, cblock, ncls;
+  const int2* cell_slot;
+  const int* mat;
+  const int* tot;
+  const int* within;
+  const int* chunk_tot;
+  int* cell_start;
+  int* far_start;
+  int4* recs;
+  int* far_g;
+  int32_t* inv;
+  int* lists;
+  int* nlist;       // [2] heavy, light tiles listed (zeroed by k_bin_colscan)
+  int* key_hist;    // [K+1][ncls] tiles per order key in each classification block
+  int* tile_pos;    // [T] a tile's rank among its classification block's tiles of its key
+};
+
+// Classification, block cb: tiles [1024 cb, 1024 (cb + 1)).  A tile's candidates are the 3x3 box
+// sum of the cell totals (regular + far).  Tiles with more than K candidates go to the front of
+// lists, the others to the back (lists[T-1], lists[T-2], ...), in no particular order (one
+// atomic per block and list places the block's tiles).  The order key K - min(candidates, K)
+// sorts by kept count, heaviest first: the block writes its tiles' count per key (column cb of
+// key_hist) and each tile's rank among them (tile_pos); k_bin_select turns these into the
+// tile's slot of the order.
+__device__ void classify_tiles(const ScatterArgs& a, int cb, int* s_bins, int* s_tmp) {
+  const int ntx = a.ntx, nty = a.nty, T = ntx * nty, K = a.K;
+  __shared__ int s_hbase, s_lbase;
+  for (int c = threadIdx.x; c <= K; c += 1024) s_bins[c] = 0;
+  const int t = cb * 1024 + threadIdx.x;
+  int nc = -1;
+  if (t < T) {
+    const int tx = t % ntx, ty = t / ntx;
+    nc = 0;
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int t = lo + k;
-      hs[k] = 0;
-      if (k < per && t < T) {
-        sr += s_r[t];
-        sf += s_f[t];
-        const int tx = t % ntx;
-        hs[k] = s_n[t] + (tx > 0 ? s_n[t - 1] : 0) + (tx + 1 < ntx ? s_n[t + 1] : 0);
-      }
-    }
-    int tr, tf, er, ef;  // barriers inside: every LDS read above is done
-    block_excl_scan2<1024>(sr, sf, s_tmp, &er, &ef, &tr, &tf);
+    for (int dy = -1; dy <= 1; ++dy) {
 #pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int t = lo + k;
-      if (k < per && t < T) {
-        const int r = s_r[t], f = s_f[t];
-        s_r[t] = er;
-        s_f[t] = ef;
-        er += r;
-        ef += f;
-        s_n[t] = hs[k];
-      }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < T; i += 1024) {
-      cell_start[i] = s_r[i];
-      far_start[i] = s_f[i];
-    }
-    if (threadIdx.x == 0) {
-      cell_start[T] = tr;
-      far_start[T] = tf;
-    }
-    // classification: candidates <= K -> light, else heavy.  Each thread takes its contiguous
-    // tiles [lo, lo + per) again, and one block scan of its packed counts (heavy << 16 | light,
-    // totals <= 8192) places them: heavy tiles to lists[0, ...), light ones to lists[T-1],
-    // lists[T-2], ..., both in ascending tile order.  The kept count every tile ends with,
-    // min(candidates, K), keys the heaviest-first order (histogram here, placement below).
-    int ncs[kPer];
-    int nh = 0, nlt = 0;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int t = lo + k;
-      ncs[k] = -1;
-      if (k < per && t < T) {
-        const int ty = t / ntx;
-        const int nc = s_n[t] + (ty > 0 ? s_n[t - ntx] : 0) + (ty + 1 < nty ? s_n[t + ntx] : 0);
-        ncs[k] = nc;
-        nh += nc > K;
-        nlt += nc <= K;
-        if (order) agg_inc(s_bins, K - min(nc, K));
-      }
-    }
-    int tot;
-    const int ex = block_excl_scan<1024>((nh << 16) | nlt, s_tmp, &tot);
-    int ph = ex >> 16, pl = ex & 0xffff;
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      if (ncs[k] >= 0) {
-        const int t = lo + k;
-        if (ncs[k] > K) lists[ph++] = t;
-        else lists[T - 1 - pl++] = t;
-      }
-    }
-    if (threadIdx.x == 0) {
-      nlist[0] = tot >> 16;
-      nlist[1] = tot & 0xffff;
-    }
-    if (!order) return;
-    // K + 1 <= 513 buckets: one per thread
-    const int v = threadIdx.x <= K ? s_bins[threadIdx.x] : 0;
-    int total;
-    const int bx = block_excl_scan<1024>(v, s_tmp, &total);
-    if (threadIdx.x <= K) s_bins[threadIdx.x] = bx;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kPer; ++k)
-      if (ncs[k] >= 0) order[agg_inc(s_bins, K - min(ncs[k], K))] = lo + k;
-    return;
-  }
-  // ---- larger grids: chunked scans; k_tile_classify / k_tile_order run separately ----
-  int carry[2] = {0, 0};
-  for (int base = 0; base < T; base += kScanChunk) {
-    const int n = min(kScanChunk, T - base);
-    for (int i = threadIdx.x; i < n; i += 1024) {
-      s_v[0][i] = reg_cnt[base + i];
-      s_v[1][i] = far_cnt[base + i];
-      reg_cnt[base + i] = 0;
-      far_cnt[base + i] = 0;
-    }
-    __syncthreads();
-    const int per = (n + 1023) / 1024;
-    const int lo = threadIdx.x * per;
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      int sum = 0;
-      for (int k = 0; k < per; ++k)
-        if (lo + k < n) sum += s_v[w][lo + k];
-      int total;
-      int ex = block_excl_scan<1024>(sum, s_tmp + 16 * w, &total) + carry[w];
-      for (int k = 0; k < per; ++k) {
-        if (lo + k < n) {
-          const int v = s_v[w][lo + k];
-          s_v[w][lo + k] = ex;
-          ex += v;
+      for (int dx = -1; dx <= 1; ++dx) {
+        const int cx = tx + dx, cy = ty + dy;
+        if (cx >= 0 && cx < ntx && cy >= 0 && cy < nty) {
+          nc += a.tot[cy * ntx + cx];
+          if (a.NB > 0 && (cx == 0 || cx == ntx - 1 || cy == 0 || cy == nty - 1))
+            nc += a.tot[a.Tpad + border_index(cx, cy, ntx, nty)];
         }
       }
-      carry[w] += total;
     }
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += 1024) {
-      cell_start[base + i] = s_v[0][i];
-      far_start[base + i] = s_v[1][i];
-    }
-    __syncthreads();
   }
+  __syncthreads();
+  const bool heavy = nc > K, light = nc >= 0 && nc <= K;
+  int nh, nl;
+  const int eh = block_excl_scan<1024>(heavy ? 1 : 0, s_tmp, &nh);
+  const int el = block_excl_scan<1024>(light ? 1 : 0, s_tmp, &nl);
   if (threadIdx.x == 0) {
-    cell_start[T] = carry[0];
-    far_start[T] = carry[1];
-    nlist[0] = 0;  // tile lists of k_tile_classify
-    nlist[1] = 0;
+    s_hbase = nh ? atomicAdd(&a.nlist[0], nh) : 0;
+    s_lbase = nl ? atomicAdd(&a.nlist[1], nl) : 0;
   }
+  const int key = nc >= 0 ? K - min(nc, K) : 0;
+  const int lrank = nc >= 0 ? agg_inc(s_bins, key) : 0;
+  __syncthreads();
+  if (heavy) a.lists[s_hbase + eh] = t;
+  if (light) a.lists[T - 1 - (s_lbase + el)] = t;
+  if (nc >= 0) a.tile_pos[t] = lrank;
+  for (int k = threadIdx.x; k <= K; k += 1024) a.key_hist[k * a.ncls + cb] = s_bins[k];
 }
 
-__global__ __launch_bounds__(256) void k_bin_scatter(const float* __restrict__ mu2d, int mu_stride,
-                                                     int G, int ntx, int nty,
-                                                     const int2* __restrict__ cell_slot,
-                                                     const int* __restrict__ cell_start,
-                                                     const int* __restrict__ far_start,
-                                                     const int* __restrict__ far_blk, int nblk,
-                                                     int4* __restrict__ recs,
-                                                     int* __restrict__ far_g,
-                                                     int32_t* __restrict__ inv) {
-  const int g = blockIdx.x * blockDim.x + threadIdx.x;
-  if (g >= G) return;
-  if (inv) {  // no slot yet: k_bin_select fills the kept (g, j) entries
-#pragma unroll
-    for (int j = 0; j < 9; ++j) inv[(int64_t)g * 9 + j] = -1;
+// Scatter pass.  Blocks [0, ncls) classify the tiles (above).  Every other block first forms, in
+// LDS, the exclusive prefix of the regular chunk totals and the far counts' prefix in cell
+// order; block ncls + i then writes cell_start / far_start for cells [1024 i, 1024 (i + 1)) and
+// places gaussian 1024 i + threadIdx.x: regular ones as (g, mu_x, mu_y) records at cell_start +
+// its count block's base in the cell + its rank, far ones as ids at far_start + its count
+// block's base + its rank, so every cell's far ids end up ascending.
+__global__ __launch_bounds__(1024) void k_bin_scatter(ScatterArgs a) {
+  __shared__ int s_cpre[kMaxLdsInts / kChunk];
+  __shared__ int s_fp[kMaxBorder + 1];
+  __shared__ int s_tmp[32];
+  __shared__ int s_bins[kMaxK + 2];
+  if (static_cast<int>(blockIdx.x) < a.ncls) {
+    classify_tiles(a, blockIdx.x, s_bins, s_tmp);
+    return;
   }
-  const int2 cs = cell_slot[g];
-  const float mx = mu2d[(int64_t)g * mu_stride], my = mu2d[(int64_t)g * mu_stride + 1];
+  const int ntx = a.ntx, nty = a.nty, T = ntx * nty, NB = a.NB;
+  const int tid = threadIdx.x;
+  const int nch = a.Tpad / kChunk;
+  int regtot;
+  const int cex = block_excl_scan<1024>(tid < nch ? a.chunk_tot[tid] : 0, s_tmp, &regtot);
+  if (tid < nch) s_cpre[tid] = cex;
+  if (tid < NB) s_fp[border_rank(tid, ntx, nty)] = a.tot[a.Tpad + tid];
+  __syncthreads();
+  int ftot;
+  const int fex = block_excl_scan<1024>(tid < NB ? s_fp[tid] : 0, s_tmp, &ftot);
+  if (tid < NB) s_fp[tid] = fex;
+  __syncthreads();
+  const int i0 = (blockIdx.x - a.ncls) * 1024 + tid;
+  if (i0 <= T) {
+    const int c = i0;
+    int fs = ftot;
+    if (c < T && NB > 0) {
+      const int cx = c % ntx, cy = c / ntx;
+      const bool border = cx == 0 || cx == ntx - 1 || cy == 0 || cy == nty - 1;
+      // an inner cell follows its row's left border cell: the prefix up to its right one
+      fs = s_fp[border ? border_rank(border_index(cx, cy, ntx, nty), ntx, nty)
+                       : ntx + 2 * (cy - 1) + 1];
+    } else if (c < T) {
+      fs = 0;
+    }
+    a.cell_start[c] = c < T ? s_cpre[c / kChunk] + a.within[c] : regtot;
+    a.far_start[c] = fs;
+  }
+  const int g = i0;
+  if (g >= a.G) return;
+  if (a.inv) {  // no slot yet: k_bin_select fills the kept (g, j) entries
+#pragma unroll
+    for (int j = 0; j < 9; ++j) a.inv[(int64_t)g * 9 + j] = -1;
+  }
+  const int2 cs = a.cell_slot[g];
   if (cs.x < 0) return;
+  const int X = a.Tpad + NB;
+  const int* row = a.mat + (int64_t)(g / a.cblock) * X;
   if (cs.x >> kFarBit) {
     const int c = cs.x & ~(1 << kFarBit);
     const int b = border_index(c % ntx, c / ntx, ntx, nty);
-    far_g[far_start[c] + far_blk[(int64_t)b * nblk + g / kCountBlock] + cs.y] = g;
+    a.far_g[s_fp[border_rank(b, ntx, nty)] + row[a.Tpad + b] + cs.y] = g;
   } else {
-    recs[cell_start[cs.x] + cs.y] = make_int4(g, __float_as_int(mx), __float_as_int(my), 0);
+    const float mx = a.mu2d[(int64_t)g * a.mu_stride], my = a.mu2d[(int64_t)g * a.mu_stride + 1];
+    const int c = cs.x;
+    a.recs[s_cpre[c / kChunk] + a.within[c] + row[c] + cs.y] =
+        make_int4(g, __float_as_int(mx), __float_as_int(my), 0);
   }
 }
 
@@ -717,7 +683,26 @@ struct SelectArgs {
   int32_t* count;
   int32_t* ncand;
   int32_t* inv;
+  int32_t* order;          // heaviest-first tile order (may be null)
+  const int* key_hist;     // [K+1][ncls] per classification block tiles per order key
+  const int* tile_pos;     // [T] rank among its classification block's tiles of its key
+  int ncls;
 };
+
+// Slot of tile t (n candidates) in the heaviest-first order: tiles of smaller keys (more kept
+// slots), then this key's tiles of earlier classification blocks, then its rank in its block.
+// A lane sums whole keys (key-major table, no division); full tiles (key 0) need only their
+// own key's earlier blocks.  Every lane of the wave calls; the slot comes back in every lane.
+__device__ __forceinline__ int order_slot(const SelectArgs& a, int t, int n) {
+  const int key = a.K - min(n, a.K), cb = t >> 10, nc = a.ncls;
+  int s = 0;
+  for (int k = lane_id(); k <= key; k += 64) {
+    const int* h = a.key_hist + k * nc;
+    const int nb = k < key ? nc : cb;
+    for (int b = 0; b < nb; ++b) s += h[b];
+  }
+  return read_lane(wave_incl_scan(s), 63) + a.tile_pos[t];
+}
 
 // Light tile (n <= K candidates: all survive), one wave: collect the keys in LDS, then place
 // them by rank.
@@ -758,36 +743,14 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
       a.valid[base + s] = 0;
     }
   }
+  if (a.order) {
+    const int slot = order_slot(a, t, m);
+    if (lane == 0) a.order[slot] = t;
+  }
   if (lane == 0) {
     if (a.count) a.count[t] = m;
     if (a.ncand) a.ncand[t] = m;
   }
-}
-
-// Tiles with more than K candidates go to lists[0..nlist[0]), the others to
-// lists[T-1], lists[T-2], ... (nlist[1] of them).  nlist is zeroed by k_bin_scan.
-__global__ __launch_bounds__(256) void k_tile_classify(const int* __restrict__ cell_start,
-                                                       const int* __restrict__ far_start,
-                                                       int ntx, int nty, int K,
-                                                       int* __restrict__ lists,
-                                                       int* __restrict__ nlist) {
-  const int T = ntx * nty;
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  int n = 0;
-  if (t < T) {
-    const int tx = t % ntx, ty = t / ntx;
-    for (int j = 0; j < 9; ++j) {
-      const int cx = tx - (j % 3 - 1), cy = ty - (j / 3 - 1);
-      if (cx >= 0 && cx < ntx && cy >= 0 && cy < nty) {
-        const int c = cy * ntx + cx;
-        n += cell_start[c + 1] - cell_start[c] + far_start[c + 1] - far_start[c];
-      }
-    }
-  }
-  const int ph = wave_append(&nlist[0], t < T && n > K);
-  if (ph >= 0) lists[ph] = t;
-  const int pl = wave_append(&nlist[1], t < T && n <= K);
-  if (pl >= 0) lists[T - 1 - pl] = t;
 }
 
 // One block of NT threads per heavy tile, then one wave per light tile (NT/64 per block).
@@ -846,10 +809,14 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     s_tfill = 0;
   }
   if (threadIdx.x < 9) s_sat[threadIdx.x] = 0;
+  // heavy tiles (every block of this range) histogram qd2: zeroed while the cells load
+  for (int b = threadIdx.x; b < span; b += NT) s_hist[b] = 0;
   __syncthreads();
   const int nreg = tc.pre[9], nfar = tc.fpre[9];
   const int n = nreg + nfar;
   const int satq = span - 1;
+  // wave 0 takes the tile's order slot now; its loads overlap the candidate walks
+  const int oslot = (a.order && threadIdx.x < 64) ? order_slot(a, t, n) : 0;
 
   if (n <= K) {
     for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
@@ -862,8 +829,6 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
       s_keys[wave_append(&s_fill, true)] = make_key(satq, j, far_g[tc.fstart[j] + i - tc.fpre[j]]);
     }
   } else {
-    for (int b = threadIdx.x; b < span; b += NT) s_hist[b] = 0;
-    __syncthreads();
     for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
       const unsigned q = static_cast<unsigned>(key >> kQShift);
       hist_add(s_hist, q);
@@ -1013,26 +978,36 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     }
   }
   __syncthreads();
-  // Place the m survivors by rank (unique keys: rank = number of smaller survivors).
+  // Place the m survivors by rank (unique keys: rank = number of smaller survivors).  Two
+  // adjacent lanes share a survivor, each counting over half of them.
   const int m = min(s_fill, K);
   const int64_t base = static_cast<int64_t>(t) * K;
-  for (int s = threadIdx.x; s < K; s += NT) {
-    if (s < m) {
-      const unsigned long long key = s_keys[s];
-      int rank = 0;
-      for (int e = 0; e < m; ++e) rank += (s_keys[e] < key) ? 1 : 0;
-      const int g = static_cast<int32_t>(key & 0xffffffffull);
-      a.idx[base + rank] = g;
-      if (a.inv) a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-      a.valid[base + rank] = 1;
-    } else {
-      a.idx[base + s] = 0;
-      a.valid[base + s] = 0;
+  const int half = threadIdx.x & 1;
+  const int e0 = half ? (m + 1) / 2 : 0, e1 = half ? m : (m + 1) / 2;
+  for (int s0 = 0; s0 < K; s0 += NT / 2) {
+    const int s = s0 + (static_cast<int>(threadIdx.x) >> 1);
+    const unsigned long long key = s < m ? s_keys[s] : 0ull;
+    int rank = 0;
+    if (s < m)
+      for (int e = e0; e < e1; ++e) rank += (s_keys[e] < key) ? 1 : 0;
+    rank += __shfl_xor(rank, 1);
+    if (half == 0 && s < K) {
+      if (s < m) {
+        const int g = static_cast<int32_t>(key & 0xffffffffull);
+        a.idx[base + rank] = g;
+        if (a.inv)
+          a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
+        a.valid[base + rank] = 1;
+      } else {
+        a.idx[base + s] = 0;
+        a.valid[base + s] = 0;
+      }
     }
   }
   if (threadIdx.x == 0) {
     if (a.count) a.count[t] = m;
     if (a.ncand) a.ncand[t] = n;
+    if (a.order) a.order[oslot] = t;
   }
 }
 
@@ -1060,33 +1035,39 @@ __global__ __launch_bounds__(1024) void k_tile_order(const int32_t* __restrict__
 }
 
 struct BinWorkspace {
-  int* reg_cnt;     // [T]   zero between calls
-  int* far_cnt;     // [T]   zero between calls
+  int* mat;         // [nblk][Tpad + NB] counts per (count block, column), then block bases
+  int* tot;         // [Tpad + NB] column totals: regular count per cell, far count per border cell
+  int* within;      // [Tpad + NB] exclusive prefix of tot inside its 64-column chunk
+  int* chunk_tot;   // [(Tpad + NB) / 64 + 1] chunk totals
   int* cell_start;  // [T+1]
   int* far_start;   // [T+1]
-  int* far_blk;     // [NB][nblk] far count per (border cell, count block), then its column scan
   int2* cell_slot;  // [G]
   int4* recs;       // [G]
   int* far_g;       // [G]
   int* lists;       // [T]  heavy tiles from the front, light tiles from the back
-  int* nlist;       // [2]  heavy, light counts
+  int* nlist;       // [2] heavy, light counts
+  int* key_hist;    // [K+1][ncls] tiles per order key per classification block
+  int* tile_pos;    // [T] rank of a tile among its classification block's tiles of its key
   int NB;           // border cells with far handling (0: every gaussian is regular)
+  int Tpad;         // cells rounded up to whole 64-column chunks
+  int cblock;       // gaussians per count block
   int nblk;         // count-pass blocks
 };
 
-// Far handling is on when the border fits the count pass's LDS tables and the per-block table
-// stays small.
-inline int far_border_cells(int G, int ntx, int nty) {
+// Far handling is on when the count pass's LDS holds the border's per-wave tables beside the
+// cell histogram.
+inline int far_border_cells(int ntx, int nty) {
   const int NB = border_count(ntx, nty);
-  const long long nblk = (G + kCountBlock - 1) / kCountBlock;
-  return (NB <= kMaxBorder && nblk * NB <= (1ll << 26)) ? NB : 0;
+  return (NB <= kMaxBorder && pad_cells(ntx * nty) + kMaxCountWaves * NB <= kMaxLdsInts) ? NB : 0;
 }
-
 
 inline size_t bin_ws_layout(int G, int ntx, int nty, char* base, BinWorkspace* ws) {
   const int T = ntx * nty;
-  const int NB = far_border_cells(G, ntx, nty);
-  const int nblk = (G + kCountBlock - 1) / kCountBlock;
+  const int NB = far_border_cells(ntx, nty);
+  const int Tpad = pad_cells(T);
+  const int cblock = count_block(G);
+  const int nblk = (G + cblock - 1) / cblock;
+  const size_t X = (size_t)Tpad + NB;
   size_t off = 0;
   auto take = [&](size_t bytes) {
     char* p = base ? base + off : nullptr;
@@ -1094,29 +1075,37 @@ inline size_t bin_ws_layout(int G, int ntx, int nty, char* base, BinWorkspace* w
     return p;
   };
   const size_t g1 = (size_t)(G > 0 ? G : 1);
-  char* a = take(sizeof(int) * (size_t)T);
-  char* a2 = take(sizeof(int) * (size_t)T);
+  char* m = take(sizeof(int) * ((size_t)nblk * X + 1));
+  char* t = take(sizeof(int) * X);
+  char* w = take(sizeof(int) * X);
+  char* ct = take(sizeof(int) * (X / kChunk + 2));
   char* b = take(sizeof(int) * ((size_t)T + 1));
   char* b2 = take(sizeof(int) * ((size_t)T + 1));
-  char* f = take(sizeof(int) * ((size_t)NB * nblk + 1));
   char* c = take(sizeof(int2) * g1);
   char* d = take(sizeof(int4) * g1);
   char* e = take(sizeof(int) * g1);
   char* l = take(sizeof(int) * (size_t)T);
   char* nl = take(sizeof(int) * 2);
+  char* kh = take(sizeof(int) * (size_t)((T + 1023) / 1024) * (kMaxK + 1));
+  char* tp = take(sizeof(int) * (size_t)T);
   if (ws) {
-    ws->reg_cnt = reinterpret_cast<int*>(a);
-    ws->far_cnt = reinterpret_cast<int*>(a2);
+    ws->mat = reinterpret_cast<int*>(m);
+    ws->tot = reinterpret_cast<int*>(t);
+    ws->within = reinterpret_cast<int*>(w);
+    ws->chunk_tot = reinterpret_cast<int*>(ct);
     ws->cell_start = reinterpret_cast<int*>(b);
     ws->far_start = reinterpret_cast<int*>(b2);
-    ws->far_blk = reinterpret_cast<int*>(f);
-    ws->NB = NB;
-    ws->nblk = nblk;
     ws->cell_slot = reinterpret_cast<int2*>(c);
     ws->recs = reinterpret_cast<int4*>(d);
     ws->far_g = reinterpret_cast<int*>(e);
     ws->lists = reinterpret_cast<int*>(l);
     ws->nlist = reinterpret_cast<int*>(nl);
+    ws->key_hist = reinterpret_cast<int*>(kh);
+    ws->tile_pos = reinterpret_cast<int*>(tp);
+    ws->NB = NB;
+    ws->Tpad = Tpad;
+    ws->cblock = cblock;
+    ws->nblk = nblk;
   }
   return off;
 }
@@ -1145,55 +1134,51 @@ static int bin_check(const float* mu2d, int mu_stride, const uint8_t* keep, int 
   if (G > (1 << 28)) return TTS_EG;  // (j << gbits) | g must fit in 32 bits
   if (S != 16 && S != 32) return TTS_ETILE;
   if (H % S || W % S) return TTS_ETILE;
+  if (pad_cells((H / S) * (W / S)) > kMaxLdsInts) return TTS_ETILE;  // the count pass's histogram
   if (R != 1) return TTS_ERADIUS;
   if (K < 1 || K > kMaxK) return TTS_EK;
   if (span < 1 || span > kMaxSpan) return TTS_ESPAN;
   return TTS_OK;
 }
 
-__global__ void k_zero_i32(int* __restrict__ p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
-// The binning passes on a laid-out workspace (arguments already checked).  clear_counters: the
-// per-cell counters (reg_cnt, far_cnt) are zeroed by a fill kernel first instead of being
-// trusted to be zero from the previous call.
+// The binning passes on a laid-out workspace (arguments already checked).  Every buffer the
+// passes read is written earlier in the same call: nothing has to be zero on entry.
 static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                    int G, int H, int W, int S, int K, int span, int32_t* idx, uint8_t* valid,
                    int32_t* count, int32_t* ncand, int32_t* inv, int32_t* order,
-                   const BinWorkspace& ws, bool clear_counters, hipStream_t stream) {
+                   const BinWorkspace& ws, hipStream_t stream) {
   const int ntx = W / S, nty = H / S, T = ntx * nty;
-  if (clear_counters) {
-    // reg_cnt and far_cnt are the first two sub-buffers: one fill covers both
-    const int n = static_cast<int>((reinterpret_cast<char*>(ws.far_cnt) -
-                                    reinterpret_cast<char*>(ws.reg_cnt)) / sizeof(int)) + T;
-    k_zero_i32<<<grid1d(n, 256), 256, 0, stream>>>(ws.reg_cnt, n);
-  }
   const float Sf = static_cast<float>(S);
-  const int NB = ws.NB;
-  const int nblk = ws.nblk;
+  const int NB = ws.NB, Tpad = ws.Tpad, nblk = ws.nblk;
+  const int X = Tpad + NB;
   if (G > 0) {
-    const bool reg_lds = T + 4 * NB <= kMaxLdsCells;
-    const size_t lds = sizeof(int) * (size_t)(4 * NB + (reg_lds ? T : 0));
-    if (reg_lds)
-      k_bin_count<true><<<nblk, 256, lds, stream>>>(mu2d, mu_stride, keep, keep_stride, G, ntx,
-                                                    nty, Sf, span, NB, ws.reg_cnt, ws.far_blk,
-                                                    nblk, ws.cell_slot);
+    const bool small = ws.cblock == CountSmall::kBlock;
+    const size_t lds =
+        sizeof(int) * (size_t)(Tpad + (small ? CountSmall::kWaves : CountLarge::kWaves) * NB);
+    const void* fn = small ? reinterpret_cast<const void*>(&k_bin_count<256, 2>)
+                           : reinterpret_cast<const void*>(&k_bin_count<1024, 4>);
+    if (lds > 65536) {
+      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               static_cast<int>(lds));
+      if (e != hipSuccess) return static_cast<int>(e);
+    }
+    if (small)
+      k_bin_count<256, 2><<<nblk, 256, lds, stream>>>(mu2d, mu_stride, keep, keep_stride, G, ntx,
+                                                      nty, Sf, span, NB, Tpad, ws.mat,
+                                                      ws.cell_slot);
     else
-      k_bin_count<false><<<nblk, 256, lds, stream>>>(mu2d, mu_stride, keep, keep_stride, G, ntx,
-                                                     nty, Sf, span, NB, ws.reg_cnt, ws.far_blk,
-                                                     nblk, ws.cell_slot);
-    if (NB > 0) k_far_colscan<<<NB, 256, 0, stream>>>(ws.far_blk, nblk, ntx, nty, ws.far_cnt);
+      k_bin_count<1024, 4><<<nblk, 1024, lds, stream>>>(mu2d, mu_stride, keep, keep_stride, G,
+                                                        ntx, nty, Sf, span, NB, Tpad, ws.mat,
+                                                        ws.cell_slot);
   }
-  const int fuse = T <= kScanChunk;
-  k_bin_scan<<<1, 1024, 0, stream>>>(ws.reg_cnt, ws.far_cnt, ws.cell_start, ws.far_start, ntx,
-                                     nty, K, fuse, ws.lists, ws.nlist, order);
-  if (G > 0) {
-    k_bin_scatter<<<grid1d(G, 256), 256, 0, stream>>>(mu2d, mu_stride, G, ntx, nty, ws.cell_slot,
-                                                      ws.cell_start, ws.far_start, ws.far_blk,
-                                                      nblk, ws.recs, ws.far_g, inv);
-  }
+  k_bin_colscan<<<(X + kChunk - 1) / kChunk, 1024, 0, stream>>>(ws.mat, nblk, X, ws.tot,
+                                                                ws.within, ws.chunk_tot,
+                                                                ws.nlist, 2);
+  const int ncls = (T + 1023) / 1024;
+  ScatterArgs sc{mu2d, mu_stride, G, ntx, nty, NB, Tpad, K, ws.cblock, ncls, ws.cell_slot,
+                 ws.mat, ws.tot, ws.within, ws.chunk_tot, ws.cell_start, ws.far_start, ws.recs,
+                 ws.far_g, inv, ws.lists, ws.nlist, ws.key_hist, ws.tile_pos};
+  k_bin_scatter<<<ncls + (max(G, T + 1) + 1023) / 1024, 1024, 0, stream>>>(sc);
   int kpow2 = 1;
   while (kpow2 < K) kpow2 <<= 1;
   int gbits = 1;
@@ -1203,14 +1188,9 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
                            sizeof(unsigned) * (size_t)hist_bins;
   const size_t light_lds = sizeof(unsigned long long) * (size_t)kpow2 * (kSelThreads / 64);
   const size_t lds = heavy_lds > light_lds ? heavy_lds : light_lds;
-  if (!fuse)
-    k_tile_classify<<<grid1d(T, 256), 256, 0, stream>>>(ws.cell_start, ws.far_start, ntx, nty, K,
-                                                        ws.lists, ws.nlist);
   SelectArgs sa{ws.recs, ws.far_g, ws.cell_start, ws.far_start, ntx, nty, Sf, span, K, kpow2,
-                gbits, idx, valid, count, ncand, inv};
+                gbits, idx, valid, count, ncand, inv, order, ws.key_hist, ws.tile_pos, ncls};
   k_bin_select<kSelThreads><<<T, kSelThreads, lds, stream>>>(sa, ws.lists, ws.nlist);
-  // large grids: the order pass runs on the kept counts (the fused scan wrote it otherwise)
-  if (order && !fuse) k_tile_order<<<1, 1024, 0, stream>>>(count, T, K, order);
   return launch_status();
 }
 
@@ -1254,13 +1234,12 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
   const int rc = bin_check(mu2d, mu_stride, keep, keep_stride, G, H, W, S, R, K, span, idx, valid);
   if (rc != TTS_OK) return rc;
   const int ntx = W / S, nty = H / S;
-  if (order && ntx * nty > kScanChunk && !count) return TTS_EINVAL;
   if (!workspace || workspace_bytes < bin_ws_layout(G, ntx, nty, nullptr, nullptr))
     return TTS_EWORKSPACE;
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
   return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
-                 ncand, inv, order, ws, false, stream);
+                 ncand, inv, order, ws, stream);
 }
 
 int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* keep,
@@ -1270,7 +1249,6 @@ int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* kee
   const int rc = bin_check(mu2d, mu_stride, keep, keep_stride, G, H, W, S, R, K, span, idx, valid);
   if (rc != TTS_OK) return rc;
   const int ntx = W / S, nty = H / S;
-  if (order && ntx * nty > kScanChunk && !count) return TTS_EINVAL;
   if (bin_ws_layout(G, ntx, nty, nullptr, nullptr) > kScratchBytes) return TTS_ESCRATCH;
   void* base = nullptr;
   const int sc = scratch_base(&base);
@@ -1278,7 +1256,7 @@ int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* kee
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(base), &ws);
   return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
-                 ncand, inv, order, ws, true, stream);
+                 ncand, inv, order, ws, stream);
 }
 
 int tts_tile_order(const int32_t* count, int T, int K, int32_t* order, hipStream_t stream) {
