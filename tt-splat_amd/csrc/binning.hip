@@ -215,12 +215,10 @@ __global__ __launch_bounds__(NT) void k_bin_count(
   extern __shared__ int s_lds[];
   int* s_reg = s_lds;            // [Tpad] regular count per cell
   int* s_wrun = s_lds + Tpad;    // [waves][NB] far count per wave (running, then total)
-  const int nl = Tpad + C::kWaves * NB;
-  for (int c = threadIdx.x; c < nl; c += NT) s_lds[c] = 0;
-  __syncthreads();
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int g0 = blockIdx.x * C::kBlock + wave * C::kWaveSpan + lane;
   // loads from clamped indices, unconditionally, so that all of them are in flight at once
+  // (and while the histogram is zeroed)
   float mx[kCountPerLane], my[kCountPerLane];
   uint8_t kv[kCountPerLane];
 #pragma unroll
@@ -230,6 +228,9 @@ __global__ __launch_bounds__(NT) void k_bin_count(
     mx[i] = mu2d[(int64_t)gc * mu_stride];
     my[i] = mu2d[(int64_t)gc * mu_stride + 1];
   }
+  const int nl = Tpad + C::kWaves * NB;
+  for (int c = threadIdx.x; c < nl; c += NT) s_lds[c] = 0;
+  __syncthreads();
   int cell[kCountPerLane], rank[kCountPerLane];
   bool farv[kCountPerLane];
 #pragma unroll
@@ -460,6 +461,17 @@ __global__ __launch_bounds__(1024) void k_bin_scatter(ScatterArgs a) {
   }
   const int ntx = a.ntx, nty = a.nty, T = ntx * nty, NB = a.NB;
   const int tid = threadIdx.x;
+  const int i0 = (blockIdx.x - a.ncls) * 1024 + tid;
+  // this thread's gaussian, loaded before the prologue's scans
+  const int g = i0;
+  const int gl = min(g, max(a.G - 1, 0));
+  int2 cs = make_int2(-1, 0);
+  float mx = 0.f, my = 0.f;
+  if (a.G > 0) {
+    cs = a.cell_slot[gl];
+    mx = a.mu2d[(int64_t)gl * a.mu_stride];
+    my = a.mu2d[(int64_t)gl * a.mu_stride + 1];
+  }
   const int nch = a.Tpad / kChunk;
   int regtot;
   const int cex = block_excl_scan<1024>(tid < nch ? a.chunk_tot[tid] : 0, s_tmp, &regtot);
@@ -470,7 +482,6 @@ __global__ __launch_bounds__(1024) void k_bin_scatter(ScatterArgs a) {
   const int fex = block_excl_scan<1024>(tid < NB ? s_fp[tid] : 0, s_tmp, &ftot);
   if (tid < NB) s_fp[tid] = fex;
   __syncthreads();
-  const int i0 = (blockIdx.x - a.ncls) * 1024 + tid;
   if (i0 <= T) {
     const int c = i0;
     int fs = ftot;
@@ -486,13 +497,11 @@ __global__ __launch_bounds__(1024) void k_bin_scatter(ScatterArgs a) {
     a.cell_start[c] = c < T ? s_cpre[c / kChunk] + a.within[c] : regtot;
     a.far_start[c] = fs;
   }
-  const int g = i0;
   if (g >= a.G) return;
   if (a.inv) {  // no slot yet: k_bin_select fills the kept (g, j) entries
 #pragma unroll
     for (int j = 0; j < 9; ++j) a.inv[(int64_t)g * 9 + j] = -1;
   }
-  const int2 cs = a.cell_slot[g];
   if (cs.x < 0) return;
   const int X = a.Tpad + NB;
   const int* row = a.mat + (int64_t)(g / a.cblock) * X;
@@ -501,7 +510,6 @@ __global__ __launch_bounds__(1024) void k_bin_scatter(ScatterArgs a) {
     const int b = border_index(c % ntx, c / ntx, ntx, nty);
     a.far_g[s_fp[border_rank(b, ntx, nty)] + row[a.Tpad + b] + cs.y] = g;
   } else {
-    const float mx = a.mu2d[(int64_t)g * a.mu_stride], my = a.mu2d[(int64_t)g * a.mu_stride + 1];
     const int c = cs.x;
     a.recs[s_cpre[c / kChunk] + a.within[c] + row[c] + cs.y] =
         make_int4(g, __float_as_int(mx), __float_as_int(my), 0);
