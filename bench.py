@@ -17,16 +17,18 @@ samples of the same workload.
 
 Clock state: before any timed region the GPU replays the forward graphs for ~1.5 s (no state
 change), so every timed region runs at steady clocks; a cold GPU measures several percent slower
-for the first second.  Per-kernel times are HIP events on the launch stream, camera 0 (and each
-of the 8 cameras for the splat kernels, with their pair counts, so the roofline fraction can be
-recomputed from a profile of the same run).
+for the first second.  Per-kernel times are HIP events on the launch stream around replays of a
+graph of 20 back-to-back launches, camera 0 (and each of the 8 cameras for the splat kernels,
+with their pair counts, so the roofline fraction can be recomputed from a profile of the same
+run, whose kernel durations these agree with: no host time between the launches).
 
 Roofline convention: the splat kernels are priced in the reference's algorithmic flops per
 (pixel, valid slot) pair -- 22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80,
 Phi.theta 12 + relu^2 2 + WSR 8, and the transposed contractions) -- against MI355X's 157.3
-TFLOP/s FP32 peak.  That peak is reachable without packed FP32 instructions on gfx950 (wave64
-FP32 FMAs issue at two cycles each when enough waves are ready), so frac is the fraction of
-the attainable VALU rate.
+TFLOP/s FP32 peak (the same for vector and matrix FP32; `bound` reads "mfma", the arithmetic
+roof, as opposed to "hbm").  That peak is reachable without packed FP32 instructions on gfx950
+(wave64 FP32 FMAs issue at two cycles each when enough waves are ready), so frac is the
+fraction of the attainable VALU rate.
 """
 import argparse
 import json
@@ -161,11 +163,38 @@ def warm_clocks(ts, torch, seconds=1.5):
     return i
 
 
+def graph_time(fn, reps, torch, per_graph=20):
+    """Microseconds per launch of fn(): per_graph launches captured back to back in one HIP graph
+    (no host work between them), the graph replayed until about reps launches have run, between
+    two HIP events on the stream the launches run on.  Timing eager launches instead would add
+    the host's per-call time to every kernel shorter than it."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    n = max(1, reps // per_graph)
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(n):
+        g.replay()
+    e1.record(stream)
+    e1.synchronize()
+    us = e0.elapsed_time(e1) / (n * per_graph) * 1e3
+    del g
+    return us
+
+
 def time_splat_per_camera(ts, reps, torch, kernels):
     """Fused splat forward / backward of every camera: HIP-event microseconds per launch and the
     (pixel, valid slot) pairs of that camera's bins (the state is the current one; the
     backward's input image gradient is a fixed random field)."""
-    stream = torch.cuda.current_stream()
     gim = torch.randn(ts.H, ts.W, 3, generator=torch.Generator().manual_seed(11)).cuda()
     rows = []
     for ci in range(len(ts.cams)):
@@ -180,16 +209,7 @@ def time_splat_per_camera(ts, reps, torch, kernels):
                                                        ts.W, ts.S, ts.k, ts.image, ts.den, gim,
                                                        ts.gslot, order=ts.order)}
         for name, fn in jobs.items():
-            for _ in range(3):
-                fn()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                fn()
-            e1.record(stream)
-            e1.synchronize()
-            rec[name + "_us"] = e0.elapsed_time(e1) / reps * 1e3
+            rec[name + "_us"] = graph_time(fn, reps, torch)
         rows.append(rec)
     ts.forward(0)
     torch.cuda.synchronize()
@@ -198,10 +218,9 @@ def time_splat_per_camera(ts, reps, torch, kernels):
 
 def time_kernels(ts, reps, torch, kernels):
     """Average duration of each kernel group at the current state (camera 0), from HIP events
-    recorded on the stream the kernels are launched on."""
+    around graph replays of its launches (graph_time)."""
     ts.enqueue(0)                       # bring every buffer to a consistent step state
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
     P_save, m_save, v_save, s_save = (t.clone() for t in (ts.P, ts.m, ts.v, ts.step_block))
     cam = ts.cams[0]
     sh = dict(sh_rest=ts.sh, sh_degree=ts.sh_degree)
@@ -234,17 +253,7 @@ def time_kernels(ts, reps, torch, kernels):
                                                                 gacc_sh=ts.gacc_sh, **sh)
     out = {}
     for name, fn in jobs.items():
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            fn()
-        e1.record(stream)
-        e1.synchronize()
-        out[name] = e0.elapsed_time(e1) / reps * 1e3      # microseconds per launch
+        out[name] = graph_time(fn, reps, torch)          # microseconds per launch
     # restore the state the measurement perturbed
     for dst, src in zip((ts.P, ts.m, ts.v, ts.step_block, *shs),
                         (P_save, m_save, v_save, s_save, *saved_sh)):
@@ -580,16 +589,19 @@ def main():
     dom = max(("splat_fwd", "splat_bwd"), key=lambda n: kt[n])
     all_pairs = sum(r["pairs"] for r in per_cam)
     all_us = sum(r[dom + "_us"] for r in per_cam)
-    roofline = dict(bound="valu", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
+    roofline = dict(bound="mfma", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
                     unit="TFLOP/s", frac=rows[dom]["frac"], traffic=load_traffic(dom, cfg.name),
                     flops_per_pair=FLOP_PER_PAIR[dom], flops_per_launch=FLOP_PER_PAIR[dom] * pairs,
                     pairs_per_launch=pairs, us_per_launch=kt[dom], camera=0,
                     frac_all_cameras=FLOP_PER_PAIR[dom] * all_pairs / (all_us * 1e-6) / 1e12
                     / PEAK_FP32_TFLOPS,
-                    convention="algorithmic flops of the reference's GEMM form per (pixel, "
+                    convention="compute-bound (bound 'mfma' = the arithmetic roofline, not HBM): "
+                               "algorithmic flops of the reference's GEMM form per (pixel, "
                                "valid slot) pair (22 fwd / 44 bwd) x pairs of the launch / its "
-                               "HIP-event duration, camera 0; peak = MI355X FP32 157.3 TFLOP/s, "
-                               "attainable without packed FP32 instructions")
+                               "HIP-event duration over graph replays of 20 launches, camera 0; peak = MI355X FP32 157.3 TFLOP/s, "
+                               "the same for FP32 vector and matrix issue; the kernel issues "
+                               "its FP32 on the VALU, which reaches that rate without packed "
+                               "FP32 instructions")
     small = {} if args.no_small else small_configs(torch, scenes, TrainStep)
     extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)

@@ -44,7 +44,7 @@ extern "C" {
 
 #define TTS_OK 0
 #define TTS_EINVAL (-1)     /* null pointer, non-positive size, or a size over an entry's limit */
-#define TTS_ETILE (-2)      /* S not in {16,32}, or H/W not a multiple of S */
+#define TTS_ETILE (-2)      /* S not in {16,32}, H/W not a multiple of S, or over 38912 tiles */
 #define TTS_EK (-3)         /* K outside [1, 512] */
 #define TTS_EWORKSPACE (-4) /* workspace missing or too small */
 #define TTS_ESPAN (-5)      /* quantised-distance span outside [1, 8192] */
@@ -78,8 +78,8 @@ int tts_geom_bwd(const float* params, int G, const float* camera, float near_z, 
 
 /* ------------------------------------------------------------------ binning --------- */
 
-/* Bytes of zero-initialised scratch tts_assign_bins needs for G gaussians on an H x W image
- * with S x S tiles.  The caller zeroes it once; every successful call leaves it zeroed. */
+/* Bytes of scratch tts_assign_bins needs for G gaussians on an H x W image with S x S tiles.
+ * It needs no initialisation: every pass writes what the next one reads. */
 size_t tts_bin_workspace_bytes(int G, int H, int W, int S);
 
 /* Fixed-budget spatial-hash binning, R = 1: each gaussian is hashed to one S x S cell, offered
@@ -90,25 +90,24 @@ size_t tts_bin_workspace_bytes(int G, int H, int W, int S);
  * index j, gaussian id), i.e. the reference's sort key with ties in its concatenation order;
  * span = 2048 at S = 16.  Writes idx[T,K], valid[T,K]; count[T] (kept per tile), ncand[T]
  * (candidates per tile), inv[G,9] and order[T] are optional (may be NULL).  order receives the
- * tile ids sorted by kept count, heaviest first (what tts_tile_order computes; for grids of up
- * to 8192 tiles it comes out of the offset scan at no extra pass, beyond that count[T] is
- * required). */
+ * tile ids sorted by kept count, heaviest first (what tts_tile_order computes, here without a
+ * pass of its own).  Grids of up to 38912 tiles (T rounded up to 64; TTS_ETILE beyond). */
 int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                     int G, int H, int W, int S, int R, int K, int span,
                     int32_t* idx, uint8_t* valid, int32_t* count, int32_t* ncand, int32_t* inv,
                     int32_t* order, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* Size of the fixed device scratch behind tts_assign_bins_noalloc (40 MiB per GPU: enough for
- * G = 2^20 gaussians on images up to 4096 x 4096 at S = 16). */
+ * G = 2^20 gaussians on 1920 x 1072 at S = 16, which needs 36.4 MiB). */
 #define TTS_BIN_SCRATCH_BYTES ((size_t)40 << 20)
 
 /* tts_assign_bins without a caller workspace and without any allocation: the binning scratch
  * lives in a file-scope device array of TTS_BIN_SCRATCH_BYTES in the library (each GPU the
  * library runs on holds its own copy until the process ends; its address is looked up on the
  * first call on a device).  Same arguments, checks and results as tts_assign_bins; returns
- * TTS_ESCRATCH when tts_bin_workspace_bytes(G, H, W, S) exceeds TTS_BIN_SCRATCH_BYTES.  The
- * per-cell counters are cleared by a fill kernel at the start of every call, so a call does
- * not depend on what an earlier one left.  Every call on one GPU shares that GPU's scratch:
+ * TTS_ESCRATCH when tts_bin_workspace_bytes(G, H, W, S) exceeds TTS_BIN_SCRATCH_BYTES.
+ * Nothing in the scratch has to start at zero, so a call does not depend on what an earlier
+ * one left.  Every call on one GPU shares that GPU's scratch:
  * calls that overlap on one GPU (different streams or threads without ordering) race.
  * No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */

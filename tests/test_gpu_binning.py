@@ -204,9 +204,9 @@ def _check_order(order, count):
 
 @pytest.mark.parametrize("H,W,G", [(832, 1264, 100_000), (2064, 1024, 50_000)])
 def test_bins_tile_order_output(H, W, G):
-    """order[T] from assign_bins: a permutation sorted by kept count, heaviest first, produced
-    by the offset scan when the grid has at most 8192 tiles and by the order pass above that
-    (2064 x 1024 = 8256 tiles, which also takes the separate classification path)."""
+    """order[T] from assign_bins: a permutation sorted by kept count, heaviest first, written by
+    the select pass from the per-block key counts of the tile classification; 2064 x 1024 =
+    8256 tiles takes nine classification blocks and an order-key table of 16 columns."""
     cfg = scenes.CONFIGS["c4"]
     P = cfg.params(0)[:G] if G <= cfg.G else cfg.params(0)
     cam = pinhole(H, W, scenes.orbit_eyes(1)[0])
@@ -219,7 +219,7 @@ def test_bins_tile_order_output(H, W, G):
     assert torch.equal(count.cpu().long(), torch.clamp(ncand.cpu().long(), max=128))
     ref = kernels.tile_order(count, 128)
     assert torch.equal(count.cpu()[ref.cpu().long()], count.cpu()[order.cpu().long()])
-    if T > 8192:     # the non-fused path's bins stay bit-exact
+    if T > 8192:     # the larger grid's bins stay bit-exact
         tmap = obin.TileMap(H, W, 16)
         ridx, rvalid = obin.assign_bins(proj[:, 0:2].cpu(), keep.cpu().bool(), tmap, 1, 128,
                                         2048, stable=True)

@@ -931,7 +931,7 @@ const char* tts_strerror(int code) {
   switch (code) {
     case TTS_OK: return "ok";
     case TTS_EINVAL: return "invalid argument (null pointer, non-positive size or size over the limit)";
-    case TTS_ETILE: return "tile side must be 16 or 32 and divide H and W";
+    case TTS_ETILE: return "tile side must be 16 or 32 and divide H and W (binning: at most 38912 tiles)";
     case TTS_EK: return "K must be in [1, 512]";
     case TTS_EWORKSPACE: return "workspace missing or too small";
     case TTS_ESPAN: return "span must be in [1, 8192]";
