@@ -68,6 +68,35 @@ def test_splat_fwd_ragged_budgets(K):
     assert max_abs(den, ex["den"]) <= 1e-4 * float(ex["den"].abs().max())
 
 
+@pytest.mark.parametrize("K", [128, 300])
+def test_splat_fwd_holes_in_valid(K):
+    """Valid masks that are not a prefix of each tile's slots (user bins): the forward stages
+    slot s at LDS entry s and walks to the highest valid slot, so the holes must add nothing.
+    K = 300 also takes the slots past the first 256 (a second staging pass)."""
+    cfg, P, cam = config_inputs("c3")
+    proj, keep = kernels.geom_fwd(P.cuda(), cam.device_block("cuda"))
+    idx, valid, count, _ = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, K,
+                                               cfg.span)
+    gen = torch.Generator().manual_seed(5)
+    holes = (torch.rand(valid.shape, generator=gen) < 0.35).to(valid.device)
+    valid2 = valid & ~holes.bool()
+    T = valid.shape[0]
+    g = int(idx[valid.bool()][0])       # a binned (kept) gaussian
+    valid2[T // 2, :] = False           # one tile whose only valid slot is the last one
+    valid2[T // 2, K - 1] = True
+    idx[T // 2, K - 1] = g
+    bg = torch.tensor([float(torch.nn.functional.softplus(torch.tensor(-3.0))), 1.0, 1.0, 1.0],
+                      device="cuda")
+    img, den = kernels.splat_fwd(proj, idx, valid2, bg, cfg.H, cfg.W, cfg.S, cfg.k)
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ref, ex = osplat.render_binned(P, cam_dict(cam), tmap, K=K, k=cfg.k,
+                                   bins=(idx.cpu().long(), valid2.cpu().bool()), return_all=True)
+    err = max_abs(img, ref)
+    print(f"[fwd holes] K={K} max|err|={err:.3e}", flush=True)
+    assert err <= 1e-4
+    assert max_abs(den, ex["den"]) <= 1e-4 * float(ex["den"].abs().max())
+
+
 def test_theta_gather_matches_operands():
     cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup("c1_ref")
     th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, k)

@@ -598,7 +598,9 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
 // Each A entry is (p ly + q) ly + r with (p, q, r) per (slot, depth k) staged in LDS:
 // k = 0: (0, 0, theta0), k = 1: (0, theta2, theta3), k = 2: (theta1, theta4, theta5), k = 3: 0.
 // The VALU keeps relu^2 and the colour / density sums (6 instructions per pair, 2 more per
-// 256 pairs for A); padding slots of the last group are zero (u = 0, w = 0).
+// 256 pairs for A).  Slot s is staged at LDS entry s (zero when invalid: u = 0, w = 0) and the
+// walk runs to the highest valid slot, so bins whose valid slots form a prefix (tts_assign_bins)
+// are summed in slot order with no zero terms beyond the last group.
 inline size_t fwd_mf_lds(int K) {
   const int k4 = (K + 3) & ~3;
   return (size_t)k4 * 5 * sizeof(float4);
@@ -609,7 +611,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     float inv_k, const float* __restrict__ bg, float* __restrict__ image,
     float* __restrict__ den_out) {
   extern __shared__ unsigned char s_dyn[];
-  __shared__ int s_tmp[4];
+  __shared__ int s_hi[2][4];
   const int k4 = (K + 3) & ~3;
   float4* s_coef = reinterpret_cast<float4*>(s_dyn);  // [k4][4]: (p, q, r, 0) per depth k
   float4* s_col = s_coef + (size_t)k4 * 4;           // [k4]: col_o r, g, b, o_col
@@ -617,48 +619,63 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * 16, oy = ty * 16;
   const float oxf = (float)ox, oyf = (float)oy;
-  // compact the valid slots in slot order (idx beside valid; a valid slot's proj record in flight
-  // across the scan), build theta and stage the per-depth coefficients and the colours
-  int n = 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   bool bad = false;
-  for (int s0 = 0; s0 < K; s0 += 256) {
-    const int s = s0 + threadIdx.x;
-    const int64_t ts = (int64_t)t * K + min(s, K - 1);
-    const uint8_t vb = valid[ts];
-    const int g = idx[ts];
-    const int v = (s < K && vb != 0) ? 1 : 0;
-    float4 r0, r1, r2;
-    if (v) {
-      const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
-      r0 = r[0];
-      r1 = r[1];
-      r2 = r[2];
-    }
-    int total;
-    const int pos = n + block_excl_scan256(v, s_tmp, &total);
+  // slot s's coefficients go to LDS entry s (zero for an invalid slot)
+  auto stage = [&](int s, int v, const float4& r0, const float4& r1, const float4& r2) {
+    if (s >= k4) return;
+    float4* c = s_coef + (size_t)s * 4;
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
       bad = bad || theta_poisons(ta, tb);
-      float4* c = s_coef + (size_t)pos * 4;
       c[0] = make_float4(0.f, 0.f, ta.x, 0.f);
       c[1] = make_float4(0.f, ta.z, ta.w, 0.f);
       c[2] = make_float4(ta.y, tb.x, tb.y, 0.f);
       c[3] = make_float4(0.f, 0.f, 0.f, 0.f);
-      s_col[pos] = cl;
+      s_col[s] = cl;
+    } else {
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      c[0] = z;
+      c[1] = z;
+      c[2] = z;
+      c[3] = z;
+      s_col[s] = z;
     }
-    n += total;
+  };
+  auto gather = [&](int g, float4& r0, float4& r1, float4& r2) {
+    const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+    r0 = r[0];
+    r1 = r[1];
+    r2 = r[2];
+  };
+  // the first 256 slots, one per thread: valid and idx together; the highest valid slot of
+  // each wave's 64 (slot order = LDS order, so the walk needs no compaction)
+  const int s = threadIdx.x;
+  int v, g;
+  {
+    const int64_t ts = (int64_t)t * K + min(s, K - 1);
+    const uint8_t vb = valid[ts];
+    g = idx[ts];
+    v = (s < K && vb != 0) ? 1 : 0;
   }
-  const int ngrp = (n + 3) >> 2;
-  for (int p = n + (int)threadIdx.x; p < ngrp * 4; p += 256) {  // at most 3 padding slots
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) s_coef[(size_t)p * 4 + k] = z;
-    s_col[p] = z;
+  {
+    const uint64_t m = __ballot(v);
+    if (lane == 0) s_hi[0][wave] = m ? wave * 64 + 64 - __clzll((long long)m) : 0;
   }
-  const bool poisoned = __syncthreads_or(bad);
+  // slots 0..63 (wave 0) are staged and walked first; the records of the other slots are
+  // requested only then, so the first walk's gathers are not queued behind theirs and the rest
+  // arrive during that walk
+  float4 r0, r1, r2;
+  if (wave == 0) {
+    if (v) gather(g, r0, r1, r2);
+    stage(s, v, r0, r1, r2);
+  }
+  bool poisoned = __syncthreads_or(bad);
+  const int n0 = max(max(s_hi[0][0], s_hi[0][1]), max(s_hi[0][2], s_hi[0][3]));
+  const bool more = n0 > 64 || k4 > 256;
+  if (more && wave > 0 && v) gather(g, r0, r1, r2);
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane & 15, q = lane >> 4;
   // A side of this lane: row (lane >> 2) & 3 of the wave, slot lane & 3 of a group, depth q
   const float ly_a = (float)(4 * wave + ((lane >> 2) & 3)) + 0.5f;
@@ -668,27 +685,50 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   const float bq = q == 0 ? lx * lx : (q == 1 ? lx : (q == 2 ? 1.0f : 0.0f));
   float ar = 0.f, ag = 0.f, ab = 0.f, ad = 0.f;
   const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+  auto walk = [&](int g0, int g1) {
 #pragma unroll 4
-  for (int gi = 0; gi < ngrp; ++gi) {
-    const float4 pc = s_coef[(size_t)gi * 16 + a_off];
-    const float a = fmaf(fmaf(pc.x, ly_a, pc.y), ly_a, pc.z);
-    const floatx4 u = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq, zero4, 0, 0, 0);
-    // elements copied out before their bits are reinterpreted (a bit cast applied to the
-    // vector-element expression itself compiled to element 0 for every e)
-    const float ue[4] = {u[0], u[1], u[2], u[3]};
+    for (int gi = g0; gi < g1; ++gi) {
+      const float4 pc = s_coef[(size_t)gi * 16 + a_off];
+      const float a = fmaf(fmaf(pc.x, ly_a, pc.y), ly_a, pc.z);
+      const floatx4 u = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq, zero4, 0, 0, 0);
+      // elements copied out before their bits are reinterpreted (a bit cast applied to the
+      // vector-element expression itself compiled to element 0 for every e)
+      const float ue[4] = {u[0], u[1], u[2], u[3]};
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float4 cl = s_col[gi * 4 + e];
-      // relu as one integer max on the bit pattern (a float max would first canonicalise the
-      // matrix-core result): u >= +0 keeps its bits, negative u becomes +0; a NaN u (a
-      // poisoned tile, whatever its sign bit) is overwritten by the NaN store below
-      const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
-      const float w = rl * rl;
-      ar += w * cl.x;
-      ag += w * cl.y;
-      ab += w * cl.z;
-      ad += w * cl.w;
+      for (int e = 0; e < 4; ++e) {
+        const float4 cl = s_col[gi * 4 + e];
+        // relu as one integer max on the bit pattern (a float max would first canonicalise the
+        // matrix-core result): u >= +0 keeps its bits, negative u becomes +0; a NaN u (a
+        // poisoned tile, whatever its sign bit) is overwritten by the NaN store below
+        const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
+        const float w = rl * rl;
+        ar += w * cl.x;
+        ag += w * cl.y;
+        ab += w * cl.z;
+        ad += w * cl.w;
+      }
     }
+  };
+  walk(0, (min(n0, 64) + 3) >> 2);
+  if (more) {
+    if (wave > 0) stage(s, v, r0, r1, r2);
+    int hi = 0;
+    for (int s0 = 256; s0 < k4; s0 += 256) {
+      const int s2 = s0 + threadIdx.x;
+      const int64_t ts = (int64_t)t * K + min(s2, K - 1);
+      const uint8_t vb = valid[ts];
+      const int g2 = idx[ts];
+      const int v2 = (s2 < K && vb != 0) ? 1 : 0;
+      float4 q0, q1, q2;
+      if (v2) gather(g2, q0, q1, q2);
+      stage(s2, v2, q0, q1, q2);
+      const uint64_t m = __ballot(v2);
+      if (m) hi = s0 + wave * 64 + 64 - __clzll((long long)m);
+    }
+    if (lane == 0) s_hi[1][wave] = hi;
+    poisoned = __syncthreads_or(bad) || poisoned;
+    const int n = max(n0, max(max(s_hi[1][0], s_hi[1][1]), max(s_hi[1][2], s_hi[1][3])));
+    walk(16, (n + 3) >> 2);
   }
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
