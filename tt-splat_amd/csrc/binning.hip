@@ -548,9 +548,9 @@ __device__ __forceinline__ int4 load_candidate(const TileCells& tc, const int4* 
 // f(key) for every regular candidate of the tile, flattened over the nine cells so that all
 // loads of a light tile are issued in one round, four independent loads in flight per thread.
 template <int NT, typename F>
-__device__ __forceinline__ void for_each_candidate(const TileCells& tc,
-                                                   const int4* __restrict__ recs, int tx, int ty,
-                                                   float S, int span, int tid, F&& f) {
+__device__ __forceinline__ void for_each_candidate_at(const TileCells& tc,
+                                                      const int4* __restrict__ recs, int tx,
+                                                      int ty, float S, int span, int tid, F&& f) {
   const int n = tc.pre[9];
   int i = tid;
   for (; i + 3 * NT < n; i += 4 * NT) {
@@ -560,15 +560,23 @@ __device__ __forceinline__ void for_each_candidate(const TileCells& tc,
     const int4 r1 = load_candidate(tc, recs, i + NT, j1);
     const int4 r2 = load_candidate(tc, recs, i + 2 * NT, j2);
     const int4 r3 = load_candidate(tc, recs, i + 3 * NT, j3);
-    f(record_key(r0, j0, tx, ty, S, span));
-    f(record_key(r1, j1, tx, ty, S, span));
-    f(record_key(r2, j2, tx, ty, S, span));
-    f(record_key(r3, j3, tx, ty, S, span));
+    f(i, record_key(r0, j0, tx, ty, S, span));
+    f(i + NT, record_key(r1, j1, tx, ty, S, span));
+    f(i + 2 * NT, record_key(r2, j2, tx, ty, S, span));
+    f(i + 3 * NT, record_key(r3, j3, tx, ty, S, span));
   }
   for (; i < n; i += NT) {
     const int j = stencil_of(tc, i);
-    f(record_key(load_candidate(tc, recs, i, j), j, tx, ty, S, span));
+    f(i, record_key(load_candidate(tc, recs, i, j), j, tx, ty, S, span));
   }
+}
+// The same walk, f(key) only.
+template <int NT, typename F>
+__device__ __forceinline__ void for_each_candidate(const TileCells& tc,
+                                                   const int4* __restrict__ recs, int tx, int ty,
+                                                   float S, int span, int tid, F&& f) {
+  for_each_candidate_at<NT>(tc, recs, tx, ty, S, span, tid,
+                            [&](int, unsigned long long key) { f(key); });
 }
 
 // f(key) for the regular candidates of one cell (stencil index j) only.
@@ -736,19 +744,43 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int m = *fill;
+  // the keys padded to a multiple of 16 with the largest key (never below a survivor), so the
+  // rank counts read them 8 at a time with no tail
+  const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
+  if (lane < m16 - m) keys[m + lane] = ~0ull;
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
   const int64_t base = static_cast<int64_t>(t) * a.K;
-  for (int s = lane; s < a.K; s += 64) {
-    if (s < m) {
-      const unsigned long long key = keys[s];
-      int rank = 0;
-      for (int e = 0; e < m; ++e) rank += (keys[e] < key) ? 1 : 0;
-      const int g = static_cast<int32_t>(key & 0xffffffffull);
-      a.idx[base + rank] = g;
-      if (a.inv) a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-      a.valid[base + rank] = 1;
-    } else {
-      a.idx[base + s] = 0;
-      a.valid[base + s] = 0;
+  const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(keys);
+  for (int s0 = 0; s0 < a.K; s0 += 128) {
+    // slots s0 + lane and s0 + 64 + lane share each key read
+    const int sa = s0 + lane, sb = sa + 64;
+    const unsigned long long ka = sa < m ? keys[sa] : 0ull, kb = sb < m ? keys[sb] : 0ull;
+    int ra = 0, rb = 0;
+    if (s0 < m) {
+      for (int e = 0; e < m16 / 2; e += 4) {
+        const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
+        ra += (k0.x < ka) + (k0.y < ka) + (k1.x < ka) + (k1.y < ka) + (k2.x < ka) + (k2.y < ka) +
+              (k3.x < ka) + (k3.y < ka);
+        rb += (k0.x < kb) + (k0.y < kb) + (k1.x < kb) + (k1.y < kb) + (k2.x < kb) + (k2.y < kb) +
+              (k3.x < kb) + (k3.y < kb);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int s = h ? sb : sa;
+      const unsigned long long key = h ? kb : ka;
+      const int rank = h ? rb : ra;
+      if (s < m) {
+        const int g = static_cast<int32_t>(key & 0xffffffffull);
+        a.idx[base + rank] = g;
+        if (a.inv)
+          a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
+        a.valid[base + rank] = 1;
+      } else if (s < a.K) {
+        a.idx[base + s] = 0;
+        a.valid[base + s] = 0;
+      }
     }
   }
   if (a.order) {
@@ -837,12 +869,35 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
       s_keys[wave_append(&s_fill, true)] = make_key(satq, j, far_g[tc.fstart[j] + i - tc.fpre[j]]);
     }
   } else {
-    for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
+    // the regular candidates' keys stay in the tie buffer when they fit, so the collecting walk
+    // below reads them from LDS (its own tie entries are written only after every key is read)
+    const bool cached = nreg <= kTieCap;
+    for_each_candidate_at<NT>(tc, recs, tx, ty, S, span, threadIdx.x,
+                              [&](int i, unsigned long long key) {
       const unsigned q = static_cast<unsigned>(key >> kQShift);
       hist_add(s_hist, q);
       if (static_cast<int>(q) == satq)
         agg_inc(s_sat, static_cast<int>((key >> kJShift) & 15ull));
+      if (cached) s_tie[i] = key;
     });
+    // f(key) over the regular candidates: from the cached keys (a barrier between the reads and
+    // f, which may write the tie buffer) or by a walk over the records
+    auto collect = [&](auto&& f) {
+      if (cached) {
+        unsigned long long ck[kTieCap / NT];
+#pragma unroll
+        for (int k = 0; k < kTieCap / NT; ++k) {
+          const int i = static_cast<int>(threadIdx.x) + k * NT;
+          ck[k] = i < nreg ? s_tie[i] : 0ull;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kTieCap / NT; ++k)
+          if (static_cast<int>(threadIdx.x) + k * NT < nreg) f(ck[k]);
+      } else {
+        for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, f);
+      }
+    };
     __syncthreads();
     if (threadIdx.x == 0) s_hist[satq] += nfar;
     __syncthreads();
@@ -852,7 +907,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     if (qb < satq) {
       // ---------------- tie bin of regular candidates only ----------------
       const bool in_lds = cnt <= kTieCap;
-      for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
+      collect([&](unsigned long long key) {
         const int q = static_cast<int>(key >> kQShift);
         const int p = wave_append(&s_fill, q < qb);
         if (p >= 0) s_keys[p] = key;
@@ -918,7 +973,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
       const int fb = min(fn, rr + 1);
       const bool in_lds = satj + fb <= kTieCap;
       // regular keys below the bin, saturated ones with j < j*, and cell j*'s saturated ones
-      for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
+      collect([&](unsigned long long key) {
         const int q = static_cast<int>(key >> kQShift);
         const int j = static_cast<int>((key >> kJShift) & 15ull);
         const int p = wave_append(&s_fill, q < satq || j < js);
@@ -987,17 +1042,26 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
   }
   __syncthreads();
   // Place the m survivors by rank (unique keys: rank = number of smaller survivors).  Two
-  // adjacent lanes share a survivor, each counting over half of them.
+  // adjacent lanes share a survivor, each counting over half of them; the keys are padded to a
+  // multiple of 16 with the largest key (never below a survivor) and read 8 at a time.
   const int m = min(s_fill, K);
+  const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
+  if (static_cast<int>(threadIdx.x) < m16 - m) s_keys[m + threadIdx.x] = ~0ull;
+  __syncthreads();
   const int64_t base = static_cast<int64_t>(t) * K;
   const int half = threadIdx.x & 1;
-  const int e0 = half ? (m + 1) / 2 : 0, e1 = half ? m : (m + 1) / 2;
+  const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(s_keys + half * (m16 / 2));
   for (int s0 = 0; s0 < K; s0 += NT / 2) {
     const int s = s0 + (static_cast<int>(threadIdx.x) >> 1);
     const unsigned long long key = s < m ? s_keys[s] : 0ull;
     int rank = 0;
-    if (s < m)
-      for (int e = e0; e < e1; ++e) rank += (s_keys[e] < key) ? 1 : 0;
+    if (s0 < m) {
+      for (int e = 0; e < m16 / 4; e += 4) {
+        const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
+        rank += (k0.x < key) + (k0.y < key) + (k1.x < key) + (k1.y < key) + (k2.x < key) +
+                (k2.y < key) + (k3.x < key) + (k3.y < key);
+      }
+    }
     rank += __shfl_xor(rank, 1);
     if (half == 0 && s < K) {
       if (s < m) {
@@ -1187,7 +1251,7 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
                  ws.mat, ws.tot, ws.within, ws.chunk_tot, ws.cell_start, ws.far_start, ws.recs,
                  ws.far_g, inv, ws.lists, ws.nlist, ws.key_hist, ws.tile_pos};
   k_bin_scatter<<<ncls + (max(G, T + 1) + 1023) / 1024, 1024, 0, stream>>>(sc);
-  int kpow2 = 1;
+  int kpow2 = 16;  // at least 16: the survivors are padded to a multiple of 16
   while (kpow2 < K) kpow2 <<= 1;
   int gbits = 1;
   while ((1ll << gbits) < (long long)(G > 1 ? G : 2)) ++gbits;
