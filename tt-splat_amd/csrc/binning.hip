@@ -683,6 +683,20 @@ __device__ __forceinline__ void radix_select(V&& visit, int r, int bits, unsigne
   *stop_out = stop;
 }
 
+// Number of the n values get(0..n-1) below v, read 8 at a time (n small: a few tie keys).
+template <typename G>
+__device__ __forceinline__ int count_below(unsigned v, int n, G&& get) {
+  int c = 0;
+  for (int f = 0; f < n; f += 8) {
+    unsigned w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = f + i < n ? get(f + i) : ~0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c += w[i] < v ? 1 : 0;
+  }
+  return c;
+}
+
 constexpr int kSelThreads = 256;
 constexpr int kTieCap = 1024;   // tie-bin candidates kept in LDS for the sub-key select
 
@@ -719,6 +733,32 @@ __device__ __forceinline__ int order_slot(const SelectArgs& a, int t, int n) {
   }
   return read_lane(wave_incl_scan(s), 63) + a.tile_pos[t];
 }
+// The same slot in two halves: the key-major table's entries before (key, cb) form one
+// contiguous prefix [0, key * ncls + cb); begin() requests up to 64 * kOsPre of them (and the
+// tile's rank) into registers, end() waits for them, adds any further entries and reduces.
+constexpr int kOsPre = 8;
+struct OrderSlot {
+  int v[kOsPre];
+  int pos, len;
+  __device__ __forceinline__ void begin(const SelectArgs& a, int t, int n) {
+    const int key = a.K - min(n, a.K);
+    len = key * a.ncls + (t >> 10);
+    const int lane = lane_id();
+#pragma unroll
+    for (int i = 0; i < kOsPre; ++i) {
+      const int e = lane + 64 * i;
+      v[i] = e < len ? a.key_hist[e] : 0;
+    }
+    pos = a.tile_pos[t];
+  }
+  __device__ __forceinline__ int end(const SelectArgs& a) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < kOsPre; ++i) s += v[i];
+    for (int e = lane_id() + 64 * kOsPre; e < len; e += 64) s += a.key_hist[e];
+    return read_lane(wave_incl_scan(s), 63) + pos;
+  }
+};
 
 // Light tile (n <= K candidates: all survive), one wave: collect the keys in LDS, then place
 // them by rank.
@@ -732,6 +772,9 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
   __builtin_amdgcn_wave_barrier();
   const int nfar = tc.fpre[9];
   const int satq = a.span - 1;
+  // a light tile keeps all its candidates: its order slot is known now, its loads overlap the walk
+  OrderSlot os;
+  if (a.order) os.begin(a, t, tc.pre[9] + nfar);
   for_each_candidate<64>(tc, a.recs, tx, ty, a.S, a.span, lane, [&](unsigned long long key) {
     keys[wave_append(fill, true)] = key;
   });
@@ -784,7 +827,7 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
     }
   }
   if (a.order) {
-    const int slot = order_slot(a, t, m);
+    const int slot = os.end(a);
     if (lane == 0) a.order[slot] = t;
   }
   if (lane == 0) {
@@ -816,6 +859,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
   __shared__ TileCells tcs[NT / 64];
   __shared__ int s_wfill[NT / 64];
   const int T = a.ntx * a.nty;
+  const int t_heavy = lists[blockIdx.x];  // this block's tile if it is a heavy one (read ahead)
   const int nh = nlist[0], nl = nlist[1];
   if (static_cast<int>(blockIdx.x) >= nh) {
     const int g0 = (static_cast<int>(blockIdx.x) - nh) * (NT / 64);
@@ -841,7 +885,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
   __shared__ int s_sat[9];      // saturated regular candidates per stencil index
   __shared__ int s_jstar[2];    // j*, rank inside cell j*'s tie set
 
-  const int t = lists[blockIdx.x];
+  const int t = t_heavy;
   const int tx = t % a.ntx, ty = t / a.ntx;
   if (threadIdx.x < 64) load_tile_cells(tc, tx, ty, a.ntx, a.nty, a.cell_start, a.far_start);
   if (threadIdx.x == 0) {
@@ -920,6 +964,19 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
       if (r == cnt - 1) {  // the whole bin survives
         prefix = ~0u;
         stop = 0;
+      } else if (cnt <= 32) {
+        // a few ties (the usual case): each thread ranks one of them by its (j, g) sub-key
+        if (static_cast<int>(threadIdx.x) < cnt) {
+          const unsigned long long key = s_tie[threadIdx.x];
+          const int below = count_below(sub_key(key, gbits), cnt,
+                                        [&](int f) { return sub_key(s_tie[f], gbits); });
+          const int p = wave_append(&s_fill, below <= r);
+          if (p >= 0) s_keys[p] = key;
+        } else {
+          wave_append(&s_fill, false);
+        }
+        prefix = 0;
+        stop = -1;
       } else if (in_lds) {
         radix_select<NT>([&](auto&& g) {
           for (int e = threadIdx.x; e < cnt; e += NT) g(sub_key(s_tie[e], gbits));
@@ -931,8 +988,10 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
           });
         }, r, 4 + gbits, s_hist, s_tmp, s_out, &prefix, &stop);
       }
-      const unsigned thr = stop >= 32 ? 0u : (prefix >> stop);
-      if (in_lds) {
+      const unsigned thr = stop >= 32 ? 0u : (prefix >> (stop < 0 ? 0 : stop));
+      if (stop < 0) {
+        // taken above
+      } else if (in_lds) {
         for (int e = threadIdx.x; e < cnt; e += NT) {
           const unsigned long long key = s_tie[e];
           const bool take = (sub_key(key, gbits) >> stop) <= thr;
@@ -995,7 +1054,20 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
       const unsigned gmask = (gbits >= 32) ? ~0u : ((1u << gbits) - 1u);
       unsigned prefix;
       int stop;
-      if (in_lds) {
+      if (in_lds && satj + fb <= 32 && rr < satj + fb - 1) {
+        // a few ties: each thread ranks one of them by g
+        const int nt = satj + fb;
+        if (static_cast<int>(threadIdx.x) < nt) {
+          const unsigned long long key = s_tie[threadIdx.x];
+          const int below = count_below(static_cast<unsigned>(key) & gmask, nt, [&](int f) {
+            return static_cast<unsigned>(s_tie[f]) & gmask;
+          });
+          const int p = wave_append(&s_fill, below <= rr);
+          if (p >= 0) s_keys[p] = key;
+        } else {
+          wave_append(&s_fill, false);
+        }
+      } else if (in_lds) {
         const int nt = satj + fb;
         if (rr == nt - 1) {  // all of them survive
           prefix = ~0u;
