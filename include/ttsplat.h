@@ -306,6 +306,21 @@ int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
                     float* proj, uint8_t* keep, int32_t* step_adv, float beta1, float beta2,
                     hipStream_t stream);
 
+/* tts_geom_fwd_ex followed by tts_assign_bins on its output (mu2d = proj, mu_stride 12, keep
+ * stride 1), as one call with the results of the two: the geometry trace and the rebin that
+ * follows it in the reference trainer (tools/resident_traced.py:682-686, geom_fwd :327-346,
+ * do_bin :519-539 on the projected means cache["mu2d_x/y"] and keep).  For
+ * G <= 131072 the binning's count pass runs inside the geometry launch, on the means it has
+ * just projected (one launch and one read of proj fewer); larger G launch the two as usual.
+ * Arguments and errors as the two entry points'. */
+int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_degree,
+                             const float* depth_bt, int G, const float* camera, float near_z,
+                             float blur, float* proj, uint8_t* keep, int32_t* step_adv,
+                             float beta1, float beta2, int H, int W, int S, int R, int K,
+                             int span, int32_t* idx, uint8_t* valid, int32_t* count,
+                             int32_t* ncand, int32_t* inv, int32_t* order, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+
 /* Geometry backward with SH colour and/or the depth weight: grad9 -> gparams[G,14], gsh_rest
  * (rest layout; rows beyond the degree written as zero; needed when sh_degree > 0), gdepth [G,2]
  * (optional).  Replaces tools/resident_traced.py:397-427 (geom_bwd) with its SH and depth-weight

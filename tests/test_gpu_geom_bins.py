@@ -1,0 +1,72 @@
+"""tts_geom_fwd_assign_bins (geometry forward + binning as one call; for G <= 131072 the
+binning's count pass runs inside the geometry launch) against tts_geom_fwd_ex followed by
+tts_assign_bins on the same inputs: proj, keep, bins, counts and the inverse table equal bit for
+bit; the tile order is a heaviest-first permutation either way (ties in no fixed order)."""
+import pytest
+import torch
+
+from helpers import config_inputs
+from ttsplat import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def two_ways(cfg, P, cam, **kw):
+    dev = "cuda"
+    camera = cam.device_block(dev)
+    T = (cfg.H // cfg.S) * (cfg.W // cfg.S)
+    G = P.shape[0]
+    outs = []
+    for fused in (False, True):
+        adv = None
+        if kw.get("advance"):
+            adv = torch.zeros(4, dtype=torch.int32, device=dev)
+        inv = torch.full((G, 9), -7, dtype=torch.int32, device=dev)
+        order = torch.empty(T, dtype=torch.int32, device=dev)
+        gkw = dict(sh_rest=kw.get("sh_rest"), sh_degree=kw.get("sh_degree", 0),
+                   depth_bt=kw.get("depth_bt"), advance=adv)
+        if fused:
+            proj, keep, idx, valid, count, ncand = kernels.geom_fwd_assign_bins(
+                P, camera, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span, inv=inv, order=order, **gkw)
+        else:
+            proj, keep = kernels.geom_fwd(P, camera, **gkw)
+            idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W,
+                                                           cfg.S, cfg.K, cfg.span, inv=inv,
+                                                           order=order)
+        torch.cuda.synchronize()
+        outs.append(dict(proj=proj, keep=keep, idx=idx, valid=valid, count=count, ncand=ncand,
+                         inv=inv, order=order, adv=adv))
+    return outs
+
+
+def check_equal(a, b, K):
+    for k in ("proj", "keep", "idx", "valid", "count", "ncand", "inv"):
+        assert torch.equal(a[k], b[k]), k
+    if a["adv"] is not None:
+        assert torch.equal(a["adv"], b["adv"])
+    T = a["count"].numel()
+    for o in (a["order"], b["order"]):
+        ol = o.long()
+        assert torch.equal(torch.sort(ol).values, torch.arange(T, device=ol.device))
+        kept = a["count"].long()[ol]
+        assert bool((kept[1:] <= kept[:-1]).all())
+
+
+@pytest.mark.parametrize("name,G", [("c4", None), ("c3", None), ("c1_ref", None), ("c3", 1),
+                                    ("c3", 257), ("c3", 511), ("c3", 513), ("c4", 150000)])
+def test_geom_fwd_assign_bins_equals_two_calls(name, G):
+    cfg, P, cam = config_inputs(name, G=G)
+    print(f"[geom+bins] {name} G={cfg.G}", flush=True)
+    a, b = two_ways(cfg, P.cuda(), cam)
+    check_equal(a, b, cfg.K)
+
+
+def test_geom_fwd_assign_bins_sh_depth_weight_advance():
+    cfg, P, cam = config_inputs("c4", G=60000)
+    gen = torch.Generator().manual_seed(4)
+    rest = torch.randn(cfg.G, 15, 3, generator=gen) * 0.1
+    bt = torch.tensor([1.5, 4.0], device="cuda")
+    a, b = two_ways(cfg, P.cuda(), cam, sh_rest=kernels.sh_rest_layout(rest.cuda()),
+                    sh_degree=3, depth_bt=bt, advance=True)
+    check_equal(a, b, cfg.K)
+    assert int(a["adv"][0]) == 1

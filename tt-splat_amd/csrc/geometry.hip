@@ -20,7 +20,7 @@
 
 #include <math.h>
 
-#include "tts_common.h"
+#include "bin_count.h"
 
 namespace tts {
 
@@ -505,6 +505,38 @@ __device__ __forceinline__ void advance_step(int32_t* step, float b1, float b2) 
 // separate k_adam_advance launch would do; nothing between this kernel and the Adam update
 // reads the block).
 // SH = true: view-dependent colour from the first n = sh_rest_count(deg) rest coefficients.
+// One gaussian's projection from its staged parameter row: the [12] proj record into orow,
+// keep[g], and the mean and keep flag handed back for the count pass.
+template <bool SH>
+__device__ __forceinline__ void geo_fwd_row(const float* srow, int g, int G,
+                                            const float* __restrict__ rest, int n_rest,
+                                            const float* __restrict__ dw, const Camera& cam,
+                                            float near_z, float blur, float* orow,
+                                            uint8_t* __restrict__ keep, float* mux, float* muy,
+                                            uint8_t* kept) {
+  float p[14];
+#pragma unroll
+  for (int i = 0; i < 14; ++i) p[i] = srow[i];
+  float rv[SH ? 3 * kShRest : 1];
+  if (SH) sh_load(rest, G, g, n_rest, rv);
+  GeoState s;
+  geo_forward(p, cam, near_z, blur, s, dw);
+  if (SH) {
+    float b[16];
+    sh_basis(p, cam, b);
+    sh_apply(p, b, rv, n_rest, s);
+  }
+  const float keo = s.keep ? s.o * s.rho : 0.0f;
+  const float out[12] = {s.mux, s.muy, s.a, s.b, s.c, s.mc[2], keo * s.color[0],
+                         keo * s.color[1], keo * s.color[2], keo, s.o, 0.0f};
+#pragma unroll
+  for (int i = 0; i < 12; ++i) orow[i] = out[i];
+  keep[g] = s.keep ? 1 : 0;
+  *mux = s.mux;
+  *muy = s.muy;
+  *kept = s.keep ? 1 : 0;
+}
+
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ params, int G,
                                                   const float* __restrict__ rest, int n_rest,
@@ -521,28 +553,86 @@ __global__ __launch_bounds__(256) void k_geom_fwd(const float* __restrict__ para
   __syncthreads();
   if ((int)threadIdx.x < rows) {
     const Camera cam = load_camera(camera);
-    float p[14];
-#pragma unroll
-    for (int i = 0; i < 14; ++i) p[i] = s_p[threadIdx.x * 15 + i];
-    float rv[SH ? 3 * kShRest : 1];
-    if (SH) sh_load(rest, G, g, n_rest, rv);
-    GeoState s;
-    geo_forward(p, cam, near_z, blur, s, dw);
-    if (SH) {
-      float b[16];
-      sh_basis(p, cam, b);
-      sh_apply(p, b, rv, n_rest, s);
-    }
-    const float keo = s.keep ? s.o * s.rho : 0.0f;
-    const float out[12] = {s.mux, s.muy, s.a, s.b, s.c, s.mc[2], keo * s.color[0],
-                           keo * s.color[1], keo * s.color[2], keo, s.o, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 12; ++i) s_o[threadIdx.x * 13 + i] = out[i];
-    keep[g] = s.keep ? 1 : 0;
+    float mux, muy;
+    uint8_t kept;
+    geo_fwd_row<SH>(s_p + threadIdx.x * 15, g, G, rest, n_rest, dw, cam, near_z, blur,
+                    s_o + threadIdx.x * 13, keep, &mux, &muy, &kept);
   }
   __syncthreads();
   stage_out<12, 13>(proj, g0, rows, s_o);
   if (adv && blockIdx.x == 0 && threadIdx.x == 0) advance_step(adv, b1, b2);
+}
+
+// The geometry forward of 512 gaussians, one per thread (two 256-row halves staged by the two
+// halves of the block), followed by binning's count pass over the same gaussians as a block of
+// 8 waves x 64 (count blocks of 512 gaussians, as CountSmall: the same count-matrix rows): the
+// means and keep flags reach the count pass through LDS instead of a second kernel reading proj
+// back.  proj/keep equal k_geom_fwd's; mat rows and cell_slot are k_bin_count's (in-cell ranks
+// of regular gaussians in LDS-atomic order, as there).
+using CountFused = CountGeo<512, 1>;
+template <bool SH>
+__global__ __launch_bounds__(512) void k_geom_fwd_count(
+    const float* __restrict__ params, int G, const float* __restrict__ rest, int n_rest,
+    const float* __restrict__ dw, const float* __restrict__ camera, float near_z, float blur,
+    float* __restrict__ proj, uint8_t* __restrict__ keep, int32_t* adv, float b1, float b2,
+    int ntx, int nty, float S, int span, int NB, int Tpad, int* __restrict__ mat,
+    int2* __restrict__ cell_slot) {
+  static_assert(CountFused::kBlock == CountSmall::kBlock && CountFused::kBlock == 2 * kGeoBlock,
+                "one count block = two geometry halves");
+  extern __shared__ float s_dyn[];
+  float2* s_mu = reinterpret_cast<float2*>(s_dyn);                   // [512] means
+  uint8_t* s_kv = reinterpret_cast<uint8_t*>(s_mu + 2 * kGeoBlock);  // [512] keep flags
+  float* s_u = reinterpret_cast<float*>(s_kv + 2 * kGeoBlock);       // staging, then count
+  const int half = threadIdx.x / kGeoBlock, lt = threadIdx.x % kGeoBlock;
+  float* s_p = s_u + half * kGeoBlock * 15;                          // this half's [256][15]
+  float* s_o = s_u + 2 * kGeoBlock * 15 + half * kGeoBlock * 13;     // this half's [256][13]
+  const int g0 = blockIdx.x * 2 * kGeoBlock + half * kGeoBlock;
+  const int rows = min(kGeoBlock, G - g0);  // <= 0: the block's second half lies past G
+  if (rows > 0) {  // stage_in with this half's thread index
+    const float* base = params + (int64_t)g0 * 14;
+    const int last = rows * 14 - 1;
+    float r[14];
+#pragma unroll
+    for (int k = 0; k < 14; ++k) r[k] = base[min(lt + k * kGeoBlock, last)];
+#pragma unroll
+    for (int k = 0; k < 14; ++k) {
+      const int i = lt + k * kGeoBlock;
+      if (i <= last) s_p[(i / 14) * 15 + i % 14] = r[k];
+    }
+  }
+  __syncthreads();
+  float mux = 0.f, muy = 0.f;
+  uint8_t kept = 0;
+  if (lt < rows) {
+    const Camera cam = load_camera(camera);
+    geo_fwd_row<SH>(s_p + lt * 15, g0 + lt, G, rest, n_rest, dw, cam, near_z, blur,
+                    s_o + lt * 13, keep, &mux, &muy, &kept);
+  }
+  s_mu[threadIdx.x] = make_float2(mux, muy);
+  s_kv[threadIdx.x] = kept;
+  __syncthreads();
+  if (rows > 0) {  // stage_out with this half's thread index
+    float* base = proj + (int64_t)g0 * 12;
+    const int n = rows * 12;
+    float r[12];
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      const int i = min(lt + k * kGeoBlock, n - 1);
+      r[k] = s_o[(i / 12) * 13 + i % 12];
+    }
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+      const int i = lt + k * kGeoBlock;
+      if (i < n) base[i] = r[k];
+    }
+  }
+  if (adv && blockIdx.x == 0 && threadIdx.x == 0) advance_step(adv, b1, b2);
+  __syncthreads();  // every staging read is done: the count pass reuses that LDS
+  // count layout: wave w owns [64 w, 64 w + 64) -- the thread's own gaussian
+  const float mx[1] = {mux}, my[1] = {muy};
+  const uint8_t kv[1] = {kept};
+  count_body<512, 1>(mx, my, kv, G, ntx, nty, S, span, NB, Tpad, reinterpret_cast<int*>(s_u),
+                     mat, cell_slot);
 }
 
 // gsh (SH only): dL/drest in the rest layout; rows l >= n_rest are written as zero.
@@ -917,6 +1007,34 @@ __global__ __launch_bounds__(256) void k_dw_adam(const float* __restrict__ part,
 __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) buf[i] = 0.0f;
+}
+
+int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degree,
+                          const float* depth_bt, int G, const float* camera, float near_z,
+                          float blur, float* proj, uint8_t* keep, int32_t* step_adv, float b1,
+                          float b2, int ntx, int nty, float S, int span, int NB, int Tpad,
+                          int* mat, int2* cell_slot, hipStream_t stream) {
+  const int nblk = (G + CountFused::kBlock - 1) / CountFused::kBlock;
+  const size_t stage = sizeof(float) * 2 * kGeoBlock * (15 + 13);
+  const size_t cnt = sizeof(int) * ((size_t)Tpad + (size_t)CountFused::kWaves * NB);
+  const size_t lds = (sizeof(float2) + 1) * 2 * kGeoBlock + (stage > cnt ? stage : cnt);
+  const bool sh = sh_degree > 0;
+  const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count<true>)
+                      : reinterpret_cast<const void*>(&k_geom_fwd_count<false>);
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return static_cast<int>(e);
+  }
+  if (sh)
+    k_geom_fwd_count<true><<<nblk, 512, lds, stream>>>(
+        params, G, sh_rest, sh_rest_count(sh_degree), depth_bt, camera, near_z, blur, proj, keep,
+        step_adv, b1, b2, ntx, nty, S, span, NB, Tpad, mat, cell_slot);
+  else
+    k_geom_fwd_count<false><<<nblk, 512, lds, stream>>>(
+        params, G, nullptr, 0, depth_bt, camera, near_z, blur, proj, keep, step_adv, b1, b2, ntx,
+        nty, S, span, NB, Tpad, mat, cell_slot);
+  return launch_status();
 }
 
 }  // namespace tts

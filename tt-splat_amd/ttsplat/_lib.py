@@ -61,6 +61,10 @@ SIGNATURES = {
                                     _vp, _vp]),
     "tts_geom_fwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_float, _c_float, _vp, _vp,
                                  _vp, _c_float, _c_float, _vp]),
+    "tts_geom_fwd_assign_bins": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_float, _c_float,
+                                          _vp, _vp, _vp, _c_float, _c_float, _c_int, _c_int,
+                                          _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
+                                          _vp, _vp, _vp, _c_size, _vp]),
     "tts_geom_bwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
                                  _vp, _vp, _vp, _vp, _vp]),
     "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_float,

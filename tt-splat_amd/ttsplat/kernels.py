@@ -165,6 +165,49 @@ def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, i
     return idx, valid, count, ncand
 
 
+def geom_fwd_assign_bins(params, camera, H, W, S=16, K=128, span=2048, R=1, near=NEAR,
+                         blur=BLUR, proj=None, keep=None, sh_rest=None, sh_degree=0,
+                         depth_bt=None, advance=None, b1=None, b2=None, workspace=None, idx=None,
+                         valid=None, count=None, ncand=None, inv=None, order=None):
+    """geom_fwd then assign_bins on proj's means and keep, as one call (for G <= 131072 the
+    binning's count pass runs inside the geometry launch).  Returns (proj, keep, idx, valid,
+    count, ncand); inv and order are written when buffers are passed."""
+    G = params.shape[0]
+    dev = params.device
+    require(params, "params", F32, (G, 14))
+    require(camera, "camera", F32, (16,), dev)
+    _sh_check(sh_rest, sh_degree, G, dev)
+    _dw_check(depth_bt, dev)
+    proj = torch.empty(G, 12, device=dev, dtype=F32) if proj is None else proj
+    keep = torch.empty(G, device=dev, dtype=U8) if keep is None else keep
+    _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
+    require(keep, "keep", U8, (G,), dev)
+    if advance is not None:
+        require(advance, "advance", I32, (4,), dev)
+    if S not in (16, 32) or H % S or W % S:
+        raise ValueError(f"tile side {S} must be 16 or 32 and divide {H}x{W}")
+    T = (H // S) * (W // S)
+    idx = torch.empty(T, K, device=dev, dtype=I32) if idx is None else idx
+    valid = torch.empty(T, K, device=dev, dtype=U8) if valid is None else valid
+    count = torch.empty(T, device=dev, dtype=I32) if count is None else count
+    ncand = torch.empty(T, device=dev, dtype=I32) if ncand is None else ncand
+    require(idx, "idx", I32, (T, K), dev)
+    require(valid, "valid", U8, (T, K), dev)
+    require(count, "count", I32, (T,), dev)
+    require(ncand, "ncand", I32, (T,), dev)
+    if inv is not None:
+        require(inv, "inv", I32, (G, 9), dev)
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
+    workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
+    call("tts_geom_fwd_assign_bins", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt),
+         G, ptr(camera), near, blur, ptr(proj), ptr(keep), ptr(advance),
+         BETA1 if b1 is None else b1, BETA2 if b2 is None else b2, H, W, S, R, K, span,
+         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(order), ptr(workspace),
+         workspace.numel(), stream())
+    return proj, keep, idx, valid, count, ncand
+
+
 # ---------------------------------------------------------------------------------- splat --
 def _bins_check(idx, valid, H, W, S, dev):
     T = (H // S) * (W // S)

@@ -5,7 +5,8 @@ captures the step as ttnn traces (:551-567) and replays them per iteration (:667
 host binning/loss/scatter round trips in between.  Here one step is, on one stream and with no
 host round trip:
 
-    geom_fwd (+ Adam step advance) -> assign_bins (5 kernels, + inverse table and tile order)
+    geom_fwd_assign_bins (geometry + Adam step advance + the binning's count pass in one
+             kernel, then 3 binning kernels, + inverse table and tile order)
              -> splat_fwd -> loss_grad_stats (1 kernel) -> splat_bwd (theta bwd, per-slot gradients)
              -> geom_bwd_adam (slot gather-reduce + geometry bwd + Adam)
 
@@ -186,13 +187,19 @@ class TrainStep:
         """Geometry + binning + fused splat for camera ci into self.image.  advance=True: the
         geometry launch also advances the Adam step block (a training step's first kernel).
         rebin=False: the bins last computed are reused (the binning kernels are not run)."""
-        kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep, sh_rest=self.sh,
-                         sh_degree=self.sh_degree, depth_bt=self.dw,
-                         advance=self.step_block if advance else None)
-        if rebin:
-            kernels.assign_bins(self.proj[:, 0:2], self.keep, self.H, self.W, self.S, self.K,
-                                self.span, 1, self.bin_ws, self.idx, self.valid, self.count,
-                                self.ncand, self.inv, self.order)
+        adv = self.step_block if advance else None
+        if rebin:   # one call: the binning's count pass rides on the geometry launch
+            kernels.geom_fwd_assign_bins(self.P, self.cams[ci], self.H, self.W, self.S, self.K,
+                                         self.span, proj=self.proj, keep=self.keep,
+                                         sh_rest=self.sh, sh_degree=self.sh_degree,
+                                         depth_bt=self.dw, advance=adv,
+                                         workspace=self.bin_ws, idx=self.idx, valid=self.valid,
+                                         count=self.count, ncand=self.ncand, inv=self.inv,
+                                         order=self.order)
+        else:
+            kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep,
+                             sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
+                             advance=adv)
         if self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
