@@ -231,6 +231,12 @@ def time_kernels(ts, reps, torch, kernels):
         "binning": lambda: kernels.assign_bins(ts.proj[:, 0:2], ts.keep, ts.H, ts.W, ts.S, ts.K,
                                                ts.span, 1, ts.bin_ws, ts.idx, ts.valid,
                                                ts.count, ts.ncand, ts.inv, ts.order),
+        # what the step launches: the geometry forward carrying the binning's count pass, then
+        # the other binning kernels
+        "geom_fwd_binning": lambda: kernels.geom_fwd_assign_bins(
+            ts.P, cam, ts.H, ts.W, ts.S, ts.K, ts.span, proj=ts.proj, keep=ts.keep,
+            workspace=ts.bin_ws, idx=ts.idx, valid=ts.valid, count=ts.count, ncand=ts.ncand,
+            inv=ts.inv, order=ts.order, **sh),
         "splat_fwd": (lambda: kernels.splat_fwd_mx(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
                                                    ts.S, ts.k, ts.image, ts.den, ts.order,
                                                    bf16=True))
