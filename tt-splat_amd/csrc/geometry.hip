@@ -464,10 +464,15 @@ __device__ __forceinline__ void slot_loads(const float* __restrict__ gslot, cons
                                            SlotRecs& r) {
 #pragma unroll
   for (int j = 0; j < 9; ++j) {
-    const float* src = gslot + (int64_t)(e[j] >= 0 ? e[j] : 0) * 9;
-    r.a[j] = *reinterpret_cast<const f4u*>(src);
-    r.b[j] = *reinterpret_cast<const f4u*>(src + 4);
-    r.c[j] = src[8];
+    r.a[j] = f4u{0.f, 0.f, 0.f, 0.f};
+    r.b[j] = r.a[j];
+    r.c[j] = 0.f;
+    if (e[j] >= 0) {  // lanes without this entry issue no address
+      const float* src = gslot + (int64_t)e[j] * 9;
+      r.a[j] = *reinterpret_cast<const f4u*>(src);
+      r.b[j] = *reinterpret_cast<const f4u*>(src + 4);
+      r.c[j] = src[8];
+    }
   }
 }
 __device__ __forceinline__ void slot_sum(const int* e, const SlotRecs& r, float* gin) {
