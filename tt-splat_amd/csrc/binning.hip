@@ -647,9 +647,11 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
 // The survivors are placed by rank (keys are unique: slot = number of smaller survivors).  A
 // gaussian reaches a tile through exactly one stencil index j, so the inverse table entry
 // inv[g][j] = t*K + slot has a single writer.
+// 8 waves per SIMD (at most 64 registers): a heavy tile's block waits on LDS most of its time,
+// and at K=256 the LDS use (~18 KB) still lets 8 blocks share a CU.
 template <int NT>
-__global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __restrict__ lists,
-                                                   const int* __restrict__ nlist) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_bin_select(
+    SelectArgs a, const int* __restrict__ lists, const int* __restrict__ nlist) {
   extern __shared__ unsigned char s_dyn[];
   __shared__ TileCells tcs[NT / 64];
   __shared__ int s_wfill[NT / 64];
@@ -679,6 +681,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
   __shared__ int s_fill, s_tfill;
   __shared__ int s_sat[9];      // saturated regular candidates per stencil index
   __shared__ int s_jstar[2];    // j*, rank inside cell j*'s tie set
+  __shared__ unsigned s_grp[64];  // survivors per group of qd2 bins, then packed prefixes
 
   const int t = t_heavy;
   const int tx = t % a.ntx, ty = t / a.ntx;
@@ -688,6 +691,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     s_tfill = 0;
   }
   if (threadIdx.x < 9) s_sat[threadIdx.x] = 0;
+  if (threadIdx.x < 64) s_grp[threadIdx.x] = 0;
   // heavy tiles (every block of this range) histogram qd2: zeroed while the cells load
   for (int b = threadIdx.x; b < span; b += NT) s_hist[b] = 0;
   __syncthreads();
@@ -697,6 +701,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
   // wave 0 takes the tile's order slot now; its loads overlap the candidate walks
   const int oslot = (a.order && threadIdx.x < 64) ? order_slot(a, t, n) : 0;
 
+  int qlim = span;  // above every survivor's qd2 bin
   if (n <= K) {
     for_each_candidate<NT>(tc, recs, tx, ty, S, span, threadIdx.x, [&](unsigned long long key) {
       s_keys[wave_append(&s_fill, true)] = key;
@@ -743,6 +748,7 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     find_rank_bin<NT>(s_hist, span, K - 1, s_tmp, s_out);
     const int qb = s_out[0], before = s_out[1], cnt = s_out[2];
     const int r = K - 1 - before;  // rank of the K-th key inside bin qb
+    qlim = qb + 1;
     if (qb < satq) {
       // ---------------- tie bin of regular candidates only ----------------
       const bool in_lds = cnt <= kTieCap;
@@ -908,38 +914,102 @@ __global__ __launch_bounds__(NT) void k_bin_select(SelectArgs a, const int* __re
     }
   }
   __syncthreads();
-  // Place the m survivors by rank (unique keys: rank = number of smaller survivors).  Two
-  // adjacent lanes share a survivor, each counting over half of them; the keys are padded to a
-  // multiple of 16 with the largest key (never below a survivor) and read 8 at a time.
+  // Place the m survivors by rank (unique keys: rank = number of smaller survivors).
   const int m = min(s_fill, K);
-  const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
-  if (static_cast<int>(threadIdx.x) < m16 - m) s_keys[m + threadIdx.x] = ~0ull;
-  __syncthreads();
   const int64_t base = static_cast<int64_t>(t) * K;
-  const int half = threadIdx.x & 1;
-  const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(s_keys + half * (m16 / 2));
-  for (int s0 = 0; s0 < K; s0 += NT / 2) {
-    const int s = s0 + (static_cast<int>(threadIdx.x) >> 1);
-    const unsigned long long key = s < m ? s_keys[s] : 0ull;
-    int rank = 0;
-    if (s0 < m) {
-      for (int e = 0; e < m16 / 4; e += 4) {
-        const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
-        rank += (k0.x < key) + (k0.y < key) + (k1.x < key) + (k1.y < key) + (k2.x < key) +
-                (k2.y < key) + (k3.x < key) + (k3.y < key);
+  auto put = [&](int rank, unsigned long long key) {
+    const int g = static_cast<int32_t>(key & 0xffffffffull);
+    a.idx[base + rank] = g;
+    if (a.inv)
+      a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
+    a.valid[base + rank] = 1;
+  };
+  auto clear = [&](int s) {
+    a.idx[base + s] = 0;
+    a.valid[base + s] = 0;
+  };
+  if (K <= 128) {
+    // All pairs: two adjacent lanes share a survivor, each counting over half of them; the keys
+    // are padded to a multiple of 16 with the largest key (never below a survivor) and read 8 at
+    // a time.
+    const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
+    if (static_cast<int>(threadIdx.x) < m16 - m) s_keys[m + threadIdx.x] = ~0ull;
+    __syncthreads();
+    const int half = threadIdx.x & 1;
+    const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(s_keys + half * (m16 / 2));
+    for (int s0 = 0; s0 < K; s0 += NT / 2) {
+      const int s = s0 + (static_cast<int>(threadIdx.x) >> 1);
+      const unsigned long long key = s < m ? s_keys[s] : 0ull;
+      int rank = 0;
+      if (s0 < m) {
+#pragma unroll 2  // 8 reads in flight; a deeper unroll spills at 64 registers
+        for (int e = 0; e < m16 / 4; e += 4) {
+          const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
+          rank += (k0.x < key) + (k0.y < key) + (k1.x < key) + (k1.y < key) + (k2.x < key) +
+                  (k2.y < key) + (k3.x < key) + (k3.y < key);
+        }
+      }
+      rank += __shfl_xor(rank, 1);
+      if (half == 0 && s < K) {
+        if (s < m) put(rank, key);
+        else clear(s);
       }
     }
-    rank += __shfl_xor(rank, 1);
-    if (half == 0 && s < K) {
+  } else {
+    // Larger K (the all-pairs count grows as K^2): the survivors are grouped by runs of qd2
+    // bins, 64 groups below qlim (every survivor's bin is below it), and rank = survivors in
+    // lower groups + smaller survivors in the own group.  Survivor counts per group (with each
+    // survivor's arrival index from the atomic), one wave's exclusive scan packed with the
+    // counts, the keys gathered by group in the tie buffer, then each survivor counts the
+    // smaller keys of its own group.
+    int shift = 0;
+    while (((qlim - 1) >> shift) > 63) ++shift;
+    auto group = [&](unsigned long long key) { return static_cast<int>(key >> kQShift) >> shift; };
+    constexpr int kPer = kMaxK / NT;
+    int pa[kPer];  // arrival index in the group (the keys are read again from s_keys)
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int s = static_cast<int>(threadIdx.x) + k * NT;
+      pa[k] = s < m ? static_cast<int>(atomicAdd(&s_grp[group(s_keys[s])], 1u)) : 0;
+    }
+    if (static_cast<int>(threadIdx.x) < 8) s_tie[m + threadIdx.x] = ~0ull;  // above every key
+    __syncthreads();
+    if (threadIdx.x < 64) {
+      const int v = static_cast<int>(s_grp[threadIdx.x]);
+      const int inc = wave_incl_scan(v);
+      s_grp[threadIdx.x] = static_cast<unsigned>((inc - v) << 16 | v);  // start, count (<= K)
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int s = static_cast<int>(threadIdx.x) + k * NT;
       if (s < m) {
-        const int g = static_cast<int32_t>(key & 0xffffffffull);
-        a.idx[base + rank] = g;
-        if (a.inv)
-          a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-        a.valid[base + rank] = 1;
-      } else {
-        a.idx[base + s] = 0;
-        a.valid[base + s] = 0;
+        const unsigned long long key = s_keys[s];
+        s_tie[(s_grp[group(key)] >> 16) + pa[k]] = key;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int s = static_cast<int>(threadIdx.x) + k * NT;
+      if (s < m) {
+        const unsigned long long key = s_keys[s];
+        const unsigned v = s_grp[group(key)];
+        const int start = static_cast<int>(v >> 16), c = static_cast<int>(v & 0xffffu);
+        int rank = start;
+        if (c > 1) {
+          // keys past the group's end are larger (later groups, or the padding)
+          for (int f = 0; f < c; f += 8) {
+            unsigned long long w[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = s_tie[start + f + i];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rank += w[i] < key ? 1 : 0;
+          }
+        }
+        put(rank, key);
+      } else if (s < K) {
+        clear(s);
       }
     }
   }
