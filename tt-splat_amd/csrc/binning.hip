@@ -555,10 +555,44 @@ struct OrderSlot {
   }
 };
 
+// Survivors are placed by groups in key order: 55 runs of 2^shift qd2 bins below the saturated
+// bin span-1 (group_shift picks the run length that puts bin qtop, the highest unsaturated bin
+// that holds survivors, in run 54 or below), then the saturated bin split by stencil index j
+// (groups 55..63).  Keys order by q, then j, then g, so every key of a group is below every key
+// of a later group, and a survivor's slot is the number of survivors in lower groups plus its
+// rank inside its group.
+constexpr int kGroups = 64;
+__device__ __forceinline__ int group_shift(int qtop) {
+  int shift = 0;
+  while ((qtop >> shift) > 54) ++shift;
+  return shift;
+}
+__device__ __forceinline__ int key_group(unsigned long long key, int satq, int shift) {
+  const int q = static_cast<int>(key >> kQShift);
+  return q < satq ? (q >> shift) : 55 + static_cast<int>((key >> kJShift) & 15ull);
+}
+// start + the number of the c keys buf[start, start + c) below key.  The 7 entries past the
+// group's end must hold larger keys (later groups, or padding): the reads go 8 at a time.
+__device__ __forceinline__ int rank_in_group(unsigned long long key, const unsigned long long* buf,
+                                             int start, int c) {
+  int rank = start;
+  if (c > 1) {
+    for (int f = 0; f < c; f += 8) {
+      unsigned long long w[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) w[i] = buf[start + f + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rank += w[i] < key ? 1 : 0;
+    }
+  }
+  return rank;
+}
+
 // Light tile (n <= K candidates: all survive), one wave: collect the keys in LDS, then place
-// them by rank.
+// them by groups.  keys holds 2 * kpow2 + 8 entries (the keys, then the keys gathered by group)
+// and grp kGroups words.
 __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCells& tc,
-                                             unsigned long long* keys, int* fill) {
+                                             unsigned long long* keys, unsigned* grp, int* fill) {
   const int lane = lane_id();
   const int tx = t % a.ntx, ty = t / a.ntx;
   load_tile_cells(tc, tx, ty, a.ntx, a.nty, a.cell_start, a.far_start);
@@ -582,40 +616,86 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
   const int m = *fill;
-  // the keys padded to a multiple of 16 with the largest key (never below a survivor), so the
-  // rank counts read them 8 at a time with no tail
-  const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
-  if (lane < m16 - m) keys[m + lane] = ~0ull;
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  __builtin_amdgcn_wave_barrier();
   const int64_t base = static_cast<int64_t>(t) * a.K;
-  const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(keys);
-  for (int s0 = 0; s0 < a.K; s0 += 128) {
-    // slots s0 + lane and s0 + 64 + lane share each key read
-    const int sa = s0 + lane, sb = sa + 64;
-    const unsigned long long ka = sa < m ? keys[sa] : 0ull, kb = sb < m ? keys[sb] : 0ull;
-    int ra = 0, rb = 0;
-    if (s0 < m) {
-      for (int e = 0; e < m16 / 2; e += 4) {
-        const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
-        ra += (k0.x < ka) + (k0.y < ka) + (k1.x < ka) + (k1.y < ka) + (k2.x < ka) + (k2.y < ka) +
-              (k3.x < ka) + (k3.y < ka);
-        rb += (k0.x < kb) + (k0.y < kb) + (k1.x < kb) + (k1.y < kb) + (k2.x < kb) + (k2.y < kb) +
-              (k3.x < kb) + (k3.y < kb);
+  if (a.K <= 128) {
+    // all pairs (cheaper than the groups' extra passes at this size)
+    // the keys padded to a multiple of 16 with the largest key (never below a survivor), so the
+    // rank counts read them 8 at a time with no tail
+    const int m16 = (m + 15) & ~15;  // <= kpow2, a power of two >= 16
+    if (lane < m16 - m) keys[m + lane] = ~0ull;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const ulonglong2* kp = reinterpret_cast<const ulonglong2*>(keys);
+    for (int s0 = 0; s0 < a.K; s0 += 128) {
+      // slots s0 + lane and s0 + 64 + lane share each key read
+      const int sa = s0 + lane, sb = sa + 64;
+      const unsigned long long ka = sa < m ? keys[sa] : 0ull, kb = sb < m ? keys[sb] : 0ull;
+      int ra = 0, rb = 0;
+      if (s0 < m) {
+        for (int e = 0; e < m16 / 2; e += 4) {
+          const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
+          ra += (k0.x < ka) + (k0.y < ka) + (k1.x < ka) + (k1.y < ka) + (k2.x < ka) + (k2.y < ka) +
+                (k3.x < ka) + (k3.y < ka);
+          rb += (k0.x < kb) + (k0.y < kb) + (k1.x < kb) + (k1.y < kb) + (k2.x < kb) + (k2.y < kb) +
+                (k3.x < kb) + (k3.y < kb);
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int s = h ? sb : sa;
+        const unsigned long long key = h ? kb : ka;
+        const int rank = h ? rb : ra;
+        if (s < m) {
+          const int g = static_cast<int32_t>(key & 0xffffffffull);
+          a.idx[base + rank] = g;
+          if (a.inv)
+            a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
+          a.valid[base + rank] = 1;
+        } else if (s < a.K) {
+          a.idx[base + s] = 0;
+          a.valid[base + s] = 0;
+        }
       }
     }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int s = h ? sb : sa;
-      const unsigned long long key = h ? kb : ka;
-      const int rank = h ? rb : ra;
+  } else {
+    // Group counts (LDS atomics), one scan, then the keys gathered by group behind the key list.
+    // A group's word packs start << 20 | count << 10 | cursor (each <= K <= 512); the gathering
+    // atomics advance the cursor.
+    const int shift = group_shift(satq - 1);
+    unsigned long long* gat = keys + a.kpow2;
+    grp[lane] = 0;
+    if (lane < 8) gat[m + lane] = ~0ull;  // above every key
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int s = lane; s < m; s += 64) atomicAdd(&grp[key_group(keys[s], satq, shift)], 1u);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    {
+      const int v = static_cast<int>(grp[lane]);
+      const int inc = wave_incl_scan(v);
+      grp[lane] = static_cast<unsigned>((inc - v) << 20 | v << 10);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int s = lane; s < m; s += 64) {
+      const unsigned long long key = keys[s];
+      const unsigned w = atomicAdd(&grp[key_group(key, satq, shift)], 1u);
+      gat[(w >> 20) + (w & 1023u)] = key;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int s = lane; s < a.K; s += 64) {
       if (s < m) {
+        const unsigned long long key = keys[s];
+        const unsigned w = grp[key_group(key, satq, shift)];
+        const int rank = rank_in_group(key, gat, static_cast<int>(w >> 20),
+                                       static_cast<int>((w >> 10) & 1023u));
         const int g = static_cast<int32_t>(key & 0xffffffffull);
         a.idx[base + rank] = g;
         if (a.inv)
           a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
         a.valid[base + rank] = 1;
-      } else if (s < a.K) {
+      } else {
         a.idx[base + s] = 0;
         a.valid[base + s] = 0;
       }
@@ -663,8 +743,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
     if (g0 >= nl) return;
     const int w = threadIdx.x >> 6;
     if (g0 + w < nl) {
-      unsigned long long* keys = reinterpret_cast<unsigned long long*>(s_dyn) + w * a.kpow2;
-      select_light(lists[T - 1 - (g0 + w)], a, tcs[w], keys, &s_wfill[w]);
+      unsigned long long* keys =
+          reinterpret_cast<unsigned long long*>(s_dyn) + w * (2 * a.kpow2 + 8 + kGroups / 2);
+      select_light(lists[T - 1 - (g0 + w)], a, tcs[w], keys,
+                   reinterpret_cast<unsigned*>(keys + 2 * a.kpow2 + 8), &s_wfill[w]);
     }
     return;
   }
@@ -681,7 +763,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   __shared__ int s_fill, s_tfill;
   __shared__ int s_sat[9];      // saturated regular candidates per stencil index
   __shared__ int s_jstar[2];    // j*, rank inside cell j*'s tie set
-  __shared__ unsigned s_grp[64];  // survivors per group of qd2 bins, then packed prefixes
+  __shared__ unsigned s_grp[kGroups];  // survivors per group, then packed prefixes
 
   const int t = t_heavy;
   const int tx = t % a.ntx, ty = t / a.ntx;
@@ -691,7 +773,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
     s_tfill = 0;
   }
   if (threadIdx.x < 9) s_sat[threadIdx.x] = 0;
-  if (threadIdx.x < 64) s_grp[threadIdx.x] = 0;
+  if (threadIdx.x < kGroups) s_grp[threadIdx.x] = 0;
   // heavy tiles (every block of this range) histogram qd2: zeroed while the cells load
   for (int b = threadIdx.x; b < span; b += NT) s_hist[b] = 0;
   __syncthreads();
@@ -956,15 +1038,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
       }
     }
   } else {
-    // Larger K (the all-pairs count grows as K^2): the survivors are grouped by runs of qd2
-    // bins, 64 groups below qlim (every survivor's bin is below it), and rank = survivors in
-    // lower groups + smaller survivors in the own group.  Survivor counts per group (with each
-    // survivor's arrival index from the atomic), one wave's exclusive scan packed with the
-    // counts, the keys gathered by group in the tie buffer, then each survivor counts the
-    // smaller keys of its own group.
-    int shift = 0;
-    while (((qlim - 1) >> shift) > 63) ++shift;
-    auto group = [&](unsigned long long key) { return static_cast<int>(key >> kQShift) >> shift; };
+    // Larger K (the all-pairs count grows as K^2): placement by groups (key_group; every
+    // survivor's bin is below qlim).  Survivor counts per group (with each survivor's arrival
+    // index from the atomic), one wave's exclusive scan packed with the counts, the keys
+    // gathered by group in the tie buffer, then each survivor counts the smaller keys of its
+    // own group.
+    const int shift = group_shift(min(qlim - 1, satq - 1));
+    auto group = [&](unsigned long long key) { return key_group(key, satq, shift); };
     constexpr int kPer = kMaxK / NT;
     int pa[kPer];  // arrival index in the group (the keys are read again from s_keys)
 #pragma unroll
@@ -995,19 +1075,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
       if (s < m) {
         const unsigned long long key = s_keys[s];
         const unsigned v = s_grp[group(key)];
-        const int start = static_cast<int>(v >> 16), c = static_cast<int>(v & 0xffffu);
-        int rank = start;
-        if (c > 1) {
-          // keys past the group's end are larger (later groups, or the padding)
-          for (int f = 0; f < c; f += 8) {
-            unsigned long long w[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) w[i] = s_tie[start + f + i];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) rank += w[i] < key ? 1 : 0;
-          }
-        }
-        put(rank, key);
+        put(rank_in_group(key, s_tie, static_cast<int>(v >> 16), static_cast<int>(v & 0xffffu)),
+            key);
       } else if (s < K) {
         clear(s);
       }
@@ -1196,7 +1265,8 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
   const int hist_bins = span > (1 << kDigitBits) ? span : (1 << kDigitBits);
   const size_t heavy_lds = sizeof(unsigned long long) * ((size_t)kpow2 + kTieCap) +
                            sizeof(unsigned) * (size_t)hist_bins;
-  const size_t light_lds = sizeof(unsigned long long) * (size_t)kpow2 * (kSelThreads / 64);
+  const size_t light_lds =
+      sizeof(unsigned long long) * (2 * (size_t)kpow2 + 8 + kGroups / 2) * (kSelThreads / 64);
   const size_t lds = heavy_lds > light_lds ? heavy_lds : light_lds;
   SelectArgs sa{ws.recs, ws.far_g, ws.cell_start, ws.far_start, ntx, nty, Sf, span, K, kpow2,
                 gbits, idx, valid, count, ncand, inv, order, ws.key_hist, ws.tile_pos, ncls};
