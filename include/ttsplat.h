@@ -175,6 +175,24 @@ int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
                   const float* image, const float* den, const float* gimage,
                   float* gslot, float* gwb, hipStream_t stream);
 
+/* tts_splat_fwd (S = 16) on the slot records of tts_geom_fwd_assign_bins: tile order[p] is
+ * rendered from slot_rec[p][0 .. pos_count[p]) -- the same image and den as tts_splat_fwd on
+ * those bins in that order, with one read of contiguous records per tile in place of the
+ * order -> idx -> proj chain.  Replaces tools/bh_views.py:65-71 and the device chain
+ * tools/resident_traced.py:358-370 on the operands of the θ gather
+ * (tools/m4_train_binned.py:130-143, 207-211). */
+int tts_splat_fwd_rec(const float* slot_rec, const int32_t* pos_count, const int32_t* order,
+                      int H, int W, int S, int K, float k, const float* bg, float* image,
+                      float* den, hipStream_t stream);
+
+/* tts_splat_bwd (S = 16) on the slot records: the same gslot (at slot t*K + s of tile
+ * t = order[p]) and gwb.  Replaces WSRPolySplatHot.backward (spike/backward.py:42-58) and
+ * render_bwd + theta_bwd (tools/resident_traced.py:60-88) on the gathered operands. */
+int tts_splat_bwd_rec(const float* slot_rec, const int32_t* pos_count, const int32_t* order,
+                      int H, int W, int S, int K, float k, const float* bg, const float* image,
+                      const float* den, const float* gimage, float* gslot, float* gwb,
+                      hipStream_t stream);
+
 /* Splat backward on pre-gathered operands: writes per-slot gtheta[T,6,K], gcol[T,K,3],
  * goc[T,K] (overwritten) and per-tile dL/dw_b partials gwb[T] (may be NULL).  Replaces
  * _DevRenderBinned.backward, tools/m4_train_binned.py:168-186. */
@@ -312,14 +330,22 @@ int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
  * do_bin :519-539 on the projected means cache["mu2d_x/y"] and keep).  For
  * G <= 131072 the binning's count pass runs inside the geometry launch, on the means it has
  * just projected (one launch and one read of proj fewer); larger G launch the two as usual.
- * Arguments and errors as the two entry points'. */
+ * Arguments and errors as the two entry points'.
+ * slot_rec [T][K][12] and pos_count [T] (optional, together, and only with order): the slot
+ * records of the bins -- the projection record proj[idx[t][s]] of every kept slot s, stored at
+ * slot_rec[p][s] where p is the tile's place in order (order[p] = t), and pos_count[p] =
+ * count[t].  They are the per-(tile, slot) operands of the reference's θ gather
+ * (tools/m4_train_binned.py:130-143, 207-211) in the order the splat kernels take their tiles;
+ * tts_splat_fwd_rec / tts_splat_bwd_rec read them instead of order -> idx -> proj.  Slots at or
+ * past pos_count[p] are not written. */
 int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_degree,
                              const float* depth_bt, int G, const float* camera, float near_z,
                              float blur, float* proj, uint8_t* keep, int32_t* step_adv,
                              float beta1, float beta2, int H, int W, int S, int R, int K,
                              int span, int32_t* idx, uint8_t* valid, int32_t* count,
-                             int32_t* ncand, int32_t* inv, int32_t* order, void* workspace,
-                             size_t workspace_bytes, hipStream_t stream);
+                             int32_t* ncand, int32_t* inv, int32_t* order, float* slot_rec,
+                             int32_t* pos_count, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
 
 /* Geometry backward with SH colour and/or the depth weight: grad9 -> gparams[G,14], gsh_rest
  * (rest layout; rows beyond the degree written as zero; needed when sh_degree > 0), gdepth [G,2]

@@ -1,7 +1,11 @@
 """tts_geom_fwd_assign_bins (geometry forward + binning as one call; for G <= 131072 the
 binning's count pass runs inside the geometry launch) against tts_geom_fwd_ex followed by
 tts_assign_bins on the same inputs: proj, keep, bins, counts and the inverse table equal bit for
-bit; the tile order is a heaviest-first permutation either way (ties in no fixed order)."""
+bit; the tile order is a heaviest-first permutation either way (ties in no fixed order).  The
+fused call also writes the slot records: slot_rec[p][s] = proj[idx[order[p]][s]] for every kept
+slot and pos_count[p] = count[order[p]]."""
+import dataclasses
+
 import pytest
 import torch
 
@@ -25,9 +29,13 @@ def two_ways(cfg, P, cam, **kw):
         order = torch.empty(T, dtype=torch.int32, device=dev)
         gkw = dict(sh_rest=kw.get("sh_rest"), sh_degree=kw.get("sh_degree", 0),
                    depth_bt=kw.get("depth_bt"), advance=adv)
+        rec = pos = None
         if fused:
+            rec = torch.full((T, cfg.K, 12), float("nan"), device=dev)
+            pos = torch.full((T,), -1, dtype=torch.int32, device=dev)
             proj, keep, idx, valid, count, ncand = kernels.geom_fwd_assign_bins(
-                P, camera, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span, inv=inv, order=order, **gkw)
+                P, camera, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span, inv=inv, order=order,
+                slot_rec=rec, pos_count=pos, **gkw)
         else:
             proj, keep = kernels.geom_fwd(P, camera, **gkw)
             idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W,
@@ -35,7 +43,7 @@ def two_ways(cfg, P, cam, **kw):
                                                            order=order)
         torch.cuda.synchronize()
         outs.append(dict(proj=proj, keep=keep, idx=idx, valid=valid, count=count, ncand=ncand,
-                         inv=inv, order=order, adv=adv))
+                         inv=inv, order=order, adv=adv, rec=rec, pos=pos))
     return outs
 
 
@@ -50,6 +58,17 @@ def check_equal(a, b, K):
         assert torch.equal(torch.sort(ol).values, torch.arange(T, device=ol.device))
         kept = a["count"].long()[ol]
         assert bool((kept[1:] <= kept[:-1]).all())
+    check_records(b)
+
+
+def check_records(o):
+    """Slot records of the fused call against proj gathered through its own bins and order."""
+    ol = o["order"].long()
+    assert torch.equal(o["pos"], o["count"][ol])
+    kept = o["valid"].bool()[ol]                       # [T, K] by dispatch position
+    assert torch.equal(kept.sum(1).int(), o["pos"])   # the kept slots are a prefix
+    want = o["proj"][o["idx"].long()[ol]]              # [T, K, 12]
+    assert torch.equal(o["rec"][kept], want[kept])
 
 
 @pytest.mark.parametrize("name,G", [("c4", None), ("c3", None), ("c1_ref", None), ("c3", 1),
@@ -57,6 +76,16 @@ def check_equal(a, b, K):
 def test_geom_fwd_assign_bins_equals_two_calls(name, G):
     cfg, P, cam = config_inputs(name, G=G)
     print(f"[geom+bins] {name} G={cfg.G}", flush=True)
+    a, b = two_ways(cfg, P.cuda(), cam)
+    check_equal(a, b, cfg.K)
+
+
+@pytest.mark.parametrize("K", [256, 512])
+def test_geom_fwd_assign_bins_records_large_k(K):
+    # K > 128: the select places survivors by groups (heavy and light tiles)
+    cfg, P, cam = config_inputs("c4", G=100000)
+    cfg = dataclasses.replace(cfg, K=K)
+    print(f"[geom+bins] c4 K={K}", flush=True)
     a, b = two_ways(cfg, P.cuda(), cam)
     check_equal(a, b, cfg.K)
 

@@ -29,7 +29,9 @@
 //                       and light lists, and record per block how many tiles take each order
 //                       key (K - kept count) and each tile's rank among them.
 //   4. k_bin_select     one block per tile (below); it also writes the tile's slot of the
-//                       heaviest-first order, from those per-block key counts.
+//                       heaviest-first order, from those per-block key counts, and (when
+//                       asked) the slot records: each kept gaussian's proj record at the
+//                       tile's place in that order.
 // The result does not depend on the order atomics land in.
 
 #include <mutex>
@@ -512,7 +514,27 @@ struct SelectArgs {
   const int* key_hist;     // [K+1][ncls] per classification block tiles per order key
   const int* tile_pos;     // [T] rank among its classification block's tiles of its key
   int ncls;
+  const float* proj;       // [G][12] projection records (read when rec is set)
+  float* rec;              // [T][K][12] slot records by dispatch position (may be null)
+  int32_t* pos_count;      // [T] kept count by dispatch position (with rec)
 };
+
+// Slot records: the kept gaussian's 12-float projection record, copied to its slot at the
+// tile's place in the dispatch order (rec[position][slot]), so a splat block reads its slots as
+// one contiguous run instead of order -> idx -> proj.
+struct SlotRec {
+  float4 r0, r1, r2;
+};
+__device__ __forceinline__ SlotRec rec_load(const float* __restrict__ proj, int g) {
+  const float4* src = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+  return SlotRec{src[0], src[1], src[2]};
+}
+__device__ __forceinline__ void rec_store(float* __restrict__ rb, int slot, SlotRec r) {
+  float4* dst = reinterpret_cast<float4*>(rb + (int64_t)slot * 12);
+  dst[0] = r.r0;
+  dst[1] = r.r1;
+  dst[2] = r.r2;
+}
 
 // Slot of tile t (n candidates) in the heaviest-first order: tiles of smaller keys (more kept
 // slots), then this key's tiles of earlier classification blocks, then its rank in its block.
@@ -617,6 +639,9 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
   __builtin_amdgcn_wave_barrier();
   const int m = *fill;
   const int64_t base = static_cast<int64_t>(t) * a.K;
+  // the tile's place in the dispatch order (its key-table loads were issued before the walk)
+  const int slot = a.order ? os.end(a) : 0;
+  float* rb = a.rec ? a.rec + (int64_t)slot * a.K * 12 : nullptr;
   if (a.K <= 128) {
     // all pairs (cheaper than the groups' extra passes at this size)
     // the keys padded to a multiple of 16 with the largest key (never below a survivor), so the
@@ -630,27 +655,32 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
       // slots s0 + lane and s0 + 64 + lane share each key read
       const int sa = s0 + lane, sb = sa + 64;
       const unsigned long long ka = sa < m ? keys[sa] : 0ull, kb = sb < m ? keys[sb] : 0ull;
-      int ra = 0, rb = 0;
+      // the slot records are requested before the rank counts, which hide their round trip
+      SlotRec reca{}, recb{};
+      if (rb && sa < m) reca = rec_load(a.proj, static_cast<int32_t>(ka & 0xffffffffull));
+      if (rb && sb < m) recb = rec_load(a.proj, static_cast<int32_t>(kb & 0xffffffffull));
+      int ra = 0, rnb = 0;
       if (s0 < m) {
         for (int e = 0; e < m16 / 2; e += 4) {
           const ulonglong2 k0 = kp[e], k1 = kp[e + 1], k2 = kp[e + 2], k3 = kp[e + 3];
           ra += (k0.x < ka) + (k0.y < ka) + (k1.x < ka) + (k1.y < ka) + (k2.x < ka) + (k2.y < ka) +
                 (k3.x < ka) + (k3.y < ka);
-          rb += (k0.x < kb) + (k0.y < kb) + (k1.x < kb) + (k1.y < kb) + (k2.x < kb) + (k2.y < kb) +
-                (k3.x < kb) + (k3.y < kb);
+          rnb += (k0.x < kb) + (k0.y < kb) + (k1.x < kb) + (k1.y < kb) + (k2.x < kb) +
+                 (k2.y < kb) + (k3.x < kb) + (k3.y < kb);
         }
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         const int s = h ? sb : sa;
         const unsigned long long key = h ? kb : ka;
-        const int rank = h ? rb : ra;
+        const int rank = h ? rnb : ra;
         if (s < m) {
           const int g = static_cast<int32_t>(key & 0xffffffffull);
           a.idx[base + rank] = g;
           if (a.inv)
             a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
           a.valid[base + rank] = 1;
+          if (rb) rec_store(rb, rank, h ? recb : reca);
         } else if (s < a.K) {
           a.idx[base + s] = 0;
           a.valid[base + s] = 0;
@@ -687,6 +717,8 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
     for (int s = lane; s < a.K; s += 64) {
       if (s < m) {
         const unsigned long long key = keys[s];
+        SlotRec rec{};
+        if (rb) rec = rec_load(a.proj, static_cast<int32_t>(key & 0xffffffffull));
         const unsigned w = grp[key_group(key, satq, shift)];
         const int rank = rank_in_group(key, gat, static_cast<int>(w >> 20),
                                        static_cast<int>((w >> 10) & 1023u));
@@ -695,17 +727,16 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
         if (a.inv)
           a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
         a.valid[base + rank] = 1;
+        if (rb) rec_store(rb, rank, rec);
       } else {
         a.idx[base + s] = 0;
         a.valid[base + s] = 0;
       }
     }
   }
-  if (a.order) {
-    const int slot = os.end(a);
-    if (lane == 0) a.order[slot] = t;
-  }
   if (lane == 0) {
+    if (a.order) a.order[slot] = t;
+    if (rb) a.pos_count[slot] = m;
     if (a.count) a.count[t] = m;
     if (a.ncand) a.ncand[t] = m;
   }
@@ -732,7 +763,7 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
 template <int NT>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_bin_select(
     SelectArgs a, const int* __restrict__ lists, const int* __restrict__ nlist) {
-  extern __shared__ unsigned char s_dyn[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ TileCells tcs[NT / 64];
   __shared__ int s_wfill[NT / 64];
   const int T = a.ntx * a.nty;
@@ -764,6 +795,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   __shared__ int s_sat[9];      // saturated regular candidates per stencil index
   __shared__ int s_jstar[2];    // j*, rank inside cell j*'s tie set
   __shared__ unsigned s_grp[kGroups];  // survivors per group, then packed prefixes
+  __shared__ int s_oslot;              // the tile's place in the dispatch order
 
   const int t = t_heavy;
   const int tx = t % a.ntx, ty = t / a.ntx;
@@ -782,6 +814,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   const int satq = span - 1;
   // wave 0 takes the tile's order slot now; its loads overlap the candidate walks
   const int oslot = (a.order && threadIdx.x < 64) ? order_slot(a, t, n) : 0;
+  if (threadIdx.x == 0) s_oslot = oslot;  // read after the barriers below
 
   int qlim = span;  // above every survivor's qd2 bin
   if (n <= K) {
@@ -999,12 +1032,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   // Place the m survivors by rank (unique keys: rank = number of smaller survivors).
   const int m = min(s_fill, K);
   const int64_t base = static_cast<int64_t>(t) * K;
-  auto put = [&](int rank, unsigned long long key) {
+  float* rb = a.rec ? a.rec + (int64_t)s_oslot * K * 12 : nullptr;
+  auto put = [&](int rank, unsigned long long key, SlotRec rec) {
     const int g = static_cast<int32_t>(key & 0xffffffffull);
     a.idx[base + rank] = g;
     if (a.inv)
       a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
     a.valid[base + rank] = 1;
+    if (rb) rec_store(rb, rank, rec);
   };
   auto clear = [&](int s) {
     a.idx[base + s] = 0;
@@ -1022,6 +1057,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
     for (int s0 = 0; s0 < K; s0 += NT / 2) {
       const int s = s0 + (static_cast<int>(threadIdx.x) >> 1);
       const unsigned long long key = s < m ? s_keys[s] : 0ull;
+      // the slot record is requested before the rank count, which hides its round trip
+      SlotRec rec{};
+      if (rb && half == 0 && s < m)
+        rec = rec_load(a.proj, static_cast<int32_t>(key & 0xffffffffull));
       int rank = 0;
       if (s0 < m) {
 #pragma unroll 2  // 8 reads in flight; a deeper unroll spills at 64 registers
@@ -1033,7 +1072,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
       }
       rank += __shfl_xor(rank, 1);
       if (half == 0 && s < K) {
-        if (s < m) put(rank, key);
+        if (s < m) put(rank, key, rec);
         else clear(s);
       }
     }
@@ -1074,9 +1113,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
       const int s = static_cast<int>(threadIdx.x) + k * NT;
       if (s < m) {
         const unsigned long long key = s_keys[s];
+        SlotRec rec{};
+        if (rb) rec = rec_load(a.proj, static_cast<int32_t>(key & 0xffffffffull));
         const unsigned v = s_grp[group(key)];
         put(rank_in_group(key, s_tie, static_cast<int>(v >> 16), static_cast<int>(v & 0xffffu)),
-            key);
+            key, rec);
       } else if (s < K) {
         clear(s);
       }
@@ -1086,6 +1127,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
     if (a.count) a.count[t] = m;
     if (a.ncand) a.ncand[t] = n;
     if (a.order) a.order[oslot] = t;
+    if (rb) a.pos_count[oslot] = m;
   }
 }
 
@@ -1225,7 +1267,8 @@ static int bin_check(const float* mu2d, int mu_stride, const uint8_t* keep, int 
 static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int keep_stride,
                    int G, int H, int W, int S, int K, int span, int32_t* idx, uint8_t* valid,
                    int32_t* count, int32_t* ncand, int32_t* inv, int32_t* order,
-                   const BinWorkspace& ws, bool counted, hipStream_t stream) {
+                   const float* proj, float* rec, int32_t* pos_count, const BinWorkspace& ws,
+                   bool counted, hipStream_t stream) {
   const int ntx = W / S, nty = H / S, T = ntx * nty;
   const float Sf = static_cast<float>(S);
   const int NB = ws.NB, Tpad = ws.Tpad, nblk = ws.nblk;
@@ -1269,7 +1312,8 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
       sizeof(unsigned long long) * (2 * (size_t)kpow2 + 8 + kGroups / 2) * (kSelThreads / 64);
   const size_t lds = heavy_lds > light_lds ? heavy_lds : light_lds;
   SelectArgs sa{ws.recs, ws.far_g, ws.cell_start, ws.far_start, ntx, nty, Sf, span, K, kpow2,
-                gbits, idx, valid, count, ncand, inv, order, ws.key_hist, ws.tile_pos, ncls};
+                gbits, idx, valid, count, ncand, inv, order, ws.key_hist, ws.tile_pos, ncls,
+                proj, rec, pos_count};
   k_bin_select<kSelThreads><<<T, kSelThreads, lds, stream>>>(sa, ws.lists, ws.nlist);
   return launch_status();
 }
@@ -1319,7 +1363,7 @@ int tts_assign_bins(const float* mu2d, int mu_stride, const uint8_t* keep, int k
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
   return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
-                 ncand, inv, order, ws, false, stream);
+                 ncand, inv, order, nullptr, nullptr, nullptr, ws, false, stream);
 }
 
 int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* keep,
@@ -1336,7 +1380,7 @@ int tts_assign_bins_noalloc(const float* mu2d, int mu_stride, const uint8_t* kee
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(base), &ws);
   return bin_run(mu2d, mu_stride, keep, keep_stride, G, H, W, S, K, span, idx, valid, count,
-                 ncand, inv, order, ws, false, stream);
+                 ncand, inv, order, nullptr, nullptr, nullptr, ws, false, stream);
 }
 
 int tts_tile_order(const int32_t* count, int T, int K, int32_t* order, hipStream_t stream) {
@@ -1348,15 +1392,18 @@ int tts_tile_order(const int32_t* count, int T, int K, int32_t* order, hipStream
 
 // Geometry forward + binning of one view (tts_geom_fwd_ex, then tts_assign_bins on proj's
 // means and keep): with count blocks of 512 gaussians (G <= 131072) the count pass runs inside
-// the geometry launch (k_geom_fwd_count), otherwise the two run as their own launches.
+// the geometry launch (k_geom_fwd_count), otherwise the two run as their own launches.  With
+// slot_rec the select pass also writes the slot records and per-position counts.
 int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_degree,
                              const float* depth_bt, int G, const float* camera, float near_z,
                              float blur, float* proj, uint8_t* keep, int32_t* step_adv,
                              float beta1, float beta2, int H, int W, int S, int R, int K,
                              int span, int32_t* idx, uint8_t* valid, int32_t* count,
-                             int32_t* ncand, int32_t* inv, int32_t* order, void* workspace,
-                             size_t workspace_bytes, hipStream_t stream) {
+                             int32_t* ncand, int32_t* inv, int32_t* order, float* slot_rec,
+                             int32_t* pos_count, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream) {
   if (G < 0 || (G > 0 && (!params || !camera || !proj || !keep))) return TTS_EINVAL;
+  if (slot_rec && (!pos_count || !order)) return TTS_EINVAL;
   if (sh_degree < 0 || sh_degree > 3 || (sh_degree > 0 && !sh_rest)) return TTS_ESH;
   if (G >= (1 << 30)) return TTS_EG;
   const int rc = bin_check(proj, 12, keep, 1, G, H, W, S, R, K, span, idx, valid);
@@ -1375,7 +1422,7 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
                                         blur, proj, keep, step_adv, beta1, beta2, stream);
   if (e != TTS_OK) return e;
   return bin_run(proj, 12, keep, 1, G, H, W, S, K, span, idx, valid, count, ncand, inv, order,
-                 ws, fused, stream);
+                 proj, slot_rec, pos_count, ws, fused, stream);
 }
 
 }  // extern "C"

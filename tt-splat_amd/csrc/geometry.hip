@@ -584,7 +584,7 @@ __global__ __launch_bounds__(512) void k_geom_fwd_count(
     int2* __restrict__ cell_slot) {
   static_assert(CountFused::kBlock == CountSmall::kBlock && CountFused::kBlock == 2 * kGeoBlock,
                 "one count block = two geometry halves");
-  extern __shared__ float s_dyn[];
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
   float2* s_mu = reinterpret_cast<float2*>(s_dyn);                   // [512] means
   uint8_t* s_kv = reinterpret_cast<uint8_t*>(s_mu + 2 * kGeoBlock);  // [512] keep flags
   float* s_u = reinterpret_cast<float*>(s_kv + 2 * kGeoBlock);       // staging, then count

@@ -117,6 +117,33 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
   return base;
 }
 
+// The same from slot records (rec = slot_rec [T][K][12] in dispatch order, block b reads its
+// own K records and kept count): the kept slots are the prefix [0, pos_count[b]), so no
+// compaction.  Returns the kept count.
+__device__ __forceinline__ int load_slots_rec(const float* __restrict__ rec,
+                                              const int32_t* __restrict__ pos_count, int K,
+                                              float ox, float oy, float inv_k, SlotLDS sl,
+                                              bool* bad) {
+  const int nb = min(pos_count[blockIdx.x], K);
+  for (int s = threadIdx.x; s < K; s += 256) {
+    // read whether kept or not: the loads are in flight beside pos_count
+    const float4* r = reinterpret_cast<const float4*>(rec + ((int64_t)blockIdx.x * K + s) * 12);
+    const float4 r0 = r[0], r1 = r[1], r2 = r[2];
+    if (s < nb) {
+      float4 ta, tb, cl;
+      slot_from_rec(r0, r1, r2, ox, oy, inv_k, ta, tb, cl);
+      *bad = *bad || theta_poisons(ta, tb);
+      sl.ta[s] = ta;
+      sl.tb[s] = tb;
+      sl.cl[s] = cl;
+      sl.ge[s] = make_float4(r0.z, r0.w, r1.x, r0.x - ox);
+      sl.gid[s] = s;
+      sl.sid[s] = s;
+    }
+  }
+  return nb;
+}
+
 __device__ __forceinline__ float opf(float x) { return x; }
 __device__ __forceinline__ float opf(__bf16 x) { return (float)x; }
 
@@ -148,7 +175,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
     const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
     const float* __restrict__ bg, float* __restrict__ image, float* __restrict__ den_out) {
   constexpr int PPT = S * S / 256;  // pixels per thread
-  extern __shared__ unsigned char s_dyn[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   const SlotLDS sl = carve_slots(s_dyn, K);
   const int t = order ? order[blockIdx.x] : blockIdx.x;
@@ -318,19 +345,22 @@ __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const flo
   }
 }
 
-template <int S, bool FROM_PROJ, typename OT = float>
+// REC (with FROM_PROJ): proj is slot_rec [T][K][12] in dispatch order and pos_count[b] the
+// kept count of block b's tile (load_slots_rec).
+template <int S, bool FROM_PROJ, typename OT = float, bool REC = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_splat_bwd(
     const float* __restrict__ proj, const int32_t* __restrict__ idx,
     const uint8_t* __restrict__ valid, const OT* __restrict__ theta,
     const OT* __restrict__ col, const OT* __restrict__ oc,
-    const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
+    const int32_t* __restrict__ order, const int32_t* __restrict__ pos_count, int ntx, int W,
+    int K, float inv_k,
     const float* __restrict__ bg, const float* __restrict__ image,
     const float* __restrict__ den, const float* __restrict__ gimage, float* __restrict__ gslot,
     float* __restrict__ gtheta, float* __restrict__ gcol, float* __restrict__ goc,
     float* __restrict__ gwb) {
   constexpr int P = S * S;
   constexpr int PPT = P / 256;
-  extern __shared__ unsigned char s_dyn[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   __shared__ float s_ftmp[4];
   const SlotLDS sl = carve_slots(s_dyn, K);
@@ -355,7 +385,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   }
   int n;
   bool bad = false;  // a poisoned tile's den is NaN already (the forward wrote it)
-  if constexpr (FROM_PROJ) {
+  if constexpr (REC) {
+    n = load_slots_rec(proj, pos_count, K, (float)ox, (float)oy, inv_k, sl, &bad);
+  } else if constexpr (FROM_PROJ) {
     n = load_slots_proj(proj, idx, valid, t, K, (float)ox, (float)oy, inv_k, sl, s_tmp, &bad);
   } else {
     load_slots_theta(theta, col, oc, t, K, sl, &bad);
@@ -480,7 +512,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
     const uint8_t* __restrict__ valid, const int32_t* __restrict__ order, int ntx, int W, int K,
     float inv_k, const float* __restrict__ bg, float* __restrict__ image,
     float* __restrict__ den_out) {
-  extern __shared__ unsigned char s_dyn[];
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   const int kpad = (K + 31) & ~31;
   bf16x8* s_th = reinterpret_cast<bf16x8*>(s_dyn);  // [kpad][4]
@@ -601,21 +633,26 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
 // 256 pairs for A).  Slot s is staged at LDS entry s (zero when invalid: u = 0, w = 0) and the
 // walk runs to the highest valid slot, so bins whose valid slots form a prefix (tts_assign_bins)
 // are summed in slot order with no zero terms beyond the last group.
+// REC: the slots come from slot records (src = slot_rec [T][K][12] in dispatch order, block b
+// reads src[b], its kept count pos_count[b] and its tile order[b] in one round trip); otherwise
+// src = proj and the slots from idx / valid of tile order[b].
 inline size_t fwd_mf_lds(int K) {
   const int k4 = (K + 3) & ~3;
   return (size_t)k4 * 5 * sizeof(float4);
 }
+template <bool REC>
 __global__ __launch_bounds__(256) void k_splat_fwd_mf(
-    const float* __restrict__ proj, const int32_t* __restrict__ idx,
-    const uint8_t* __restrict__ valid, const int32_t* __restrict__ order, int ntx, int W, int K,
-    float inv_k, const float* __restrict__ bg, float* __restrict__ image,
-    float* __restrict__ den_out) {
-  extern __shared__ unsigned char s_dyn[];
+    const float* __restrict__ src, const int32_t* __restrict__ idx,
+    const uint8_t* __restrict__ valid, const int32_t* __restrict__ pos_count,
+    const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
+    const float* __restrict__ bg, float* __restrict__ image, float* __restrict__ den_out) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_hi[2][4];
   const int k4 = (K + 3) & ~3;
   float4* s_coef = reinterpret_cast<float4*>(s_dyn);  // [k4][4]: (p, q, r, 0) per depth k
   float4* s_col = s_coef + (size_t)k4 * 4;           // [k4]: col_o r, g, b, o_col
   const int t = order ? order[blockIdx.x] : blockIdx.x;
+  const int nb = REC ? min(pos_count[blockIdx.x], K) : 0;
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * 16, oy = ty * 16;
   const float oxf = (float)ox, oyf = (float)oy;
@@ -643,8 +680,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
       s_col[s] = z;
     }
   };
+  // g: the gaussian (from idx), or with REC the slot of this block's records
   auto gather = [&](int g, float4& r0, float4& r1, float4& r2) {
-    const float4* r = reinterpret_cast<const float4*>(proj + (int64_t)g * 12);
+    const int64_t row = REC ? (int64_t)blockIdx.x * K + g : (int64_t)g;
+    const float4* r = reinterpret_cast<const float4*>(src + row * 12);
     r0 = r[0];
     r1 = r[1];
     r2 = r[2];
@@ -653,13 +692,14 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   // each wave's 64 (slot order = LDS order, so the walk needs no compaction)
   const int s = threadIdx.x;
   int v, g;
-  {
+  if constexpr (REC) {
+    g = min(s, K - 1);
+    v = s < nb ? 1 : 0;
+  } else {
     const int64_t ts = (int64_t)t * K + min(s, K - 1);
     const uint8_t vb = valid[ts];
     g = idx[ts];
     v = (s < K && vb != 0) ? 1 : 0;
-  }
-  {
     const uint64_t m = __ballot(v);
     if (lane == 0) s_hi[0][wave] = m ? wave * 64 + 64 - __clzll((long long)m) : 0;
   }
@@ -668,11 +708,14 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   // arrive during that walk
   float4 r0, r1, r2;
   if (wave == 0) {
-    if (v) gather(g, r0, r1, r2);
+    // records are read whether kept or not (in flight beside pos_count; a slot past the count
+    // is staged as zero)
+    if (v || REC) gather(g, r0, r1, r2);
     stage(s, v, r0, r1, r2);
   }
   bool poisoned = __syncthreads_or(bad);
-  const int n0 = max(max(s_hi[0][0], s_hi[0][1]), max(s_hi[0][2], s_hi[0][3]));
+  const int n0 = REC ? min(nb, 256)
+                     : max(max(s_hi[0][0], s_hi[0][1]), max(s_hi[0][2], s_hi[0][3]));
   const bool more = n0 > 64 || k4 > 256;
   if (more && wave > 0 && v) gather(g, r0, r1, r2);
 
@@ -715,10 +758,16 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     int hi = 0;
     for (int s0 = 256; s0 < k4; s0 += 256) {
       const int s2 = s0 + threadIdx.x;
-      const int64_t ts = (int64_t)t * K + min(s2, K - 1);
-      const uint8_t vb = valid[ts];
-      const int g2 = idx[ts];
-      const int v2 = (s2 < K && vb != 0) ? 1 : 0;
+      int v2, g2;
+      if constexpr (REC) {
+        g2 = min(s2, K - 1);
+        v2 = s2 < nb ? 1 : 0;
+      } else {
+        const int64_t ts = (int64_t)t * K + min(s2, K - 1);
+        const uint8_t vb = valid[ts];
+        g2 = idx[ts];
+        v2 = (s2 < K && vb != 0) ? 1 : 0;
+      }
       float4 q0, q1, q2;
       if (v2) gather(g2, q0, q1, q2);
       stage(s2, v2, q0, q1, q2);
@@ -727,7 +776,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     }
     if (lane == 0) s_hi[1][wave] = hi;
     poisoned = __syncthreads_or(bad) || poisoned;
-    const int n = max(n0, max(max(s_hi[1][0], s_hi[1][1]), max(s_hi[1][2], s_hi[1][3])));
+    const int n = REC ? nb
+                      : max(n0, max(max(s_hi[1][0], s_hi[1][1]), max(s_hi[1][2], s_hi[1][3])));
     walk(16, (n + 3) >> 2);
   }
   const float wb = bg[0];
@@ -785,8 +835,8 @@ int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, cons
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16 && FROM_PROJ)
-    k_splat_fwd_mf<<<T, 256, fwd_mf_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K, inv_k,
-                                                       bg, image, den);
+    k_splat_fwd_mf<false><<<T, 256, fwd_mf_lds(K), stream>>>(proj, idx, valid, nullptr, order,
+                                                              ntx, W, K, inv_k, bg, image, den);
   else if (S == 16)
     k_splat_fwd<16, FROM_PROJ, OT><<<T, 256, fwd_lds(K), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
@@ -807,12 +857,12 @@ int launch_bwd(const float* proj, const int32_t* idx, const uint8_t* valid, cons
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16)
     k_splat_bwd<16, FROM_PROJ, OT><<<T, 256, bwd_lds(K, 16), stream>>>(
-        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
-        gtheta, gcol, goc, gwb);
+        proj, idx, valid, theta, col, oc, order, nullptr, ntx, W, K, inv_k, bg, image, den,
+        gimage, gslot, gtheta, gcol, goc, gwb);
   else
     k_splat_bwd<32, FROM_PROJ, OT><<<T, 256, bwd_lds(K, 32), stream>>>(
-        proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den, gimage, gslot,
-        gtheta, gcol, goc, gwb);
+        proj, idx, valid, theta, col, oc, order, nullptr, ntx, W, K, inv_k, bg, image, den,
+        gimage, gslot, gtheta, gcol, goc, gwb);
   return launch_status();
 }
 
@@ -881,6 +931,36 @@ int tts_splat_bwd(const float* proj, const int32_t* idx, const uint8_t* valid,
   if (!proj || !idx || !valid || !bg || !image || !den || !gimage || !gslot) return TTS_EINVAL;
   return launch_bwd<true, float>(proj, idx, valid, nullptr, nullptr, nullptr, order, H, W, S, K, k, bg,
                           image, den, gimage, gslot, nullptr, nullptr, nullptr, gwb, stream);
+}
+
+int tts_splat_fwd_rec(const float* slot_rec, const int32_t* pos_count, const int32_t* order,
+                      int H, int W, int S, int K, float k, const float* bg, float* image,
+                      float* den, hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (S != 16) return TTS_ETILE;
+  if (!slot_rec || !pos_count || !order || !bg || !image) return TTS_EINVAL;
+  const int ntx = W / S, T = (H / S) * ntx;
+  k_splat_fwd_mf<true><<<T, 256, fwd_mf_lds(K), stream>>>(
+      slot_rec, nullptr, nullptr, pos_count, order, ntx, W, K, (float)(1.0 / (double)k), bg,
+      image, den);
+  return launch_status();
+}
+
+int tts_splat_bwd_rec(const float* slot_rec, const int32_t* pos_count, const int32_t* order,
+                      int H, int W, int S, int K, float k, const float* bg, const float* image,
+                      const float* den, const float* gimage, float* gslot, float* gwb,
+                      hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (S != 16) return TTS_ETILE;
+  if (!slot_rec || !pos_count || !order || !bg || !image || !den || !gimage || !gslot)
+    return TTS_EINVAL;
+  const int ntx = W / S, T = (H / S) * ntx;
+  k_splat_bwd<16, true, float, true><<<T, 256, bwd_lds(K, 16), stream>>>(
+      slot_rec, nullptr, nullptr, nullptr, nullptr, nullptr, order, pos_count, ntx, W, K,
+      (float)(1.0 / (double)k), bg, image, den, gimage, gslot, nullptr, nullptr, nullptr, gwb);
+  return launch_status();
 }
 
 int tts_splat_bwd_theta(const float* theta, const float* col, const float* oc, int H, int W,

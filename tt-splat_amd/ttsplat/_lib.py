@@ -37,6 +37,10 @@ SIGNATURES = {
                                      _vp, _vp]),
     "tts_splat_bwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tts_splat_fwd_rec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                   _vp, _vp, _vp, _vp]),
+    "tts_splat_bwd_rec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_splat_fwd_theta_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
                                           _vp, _vp, _vp]),
     "tts_splat_bwd_theta_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
@@ -64,7 +68,7 @@ SIGNATURES = {
     "tts_geom_fwd_assign_bins": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _vp, _c_float, _c_float,
                                           _vp, _vp, _vp, _c_float, _c_float, _c_int, _c_int,
                                           _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
-                                          _vp, _vp, _vp, _c_size, _vp]),
+                                          _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
     "tts_geom_bwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
                                  _vp, _vp, _vp, _vp, _vp]),
     "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_float,

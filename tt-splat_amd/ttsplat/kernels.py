@@ -168,10 +168,13 @@ def assign_bins(mu2d, keep, H, W, S=16, K=128, span=2048, R=1, workspace=None, i
 def geom_fwd_assign_bins(params, camera, H, W, S=16, K=128, span=2048, R=1, near=NEAR,
                          blur=BLUR, proj=None, keep=None, sh_rest=None, sh_degree=0,
                          depth_bt=None, advance=None, b1=None, b2=None, workspace=None, idx=None,
-                         valid=None, count=None, ncand=None, inv=None, order=None):
+                         valid=None, count=None, ncand=None, inv=None, order=None,
+                         slot_rec=None, pos_count=None):
     """geom_fwd then assign_bins on proj's means and keep, as one call (for G <= 131072 the
     binning's count pass runs inside the geometry launch).  Returns (proj, keep, idx, valid,
-    count, ncand); inv and order are written when buffers are passed."""
+    count, ncand); inv and order are written when buffers are passed, and with order the slot
+    records slot_rec [T,K,12] (proj[idx] of every kept slot, tiles in dispatch order) and
+    pos_count [T] (their kept counts) when those are passed."""
     G = params.shape[0]
     dev = params.device
     require(params, "params", F32, (G, 14))
@@ -199,12 +202,17 @@ def geom_fwd_assign_bins(params, camera, H, W, S=16, K=128, span=2048, R=1, near
         require(inv, "inv", I32, (G, 9), dev)
     if order is not None:
         require(order, "order", I32, (T,), dev)
+    if (slot_rec is None) != (pos_count is None) or (slot_rec is not None and order is None):
+        raise ValueError("slot_rec and pos_count go together, and need order")
+    if slot_rec is not None:
+        _aligned16(require(slot_rec, "slot_rec", F32, (T, K, 12), dev), "slot_rec")
+        require(pos_count, "pos_count", I32, (T,), dev)
     workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
     call("tts_geom_fwd_assign_bins", ptr(params), ptr(sh_rest), int(sh_degree), ptr(depth_bt),
          G, ptr(camera), near, blur, ptr(proj), ptr(keep), ptr(advance),
          BETA1 if b1 is None else b1, BETA2 if b2 is None else b2, H, W, S, R, K, span,
-         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(order), ptr(workspace),
-         workspace.numel(), stream())
+         ptr(idx), ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(order), ptr(slot_rec),
+         ptr(pos_count), ptr(workspace), workspace.numel(), stream())
     return proj, keep, idx, valid, count, ncand
 
 
@@ -262,6 +270,33 @@ def splat_fwd(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None
     return image, den
 
 
+def _rec_check(slot_rec, pos_count, order, H, W, S, dev):
+    if S != 16 or H % S or W % S:
+        raise ValueError(f"the slot-record splat kernels take 16x16 tiles dividing {H}x{W}")
+    T = (H // S) * (W // S)
+    if slot_rec.dim() != 3 or slot_rec.shape[0] != T or slot_rec.shape[2] != 12:
+        raise ValueError(f"slot_rec must be [T={T},K,12], got {tuple(slot_rec.shape)}")
+    K = slot_rec.shape[1]
+    _aligned16(require(slot_rec, "slot_rec", F32, (T, K, 12), dev), "slot_rec")
+    require(pos_count, "pos_count", I32, (T,), dev)
+    require(order, "order", I32, (T,), dev)
+    return T, K
+
+
+def splat_fwd_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=None):
+    """splat_fwd on the slot records of geom_fwd_assign_bins (S = 16): the same image and den."""
+    dev = slot_rec.device
+    T, K = _rec_check(slot_rec, pos_count, order, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    call("tts_splat_fwd_rec", ptr(slot_rec), ptr(pos_count), ptr(order), H, W, S, K, float(k),
+         ptr(bg), ptr(image), ptr(den), stream())
+    return image, den
+
+
 def splat_fwd_mx(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None, bf16=False):
     """Matrix-core splat forward (S = 16): fp32-level accuracy, or the bf16 render variant."""
     dev = proj.device
@@ -297,6 +332,24 @@ def splat_bwd(proj, idx, valid, bg, H, W, S, k, image, den, gimage, gslot=None, 
     if order is not None:
         require(order, "order", I32, (T,), dev)
     call("tts_splat_bwd", ptr(proj), ptr(idx), ptr(valid), ptr(order), H, W, S, K, float(k),
+         ptr(bg), ptr(image), ptr(den), ptr(gimage), ptr(gslot), ptr(gwb), stream())
+    return gslot
+
+
+def splat_bwd_rec(slot_rec, pos_count, order, bg, H, W, S, k, image, den, gimage, gslot=None,
+                  gwb=None):
+    """splat_bwd on the slot records of geom_fwd_assign_bins (S = 16): the same gslot."""
+    dev = slot_rec.device
+    T, K = _rec_check(slot_rec, pos_count, order, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    require(gimage, "gimage", F32, (H, W, 3), dev)
+    gslot = torch.zeros(T, K, 9, device=dev, dtype=F32) if gslot is None else gslot
+    require(gslot, "gslot", F32, (T, K, 9), dev)
+    if gwb is not None:
+        require(gwb, "gwb", F32, (T,), dev)
+    call("tts_splat_bwd_rec", ptr(slot_rec), ptr(pos_count), ptr(order), H, W, S, K, float(k),
          ptr(bg), ptr(image), ptr(den), ptr(gimage), ptr(gslot), ptr(gwb), stream())
     return gslot
 

@@ -154,6 +154,13 @@ class TrainStep:
         self.ncand = torch.empty(T, device=dev, dtype=I32)
         self.order = torch.empty(T, device=dev, dtype=I32)
         self.inv = torch.empty(G, 9, device=dev, dtype=I32)
+        # fp32 16x16-tile steps that rebin: the binning also writes the slot records (each kept
+        # slot's projection record, tiles in dispatch order) and the splat kernels read those
+        # instead of order -> idx -> proj; steps that reuse older bins read proj itself
+        self.use_rec = self.S == 16 and self.dtype != "bf16"
+        self.slot_rec = (torch.empty(T, K, 12, device=dev, dtype=F32) if self.use_rec
+                         else None)
+        self.pos_count = torch.empty(T, device=dev, dtype=I32) if self.use_rec else None
         self.gslot = torch.zeros(T, K, 9, device=dev, dtype=F32)
         self.image = torch.empty(H, W, 3, device=dev, dtype=F32)
         self.den = torch.empty(H, W, device=dev, dtype=F32)
@@ -195,7 +202,8 @@ class TrainStep:
                                          depth_bt=self.dw, advance=adv,
                                          workspace=self.bin_ws, idx=self.idx, valid=self.valid,
                                          count=self.count, ncand=self.ncand, inv=self.inv,
-                                         order=self.order)
+                                         order=self.order, slot_rec=self.slot_rec,
+                                         pos_count=self.pos_count)
         else:
             kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep,
                              sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
@@ -203,6 +211,9 @@ class TrainStep:
         if self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
+        elif rebin and self.use_rec:
+            kernels.splat_fwd_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
+                                  self.W, self.S, self.k, self.image, self.den)
         else:
             kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                               self.k, self.image, self.den, self.order)
@@ -218,9 +229,14 @@ class TrainStep:
         self.forward(ci, advance, rebin)
         kernels.loss_grad_stats(self.image, self.targets[ci], self.target_stats[ci], self.lam,
                                 self.gimage, self.partials)
-        kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
-                          self.k, self.image, self.den, self.gimage, self.gslot,
-                          order=self.order)
+        if rebin and self.use_rec:
+            kernels.splat_bwd_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
+                                  self.W, self.S, self.k, self.image, self.den, self.gimage,
+                                  self.gslot)
+        else:
+            kernels.splat_bwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
+                              self.k, self.image, self.den, self.gimage, self.gslot,
+                              order=self.order)
 
     def enqueue(self, i=0, rebin=True):
         """Enqueue training step i (camera i, or batch i) on the current stream; rebin=False
