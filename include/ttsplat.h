@@ -185,6 +185,14 @@ int tts_splat_fwd_rec(const float* slot_rec, const int32_t* pos_count, const int
                       int H, int W, int S, int K, float k, const float* bg, float* image,
                       float* den, hipStream_t stream);
 
+/* tts_splat_fwd_mx on the slot records (S = 16; bf16 as there): the same image and den as
+ * tts_splat_fwd_mx on those bins in that order, without its compaction scan and with one read
+ * of contiguous records per tile. */
+int tts_splat_fwd_mx_rec(const float* slot_rec, const int32_t* pos_count,
+                         const int32_t* order, int H, int W, int S, int K, float k,
+                         const float* bg, float* image, float* den, int bf16,
+                         hipStream_t stream);
+
 /* tts_splat_bwd (S = 16) on the slot records: the same gslot (at slot t*K + s of tile
  * t = order[p]) and gwb.  Replaces WSRPolySplatHot.backward (spike/backward.py:42-58) and
  * render_bwd + theta_bwd (tools/resident_traced.py:60-88) on the gathered operands. */

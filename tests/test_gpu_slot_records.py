@@ -1,8 +1,8 @@
-"""Splat forward and backward on slot records (tts_splat_fwd_rec / tts_splat_bwd_rec, the
-records written by tts_geom_fwd_assign_bins) against the same kernels on proj, idx and valid in
-the same tile order: image, den, per-slot gradients and per-tile dL/dw_b equal bit for bit,
-including slot budgets past 256 (the forward's second staging pass) and a tile poisoned by a NaN
-record."""
+"""Splat forward and backward on slot records (tts_splat_fwd_rec, tts_splat_fwd_mx_rec,
+tts_splat_bwd_rec; the records written by tts_geom_fwd_assign_bins) against the same kernels on
+proj, idx and valid in the same tile order: image, den, per-slot gradients and per-tile dL/dw_b
+equal bit for bit, including slot budgets past 256 (the forwards' second staging pass) and a
+tile poisoned by a NaN record."""
 import pytest
 import torch
 
@@ -56,6 +56,19 @@ def test_splat_on_records_equals_splat_on_bins(name, K):
     assert torch.equal(img, img2) and torch.equal(den, den2)
     assert torch.equal(g1[valid], g2[valid])
     assert torch.equal(w1, w2)
+
+
+@pytest.mark.parametrize("name,K,bf16", [("c1_ref", 128, True), ("c3", 128, True),
+                                         ("c4", 128, False), ("c4", 300, True)])
+def test_matrix_core_forward_on_records(name, K, bf16):
+    cfg, K, T, proj, idx, valid, order, rec, pos, bg = binned(name, K)
+    print(f"[rec mx] {name} K={K} bf16={bf16}", flush=True)
+    img, den = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k,
+                                    order=order, bf16=bf16)
+    img2, den2 = kernels.splat_fwd_mx_rec(rec, pos, order, bg, cfg.H, cfg.W, cfg.S, cfg.k,
+                                          bf16=bf16)
+    torch.cuda.synchronize()
+    assert torch.equal(img, img2) and torch.equal(den, den2)
 
 
 def test_splat_on_records_nan_tile():

@@ -506,12 +506,14 @@ inline size_t fwd_mx_lds(int K) {
   return (size_t)kpad * 64 + (size_t)(kpad / 32) * 512;
 }
 
-template <bool SPLIT_W>
+// REC: the slots come from slot records (src = slot_rec, block b reads src[b] and pos_count[b];
+// the kept slots are the prefix, no compaction); otherwise src = proj with idx / valid.
+template <bool SPLIT_W, bool REC>
 __global__ __launch_bounds__(256) void k_splat_fwd_mx(
-    const float* __restrict__ proj, const int32_t* __restrict__ idx,
-    const uint8_t* __restrict__ valid, const int32_t* __restrict__ order, int ntx, int W, int K,
-    float inv_k, const float* __restrict__ bg, float* __restrict__ image,
-    float* __restrict__ den_out) {
+    const float* __restrict__ src, const int32_t* __restrict__ idx,
+    const uint8_t* __restrict__ valid, const int32_t* __restrict__ pos_count,
+    const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
+    const float* __restrict__ bg, float* __restrict__ image, float* __restrict__ den_out) {
   extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_tmp[4];
   const int kpad = (K + 31) & ~31;
@@ -522,16 +524,38 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
   const int ox = tx * 16, oy = ty * 16;
   const float oxf = (float)ox, oyf = (float)oy;
   // compact the valid slots, build theta in fp32 and store its split row and the colours
+  const int nb = REC ? min(pos_count[blockIdx.x], K) : 0;
   int n = 0;
   bool bad = false;
   for (int s0 = 0; s0 < K; s0 += 256) {
     const int s = s0 + threadIdx.x;
-    const int v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
-    int total;
-    const int pos = n + block_excl_scan256(v, s_tmp, &total);
+    int v, pos, total;
+    float4 r0, r1, r2;
+    if constexpr (REC) {
+      // records read whether kept or not (in flight beside pos_count)
+      if (s < K) {
+        const float4* r = reinterpret_cast<const float4*>(src + ((int64_t)blockIdx.x * K + s) * 12);
+        r0 = r[0];
+        r1 = r[1];
+        r2 = r[2];
+      }
+      v = s < nb ? 1 : 0;
+      pos = s;
+      total = max(min(nb - s0, 256), 0);
+    } else {
+      v = (s < K) ? (valid[(int64_t)t * K + s] != 0) : 0;
+      pos = n + block_excl_scan256(v, s_tmp, &total);
+      if (v) {
+        const float4* r =
+            reinterpret_cast<const float4*>(src + (int64_t)idx[(int64_t)t * K + s] * 12);
+        r0 = r[0];
+        r1 = r[1];
+        r2 = r[2];
+      }
+    }
     if (v) {
       float4 ta, tb, cl;
-      build_slot(proj, idx[(int64_t)t * K + s], oxf, oyf, inv_k, ta, tb, cl);
+      slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
       bad = bad || theta_poisons(ta, tb);
       const float th[6] = {ta.x, ta.y, ta.z, ta.w, tb.x, tb.y};
       theta_row(th, s_th + (size_t)pos * 4);
@@ -904,11 +928,11 @@ int tts_splat_fwd_mx(const float* proj, const int32_t* idx, const uint8_t* valid
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (bf16)
-    k_splat_fwd_mx<false><<<T, 256, fwd_mx_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K,
-                                                            inv_k, bg, image, den);
+    k_splat_fwd_mx<false, false><<<T, 256, fwd_mx_lds(K), stream>>>(
+        proj, idx, valid, nullptr, order, ntx, W, K, inv_k, bg, image, den);
   else
-    k_splat_fwd_mx<true><<<T, 256, fwd_mx_lds(K), stream>>>(proj, idx, valid, order, ntx, W, K,
-                                                           inv_k, bg, image, den);
+    k_splat_fwd_mx<true, false><<<T, 256, fwd_mx_lds(K), stream>>>(
+        proj, idx, valid, nullptr, order, ntx, W, K, inv_k, bg, image, den);
   return launch_status();
 }
 
@@ -944,6 +968,25 @@ int tts_splat_fwd_rec(const float* slot_rec, const int32_t* pos_count, const int
   k_splat_fwd_mf<true><<<T, 256, fwd_mf_lds(K), stream>>>(
       slot_rec, nullptr, nullptr, pos_count, order, ntx, W, K, (float)(1.0 / (double)k), bg,
       image, den);
+  return launch_status();
+}
+
+int tts_splat_fwd_mx_rec(const float* slot_rec, const int32_t* pos_count,
+                         const int32_t* order, int H, int W, int S, int K, float k,
+                         const float* bg, float* image, float* den, int bf16,
+                         hipStream_t stream) {
+  const int e = check_tile(H, W, S, K);
+  if (e) return e;
+  if (S != 16) return TTS_ETILE;
+  if (!slot_rec || !pos_count || !order || !bg || !image) return TTS_EINVAL;
+  const int ntx = W / S, T = (H / S) * ntx;
+  const float inv_k = (float)(1.0 / (double)k);
+  if (bf16)
+    k_splat_fwd_mx<false, true><<<T, 256, fwd_mx_lds(K), stream>>>(
+        slot_rec, nullptr, nullptr, pos_count, order, ntx, W, K, inv_k, bg, image, den);
+  else
+    k_splat_fwd_mx<true, true><<<T, 256, fwd_mx_lds(K), stream>>>(
+        slot_rec, nullptr, nullptr, pos_count, order, ntx, W, K, inv_k, bg, image, den);
   return launch_status();
 }
 

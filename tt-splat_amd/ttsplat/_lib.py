@@ -39,6 +39,8 @@ SIGNATURES = {
                                _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_splat_fwd_rec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                    _vp, _vp, _vp, _vp]),
+    "tts_splat_fwd_mx_rec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
+                                      _vp, _vp, _vp, _c_int, _vp]),
     "tts_splat_bwd_rec": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tts_splat_fwd_theta_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,

@@ -297,6 +297,21 @@ def splat_fwd_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=No
     return image, den
 
 
+def splat_fwd_mx_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=None,
+                     bf16=False):
+    """splat_fwd_mx on the slot records of geom_fwd_assign_bins: the same image and den."""
+    dev = slot_rec.device
+    T, K = _rec_check(slot_rec, pos_count, order, H, W, S, dev)
+    require(bg, "bg", F32, (4,), dev)
+    image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
+    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+    require(image, "image", F32, (H, W, 3), dev)
+    require(den, "den", F32, (H, W), dev)
+    call("tts_splat_fwd_mx_rec", ptr(slot_rec), ptr(pos_count), ptr(order), H, W, S, K,
+         float(k), ptr(bg), ptr(image), ptr(den), int(bool(bf16)), stream())
+    return image, den
+
+
 def splat_fwd_mx(proj, idx, valid, bg, H, W, S, k, image=None, den=None, order=None, bf16=False):
     """Matrix-core splat forward (S = 16): fp32-level accuracy, or the bf16 render variant."""
     dev = proj.device

@@ -154,10 +154,10 @@ class TrainStep:
         self.ncand = torch.empty(T, device=dev, dtype=I32)
         self.order = torch.empty(T, device=dev, dtype=I32)
         self.inv = torch.empty(G, 9, device=dev, dtype=I32)
-        # fp32 16x16-tile steps that rebin: the binning also writes the slot records (each kept
+        # 16x16-tile steps that rebin: the binning also writes the slot records (each kept
         # slot's projection record, tiles in dispatch order) and the splat kernels read those
         # instead of order -> idx -> proj; steps that reuse older bins read proj itself
-        self.use_rec = self.S == 16 and self.dtype != "bf16"
+        self.use_rec = self.S == 16
         self.slot_rec = (torch.empty(T, K, 12, device=dev, dtype=F32) if self.use_rec
                          else None)
         self.pos_count = torch.empty(T, device=dev, dtype=I32) if self.use_rec else None
@@ -208,7 +208,10 @@ class TrainStep:
             kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep,
                              sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
                              advance=adv)
-        if self.dtype == "bf16":
+        if self.dtype == "bf16" and rebin and self.use_rec:
+            kernels.splat_fwd_mx_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
+                                     self.W, self.S, self.k, self.image, self.den, bf16=True)
+        elif self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
         elif rebin and self.use_rec:
