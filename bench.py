@@ -191,6 +191,29 @@ def graph_time(fn, reps, torch, per_graph=20):
     return us
 
 
+def step_splat_jobs(ts, kernels, gimage):
+    """The fused splat forward and backward as the training step launches them after a rebin:
+    on the slot records for 16x16 tiles, else on proj / idx / valid."""
+    if ts.use_rec:
+        fwd = ((lambda: kernels.splat_fwd_mx_rec(ts.slot_rec, ts.pos_count, ts.order, ts.bg,
+                                                 ts.H, ts.W, ts.S, ts.k, ts.image, ts.den,
+                                                 bf16=True))
+               if ts.dtype == "bf16" else
+               (lambda: kernels.splat_fwd_rec(ts.slot_rec, ts.pos_count, ts.order, ts.bg, ts.H,
+                                              ts.W, ts.S, ts.k, ts.image, ts.den)))
+        bwd = lambda: kernels.splat_bwd_rec(ts.slot_rec, ts.pos_count, ts.order, ts.bg, ts.H,
+                                            ts.W, ts.S, ts.k, ts.image, ts.den, gimage, ts.gslot)
+    else:
+        fwd = ((lambda: kernels.splat_fwd_mx(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S,
+                                             ts.k, ts.image, ts.den, ts.order, bf16=True))
+               if ts.dtype == "bf16" else
+               (lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S,
+                                          ts.k, ts.image, ts.den, ts.order)))
+        bwd = lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S,
+                                        ts.k, ts.image, ts.den, gimage, ts.gslot, order=ts.order)
+    return fwd, bwd
+
+
 def time_splat_per_camera(ts, reps, torch, kernels):
     """Fused splat forward / backward of every camera: HIP-event microseconds per launch and the
     (pixel, valid slot) pairs of that camera's bins (the state is the current one; the
@@ -202,12 +225,8 @@ def time_splat_per_camera(ts, reps, torch, kernels):
         torch.cuda.synchronize()
         pairs = int(ts.count.long().sum()) * ts.S * ts.S
         rec = dict(camera=ci, pairs=pairs)
-        jobs = {"splat_fwd": lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H,
-                                                       ts.W, ts.S, ts.k, ts.image, ts.den,
-                                                       ts.order),
-                "splat_bwd": lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H,
-                                                       ts.W, ts.S, ts.k, ts.image, ts.den, gim,
-                                                       ts.gslot, order=ts.order)}
+        fwd, bwd = step_splat_jobs(ts, kernels, gim)
+        jobs = {"splat_fwd": fwd, "splat_bwd": bwd}
         for name, fn in jobs.items():
             rec[name + "_us"] = graph_time(fn, reps, torch)
         rows.append(rec)
@@ -226,28 +245,22 @@ def time_kernels(ts, reps, torch, kernels):
     sh = dict(sh_rest=ts.sh, sh_degree=ts.sh_degree)
     shs = [ts.sh, ts.sh_m, ts.sh_v] if ts.sh is not None else []
     saved_sh = [t.clone() for t in shs]
+    fwd, bwd = step_splat_jobs(ts, kernels, ts.gimage)
     jobs = {
         "geom_fwd": lambda: kernels.geom_fwd(ts.P, cam, proj=ts.proj, keep=ts.keep, **sh),
         "binning": lambda: kernels.assign_bins(ts.proj[:, 0:2], ts.keep, ts.H, ts.W, ts.S, ts.K,
                                                ts.span, 1, ts.bin_ws, ts.idx, ts.valid,
                                                ts.count, ts.ncand, ts.inv, ts.order),
         # what the step launches: the geometry forward carrying the binning's count pass, then
-        # the other binning kernels
+        # the other binning kernels (writing the slot records the splat kernels then read)
         "geom_fwd_binning": lambda: kernels.geom_fwd_assign_bins(
             ts.P, cam, ts.H, ts.W, ts.S, ts.K, ts.span, proj=ts.proj, keep=ts.keep,
             workspace=ts.bin_ws, idx=ts.idx, valid=ts.valid, count=ts.count, ncand=ts.ncand,
-            inv=ts.inv, order=ts.order, **sh),
-        "splat_fwd": (lambda: kernels.splat_fwd_mx(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
-                                                   ts.S, ts.k, ts.image, ts.den, ts.order,
-                                                   bf16=True))
-        if ts.dtype == "bf16" else
-        (lambda: kernels.splat_fwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W, ts.S, ts.k,
-                                   ts.image, ts.den, ts.order)),
+            inv=ts.inv, order=ts.order, slot_rec=ts.slot_rec, pos_count=ts.pos_count, **sh),
+        "splat_fwd": fwd,
         "loss_grad": lambda: kernels.loss_grad_stats(ts.image, ts.targets[0], ts.target_stats[0],
                                                      ts.lam, ts.gimage, ts.partials),
-        "splat_bwd": lambda: kernels.splat_bwd(ts.proj, ts.idx, ts.valid, ts.bg, ts.H, ts.W,
-                                               ts.S, ts.k, ts.image, ts.den, ts.gimage,
-                                               ts.gslot, order=ts.order),
+        "splat_bwd": bwd,
         "geom_bwd_adam": lambda: kernels.geom_bwd_adam(ts.P, cam, ts.gslot, ts.inv, ts.m, ts.v,
                                                        ts.lr, ts.step_block, sh_m=ts.sh_m,
                                                        sh_v=ts.sh_v, lr_sh=ts.lr_sh, **sh),
