@@ -5,8 +5,9 @@
 Headline (`value`): training iterations per second at G=100k (clustered), 1264x832, K=128,
 8 orbit cameras round-robin (one camera per step), fp32: each step is geometry fwd, binning,
 fused splat fwd, L1+SSIM loss gradient, fused splat bwd (+theta bwd, per-slot gradients),
-slot gather + geometry bwd + Adam, replayed as one HIP graph per camera.  Inputs are resident
-on the GPU before the timed region; the timed region is exactly K steps between two
+slot gather + geometry bwd + Adam, captured as HIP graphs of 8 consecutive steps (one per
+starting camera; a remainder of K mod 8 steps replays one-step graphs).  Inputs are resident on
+the GPU before the timed region; the timed region is exactly K steps between two
 synchronisations.
 
 Also reported: forward fps (geometry + binning + splat, graph replay) for the same scene, the
@@ -107,15 +108,13 @@ def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0, mcmc=None):
     return ts
 
 
-def time_train(ts, steps, warmup, torch):
+def time_train(ts, steps, warmup, torch, run_len=8):
     ncam = ts.n_steps
-    ts.capture()
-    for i in range(warmup):
-        ts.step(i % ncam)
+    ts.capture(run_len=run_len)
+    ts.run(0, warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        ts.step((warmup + i) % ncam)
+    ts.run(warmup % ncam, steps)     # exactly `steps` steps, in graphs of ts.run_len steps
     torch.cuda.synchronize()
     return time.perf_counter() - t0
 
@@ -364,7 +363,7 @@ def run_c5(args, torch, scenes, kernels, TrainStep):
     cfg = scenes.CONFIGS["c5"]
     ts = build_step(cfg, torch, TrainStep, batch=len(cfg.cameras()))
     nb = max(1, args.c5_batches)
-    t_batch = time_train(ts, nb, 1, torch) / nb
+    t_batch = time_train(ts, nb, 1, torch, run_len=1) / nb   # one graph per 64-view batch
     # forward only, all 64 views, one graph
     for ci in range(len(ts.cams)):
         ts.forward(ci)
@@ -558,8 +557,7 @@ def small_configs(torch, scenes, TrainStep):
     torch.cuda.synchronize()
     loss0 = float(ts.loss())
     t0 = time.perf_counter()
-    for _ in range(2999):
-        ts.step(0)
+    ts.run(0, 2999)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     out.update(c2_train_its=2999 / dt, c2_iterations=3000, c2_seconds_3000=dt * 3000 / 2999,

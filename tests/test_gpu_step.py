@@ -220,3 +220,28 @@ def test_bin_every_reuses_bins_between_rebins():
     assert rel_l2(graph.P, eager.P) <= 1e-3
     with pytest.raises(ValueError):
         TrainStep(P, [cam, cam], [tgt, tgt], K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5, batch=2)
+
+
+@pytest.mark.parametrize("bin_every", [1, 2])
+def test_run_graphs_match_single_steps(bin_every):
+    """run(i, n) (graphs of run_len consecutive steps, then one-step graphs for the remainder)
+    leaves the same state, bit for bit, as n step() calls from step i; with bin_every > 1 it
+    falls back to step()."""
+    from ttsplat import scenes
+    cfg, P, _ = config_inputs("c1_ref")
+    cams = scenes.Config(**{**cfg.__dict__, "n_cams": 3}).cameras()
+    tgts = [target_for(cfg, c) for c in cams]
+    runs = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
+    runs.capture(run_len=4)
+    assert bool(runs.run_graphs) == (bin_every == 1)
+    single = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
+    single.capture(run_len=1)
+    runs.run(1, 11)                        # two runs of 4, then 3 single steps
+    for i in range(11):
+        single.step((1 + i) % 3)
+    torch.cuda.synchronize()
+    assert runs.steps_done == single.steps_done == 11
+    for a, b in ((runs.P, single.P), (runs.m, single.m), (runs.v, single.v),
+                 (runs.step_block, single.step_block)):
+        assert torch.equal(a, b)
+    assert float(runs.loss()) == float(single.loss())

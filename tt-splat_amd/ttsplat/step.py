@@ -66,7 +66,9 @@ class TrainStep:
     tools/resident_traced.py:103,683): step() rebins only on steps whose running count is a
     multiple of N (and on the step after an MCMC relocation); the other steps run geometry,
     splat, loss, backward and Adam on the bins last computed -- one bin table for all cameras,
-    as in that trainer.  Each camera gets a graph with and one without the binning kernels."""
+    as in that trainer.  Each camera gets a graph with and one without the binning kernels.
+    run(i, n) is n step() calls from step i on; with bin_every = 1 and no relocation it replays
+    graphs that each hold run_len consecutive steps (one graph launch per run_len steps)."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
@@ -183,6 +185,8 @@ class TrainStep:
             raise ValueError("bin_every > 1 reuses one bin table across steps: batch must be 1")
         self._force_rebin = False
         self.graphs = {}
+        self.run_graphs = {}
+        self.run_len = 1
 
     @property
     def color_rest(self):
@@ -287,9 +291,11 @@ class TrainStep:
                          mc["seed"], self.reloc_ws, self.moved, self.sh, self.sh_m, self.sh_v)
         self.relocations += self.moved
 
-    def capture(self, cams=None):
+    def capture(self, cams=None, run_len=8):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
-        kernel's code object is resident) and its effect on the state is rolled back."""
+        kernel's code object is resident) and its effect on the state is rolled back.  With
+        bin_every = 1, no relocation and all cameras, run_len > 1 also captures, for every
+        starting step, one graph of run_len consecutive steps (used by run())."""
         cams = range(self.n_steps) if cams is None else cams
         live = [self.P, self.m, self.v, self.step_block]
         if self.sh is not None:
@@ -323,7 +329,29 @@ class TrainStep:
             with torch.cuda.graph(g):
                 self.enqueue_relocate()
             self.reloc_graph = g
+        self.run_graphs, self.run_len = {}, 1
+        if (run_len > 1 and self.bin_every == 1 and not self.mc["relocate_every"]
+                and list(cams) == list(range(self.n_steps))):
+            for c in cams:
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for j in range(run_len):
+                        self.enqueue((c + j) % self.n_steps, True)
+                self.run_graphs[c] = g
+            self.run_len = run_len
         torch.cuda.synchronize(self.dev)
+
+    def run(self, ci=0, n=1):
+        """n training steps: step ci, ci + 1, ... (mod n_steps), as n step() calls would run
+        them; whole runs of run_len steps replay one captured graph each."""
+        i = 0
+        if self.run_graphs:
+            while n - i >= self.run_len:
+                self.run_graphs[(ci + i) % self.n_steps].replay()
+                self._it += self.run_len
+                i += self.run_len
+        for j in range(i, n):
+            self.step((ci + j) % self.n_steps)
 
     def step(self, ci=0):
         """Training step ci: camera ci, or batch ci (graph replay when captured, else eager).
