@@ -10,11 +10,11 @@ starting camera; a remainder of K mod 8 steps replays one-step graphs).  Inputs 
 the GPU before the timed region; the timed region is exactly K steps between two
 synchronisations.
 
-Also reported: forward fps (geometry + binning + splat, graph replay) for the same scene, the
-G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from HIP events on
-the launch stream, the roofline of the dominant kernel, and the CPU oracle (PyTorch-CPU
-restatement of the reference path) timed on this host's cores, and on one thread, on bounded
-samples of the same workload.
+Also reported: forward fps (geometry + binning + splat, graphs of 8 renders) for the same
+scene, the G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from HIP
+events on the launch stream, the roofline of the dominant kernel, and the CPU oracle
+(PyTorch-CPU restatement of the reference path) timed on this host's cores, and on one thread,
+on bounded samples of the same workload.
 
 Clock state: before any timed region the GPU replays the forward graphs for ~1.5 s (no state
 change), so every timed region runs at steady clocks; a cold GPU measures several percent slower
@@ -119,9 +119,11 @@ def time_train(ts, steps, warmup, torch, run_len=8):
     return time.perf_counter() - t0
 
 
-def time_forward(ts, steps, warmup, torch):
+def time_forward(ts, steps, warmup, torch, run_len=8):
+    """Forward renders of the cameras round-robin: graphs of run_len consecutive renders (one
+    per starting camera), one-render graphs for a remainder; exactly `steps` renders timed."""
     ncam = len(ts.cams)
-    graphs = []
+    single, runs = [], []
     for ci in range(ncam):
         ts.forward(ci)
     torch.cuda.synchronize()
@@ -129,13 +131,25 @@ def time_forward(ts, steps, warmup, torch):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             ts.forward(ci)
-        graphs.append(g)
-    for i in range(warmup):
-        graphs[i % ncam].replay()
+        single.append(g)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for j in range(run_len):
+                ts.forward((ci + j) % ncam)
+        runs.append(g)
+
+    def render(start, n):
+        i = 0
+        while n - i >= run_len:
+            runs[(start + i) % ncam].replay()
+            i += run_len
+        for j in range(i, n):
+            single[(start + j) % ncam].replay()
+
+    render(0, warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        graphs[i % ncam].replay()
+    render(warmup % ncam, steps)
     torch.cuda.synchronize()
     return time.perf_counter() - t0
 
