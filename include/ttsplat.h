@@ -233,7 +233,9 @@ int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* vali
 /* -------------------------------------------------------------------- loss ---------- */
 
 /* Bytes of the target statistics of an H x W target: mu_y and s_y = G*y^2 - mu_y^2 of each
- * channel on the (H-10) x (W-10) valid SSIM map, six planes of floats. */
+ * channel on the (H-10) x (W-10) valid SSIM map (six planes of floats), then the target itself
+ * channel-planar (three H x W planes), which the gradient kernel reads instead of the
+ * interleaved image. */
 size_t tts_loss_stats_bytes(int H, int W);
 
 /* Bytes of scratch tts_loss_grad needs: the target statistics (tts_loss_stats_bytes). */
@@ -251,9 +253,10 @@ int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipSt
 
 /* dL/dimage of L = (1-lambda)*mean|x-y| + lambda*(1 - mean SSIM(clamp(x,0,1), clamp(y,0,1))),
  * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4, with the target's
- * statistics from tts_loss_target_stats: one kernel, no workspace.  Replaces the device loss of
- * tools/resident_traced.py:431-464 (its filt/filt_T banded matmuls over precomputed target
- * maps).  image, target, gimage: [H,W,3]; H, W >= 11 and H*W*24 <= 2^31-17 (TTS_EINVAL
+ * statistics from tts_loss_target_stats (target must be the image they were computed from;
+ * the kernel reads the planar copy inside stats): one kernel, no workspace.  Replaces the
+ * device loss of tools/resident_traced.py:431-464 (its filt/filt_T banded matmuls over
+ * precomputed target maps).  image, target, gimage: [H,W,3]; H, W >= 11 and H*W*24 <= 2^31-17 (TTS_EINVAL
  * otherwise: the kernels address with 32-bit buffer offsets; 7680x4320 fits).  partials (NULL
  * or tts_loss_partials_count floats) receives the partial sums. */
 int tts_loss_grad_stats(const float* image, const float* target, const float* stats, int H,

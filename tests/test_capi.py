@@ -95,7 +95,7 @@ def test_loss_grad_size_limit(lib):
     assert lib.tts_loss_grad_stats(p, p, p, 10000, 10000, 0.2, p, None, None) == -1
     assert lib.tts_loss_target_stats(p, 10000, 10000, p, None) == -1
     assert lib.tts_loss_grad(p, p, 4320, 7680, 0.2, p, None, None, 0, None) == -4
-    assert lib.tts_loss_stats_bytes(4320, 7680) == 24 * 4310 * 7670
+    assert lib.tts_loss_stats_bytes(4320, 7680) == 24 * 4310 * 7670 + 12 * 4320 * 7680
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

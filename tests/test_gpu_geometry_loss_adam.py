@@ -77,10 +77,15 @@ def test_loss_grad_ragged_sizes(H, W):
 @pytest.mark.parametrize("H,W", [(11, 13), (37, 75), (200, 300)])
 def test_loss_target_stats(H, W):
     """Target statistics against the oracle's window sums of the clamped target: mu_y and
-    s_y = G*y^2 - mu_y^2 per channel, each channel's planes column-major [Wo][Ho]."""
+    s_y = G*y^2 - mu_y^2 per channel, each channel's planes column-major [Wo][Ho]; then the
+    target itself channel-planar [3][H][W], unclamped."""
     g = torch.Generator().manual_seed(3 * H + W)
     y = torch.rand(H, W, 3, generator=g) * 1.2 - 0.1          # some values outside [0,1]
-    st = kernels.loss_stats(y.cuda()).cpu().view(2, 3, W - 10, H - 10).double()
+    full = kernels.loss_stats(y.cuda()).cpu()
+    nst = 6 * (H - 10) * (W - 10)
+    assert full.numel() == nst + 3 * H * W
+    assert torch.equal(full[nst:].view(3, H, W), y.permute(2, 0, 1))
+    st = full[:nst].view(2, 3, W - 10, H - 10).double()
     yc = y.double().clamp(0, 1).permute(2, 0, 1)
     gw = oloss.gauss_1d()
     mu = oloss.gaussian_filter(yc, gw)

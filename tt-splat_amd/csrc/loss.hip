@@ -3,9 +3,9 @@
 // (spike/metrics.py:6-28; the manual gradient of tools/loss_manual.py:76-103).
 //
 // The target's statistics mu_y = G*y and s_y = G*y^2 - mu_y^2 depend on the target only: a
-// training loop computes them once per view (k_loss_target_stats), as the reference's resident
-// trainer keeps muy/sy per view (tools/resident_traced.py:431-464).  The step kernel then
-// filters x, x^2 and xy only.
+// training loop computes them once per view (k_loss_target_stats, with a channel-planar copy
+// of the target), as the reference's resident trainer keeps muy/sy per view
+// (tools/resident_traced.py:431-464).  The step kernel then filters x, x^2 and xy only.
 //
 // k_loss_fused: a block owns a TH x 64 tile of gradient pixels of one colour channel and runs
 // the whole chain on it, the SSIM map region it needs (the tile plus the 10-pixel halo above and
@@ -136,6 +136,18 @@ __global__ __launch_bounds__(256) void k_loss_target_stats(const float* __restri
   }
 }
 
+// The target channel-planar ([3][H][W], after the statistics planes): the step kernel's loads of
+// one channel then touch contiguous floats (the interleaved image spreads a wave's 64 columns
+// over six cache lines per load).
+__global__ __launch_bounds__(256) void k_loss_target_planar(const float* __restrict__ y,
+                                                            int64_t n, float* __restrict__ yp) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  yp[i] = y[i * 3];
+  yp[n + i] = y[i * 3 + 1];
+  yp[2 * n + i] = y[i * 3 + 2];
+}
+
 // ------------------------------------------------------------------ fused step kernel ------
 template <int TH>
 struct FGeo {
@@ -172,7 +184,10 @@ __global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
   const int Ho = H - kHalo, Wo = W - kHalo;
   const int tid = threadIdx.x;
   const size_t ibytes = (size_t)H * W * 12;
-  const Rsrc xs = rsrc(x, ibytes), ys = rsrc(y, ibytes), gs_out = rsrc(gout, ibytes);
+  // y: this channel's plane of the target's planar copy, stored after the statistics
+  const size_t npix = (size_t)H * W;
+  const Rsrc xs = rsrc(x, ibytes), gs_out = rsrc(gout, ibytes);
+  const Rsrc ys = rsrc(stats + 6 * (size_t)Ho * Wo + (size_t)ch * npix, npix * 4);
   const Rsrc ss = rsrc(stats, (size_t)Ho * Wo * 24);
   const unsigned plane4 = (unsigned)(Ho * Wo) * 4u;
   // phase-2 role: map row m2, columns [q2, q2 + 15); its target statistics loaded up front
@@ -200,11 +215,13 @@ __global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
                               ? (unsigned)((((R0 - kHalo + m0) * W + gc) * 3 + ch) * 4)
                               : kOOB;
     const unsigned rstep = (unsigned)W * 12u;
+    const unsigned ybase = (gc >= 0 && gc < W) ? (unsigned)(((R0 - kHalo + m0) * W + gc) * 4)
+                                                : kOOB;
     float xv[G::VR + kHalo], yv[G::VR + kHalo];
 #pragma unroll
     for (int k = 0; k < G::VR + kHalo; ++k) {
       xv[k] = bld(xs, base + (unsigned)k * rstep);
-      yv[k] = bld(ys, base + (unsigned)k * rstep);
+      yv[k] = bld(ys, ybase + (unsigned)k * (unsigned)W * 4u);
     }
     // the target statistics phase 2 needs, issued after the loads phase 1 waits on
     load_stats();
@@ -304,7 +321,7 @@ __global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
 #pragma unroll
   for (int o = 0; o < G::TR4; ++o) {
     xr[o] = bld(xs, col4_ok ? off4 + (unsigned)o * rstep4 : kOOB);
-    yr[o] = bld(ys, col4_ok ? off4 + (unsigned)o * rstep4 : kOOB);
+    yr[o] = bld(ys, col4_ok ? (unsigned)(((R0 + p4 + o) * W + gc4) * 4) : kOOB);
   }
   __syncthreads();
   // ---- phase 3: transposed horizontal, thread = (map row m3, run of kHC3 gradient columns):
@@ -419,7 +436,7 @@ extern "C" {
 
 size_t tts_loss_stats_bytes(int H, int W) {
   if (H < kWin || W < kWin) return 0;
-  return sizeof(float) * 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo);
+  return sizeof(float) * (6 * (size_t)(H - kHalo) * (size_t)(W - kHalo) + 3 * (size_t)H * W);
 }
 
 size_t tts_loss_workspace_bytes(int H, int W) { return tts_loss_stats_bytes(H, W); }
@@ -436,6 +453,9 @@ int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipSt
   if (!loss_size_ok(H, W)) return TTS_EINVAL;
   const int tx = (W - kHalo + kSW - 1) / kSW, ty = (H - kHalo + kSH - 1) / kSH;
   k_loss_target_stats<<<tx * ty * 3, 256, 0, stream>>>(target, H, W, tx, make_taps(), stats);
+  const int64_t n = (int64_t)H * W;
+  k_loss_target_planar<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      target, n, stats + 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo));
   return launch_status();
 }
 

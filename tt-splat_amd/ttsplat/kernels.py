@@ -473,8 +473,8 @@ def loss_grad(image, target, lam=0.2, gimage=None, partials=None, workspace=None
 
 
 def loss_stats(target, stats=None):
-    """The target's SSIM statistics (mu_y, s_y per channel on the valid map), computed once per
-    target and read by loss_grad_stats."""
+    """The target's SSIM statistics (mu_y, s_y per channel on the valid map, then the target
+    channel-planar), computed once per target and read by loss_grad_stats."""
     H, W = target.shape[0], target.shape[1]
     require(target, "target", F32, (H, W, 3))
     n = _lib.load().tts_loss_stats_bytes(H, W)
