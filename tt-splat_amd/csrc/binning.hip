@@ -120,10 +120,19 @@ __global__ __launch_bounds__(1024) void k_bin_colscan(int* __restrict__ mat, int
   const int x = blockIdx.x * kChunk + col;
   const int rows = (nblk + 15) / 16;
   const int r0 = min(seg * rows, nblk), r1 = min(r0 + rows, nblk);
+  // up to 256 count blocks a thread's rows fit in registers and are read once; more are read
+  // again for the second pass
+  const bool held = rows <= 16;
+  int v[16];
   int sum = 0;
-  if (x < X) {
+  if (held) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      v[k] = (x < X && r0 + k < r1) ? mat[(int64_t)(r0 + k) * X + x] : 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sum += v[k];
+  } else if (x < X) {
     for (int rb = r0; rb < r1; rb += 16) {
-      int v[16];
 #pragma unroll
       for (int k = 0; k < 16; ++k) v[k] = rb + k < r1 ? mat[(int64_t)(rb + k) * X + x] : 0;
 #pragma unroll
@@ -144,14 +153,21 @@ __global__ __launch_bounds__(1024) void k_bin_colscan(int* __restrict__ mat, int
   __syncthreads();
   if (x < X) {
     int base = s_seg[seg][col];
-    for (int rb = r0; rb < r1; rb += 16) {
-      int v[16];
-#pragma unroll
-      for (int k = 0; k < 16; ++k) v[k] = rb + k < r1 ? mat[(int64_t)(rb + k) * X + x] : 0;
+    if (held) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        if (rb + k < r1) mat[(int64_t)(rb + k) * X + x] = base;
+        if (r0 + k < r1) mat[(int64_t)(r0 + k) * X + x] = base;
         base += v[k];
+      }
+    } else {
+      for (int rb = r0; rb < r1; rb += 16) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = rb + k < r1 ? mat[(int64_t)(rb + k) * X + x] : 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          if (rb + k < r1) mat[(int64_t)(rb + k) * X + x] = base;
+          base += v[k];
+        }
       }
     }
   }
