@@ -121,21 +121,22 @@ def time_train(ts, steps, warmup, torch, run_len=8):
 
 def time_forward(ts, steps, warmup, torch, run_len=8):
     """Forward renders of the cameras round-robin: graphs of run_len consecutive renders (one
-    per starting camera), one-render graphs for a remainder; exactly `steps` renders timed."""
+    per starting camera), one-render graphs for a remainder; exactly `steps` renders timed.  A
+    render bins without the inverse table, which only the backward reads."""
     ncam = len(ts.cams)
     single, runs = [], []
     for ci in range(ncam):
-        ts.forward(ci)
+        ts.forward(ci, grads=False)
     torch.cuda.synchronize()
     for ci in range(ncam):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            ts.forward(ci)
+            ts.forward(ci, grads=False)
         single.append(g)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for j in range(run_len):
-                ts.forward((ci + j) % ncam)
+                ts.forward((ci + j) % ncam, grads=False)
         runs.append(g)
 
     def render(start, n):
@@ -378,14 +379,14 @@ def run_c5(args, torch, scenes, kernels, TrainStep):
     ts = build_step(cfg, torch, TrainStep, batch=len(cfg.cameras()))
     nb = max(1, args.c5_batches)
     t_batch = time_train(ts, nb, 1, torch, run_len=1) / nb   # one graph per 64-view batch
-    # forward only, all 64 views, one graph
+    # forward only (renders: no inverse table), all 64 views, one graph
     for ci in range(len(ts.cams)):
-        ts.forward(ci)
+        ts.forward(ci, grads=False)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for ci in range(len(ts.cams)):
-            ts.forward(ci)
+            ts.forward(ci, grads=False)
     g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()

@@ -87,3 +87,17 @@ def test_splat_on_records_nan_tile():
     assert same(img, img2) and same(den, den2)
     v = valid.bool()
     assert same(g1[v], g2[v]) and same(w1, w2)
+
+
+def test_render_only_forward_equals_training_forward():
+    """TrainStep.forward(grads=False) (binning without the inverse table) renders the same
+    image and den as the training step's forward."""
+    from ttsplat.step import TrainStep
+    from helpers import config_inputs as ci_
+    cfg, P, cam = ci_("c3")
+    ts = TrainStep(P, [cam], [torch.zeros(cfg.H, cfg.W, 3)], K=cfg.K, S=cfg.S, k=cfg.k)
+    img = ts.forward(0).clone()
+    den = ts.den.clone()
+    img2 = ts.forward(0, grads=False).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(img, img2) and torch.equal(den, ts.den)

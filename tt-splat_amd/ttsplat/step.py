@@ -194,10 +194,12 @@ class TrainStep:
         return None if self.sh is None else kernels.sh_rest_model(self.sh)
 
     # ---------------------------------------------------------------------------------
-    def forward(self, ci=0, advance=False, rebin=True):
+    def forward(self, ci=0, advance=False, rebin=True, grads=True):
         """Geometry + binning + fused splat for camera ci into self.image.  advance=True: the
         geometry launch also advances the Adam step block (a training step's first kernel).
-        rebin=False: the bins last computed are reused (the binning kernels are not run)."""
+        rebin=False: the bins last computed are reused (the binning kernels are not run).
+        grads=False: a render only -- the binning skips the inverse table (gaussian -> slots)
+        that only the backward reads; a later step that reuses these bins must not follow."""
         adv = self.step_block if advance else None
         if rebin:   # one call: the binning's count pass rides on the geometry launch
             kernels.geom_fwd_assign_bins(self.P, self.cams[ci], self.H, self.W, self.S, self.K,
@@ -205,7 +207,8 @@ class TrainStep:
                                          sh_rest=self.sh, sh_degree=self.sh_degree,
                                          depth_bt=self.dw, advance=adv,
                                          workspace=self.bin_ws, idx=self.idx, valid=self.valid,
-                                         count=self.count, ncand=self.ncand, inv=self.inv,
+                                         count=self.count, ncand=self.ncand,
+                                         inv=self.inv if grads else None,
                                          order=self.order, slot_rec=self.slot_rec,
                                          pos_count=self.pos_count)
         else:
