@@ -90,8 +90,8 @@ def test_splat_on_records_nan_tile():
 
 
 def test_render_only_forward_equals_training_forward():
-    """TrainStep.forward(grads=False) (binning without the inverse table) renders the same
-    image and den as the training step's forward."""
+    """TrainStep.forward(grads=False) (binning without the inverse table, no den) renders the
+    same image as the training step's forward and leaves den as that forward wrote it."""
     from ttsplat.step import TrainStep
     from helpers import config_inputs as ci_
     cfg, P, cam = ci_("c3")

@@ -283,30 +283,39 @@ def _rec_check(slot_rec, pos_count, order, H, W, S, dev):
     return T, K
 
 
-def splat_fwd_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=None):
-    """splat_fwd on the slot records of geom_fwd_assign_bins (S = 16): the same image and den."""
+def splat_fwd_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=None,
+                  write_den=True):
+    """splat_fwd on the slot records of geom_fwd_assign_bins (S = 16): the same image and den.
+    write_den=False: a render only -- den (which only the backward reads) is not written."""
     dev = slot_rec.device
     T, K = _rec_check(slot_rec, pos_count, order, H, W, S, dev)
     require(bg, "bg", F32, (4,), dev)
     image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
-    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
     require(image, "image", F32, (H, W, 3), dev)
-    require(den, "den", F32, (H, W), dev)
+    if write_den:
+        den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+        require(den, "den", F32, (H, W), dev)
+    else:
+        den = None
     call("tts_splat_fwd_rec", ptr(slot_rec), ptr(pos_count), ptr(order), H, W, S, K, float(k),
          ptr(bg), ptr(image), ptr(den), stream())
     return image, den
 
 
 def splat_fwd_mx_rec(slot_rec, pos_count, order, bg, H, W, S, k, image=None, den=None,
-                     bf16=False):
-    """splat_fwd_mx on the slot records of geom_fwd_assign_bins: the same image and den."""
+                     bf16=False, write_den=True):
+    """splat_fwd_mx on the slot records of geom_fwd_assign_bins: the same image and den
+    (write_den=False: den not written)."""
     dev = slot_rec.device
     T, K = _rec_check(slot_rec, pos_count, order, H, W, S, dev)
     require(bg, "bg", F32, (4,), dev)
     image = torch.empty(H, W, 3, device=dev, dtype=F32) if image is None else image
-    den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
     require(image, "image", F32, (H, W, 3), dev)
-    require(den, "den", F32, (H, W), dev)
+    if write_den:
+        den = torch.empty(H, W, device=dev, dtype=F32) if den is None else den
+        require(den, "den", F32, (H, W), dev)
+    else:
+        den = None
     call("tts_splat_fwd_mx_rec", ptr(slot_rec), ptr(pos_count), ptr(order), H, W, S, K,
          float(k), ptr(bg), ptr(image), ptr(den), int(bool(bf16)), stream())
     return image, den

@@ -199,7 +199,8 @@ class TrainStep:
         geometry launch also advances the Adam step block (a training step's first kernel).
         rebin=False: the bins last computed are reused (the binning kernels are not run).
         grads=False: a render only -- the binning skips the inverse table (gaussian -> slots)
-        that only the backward reads; a later step that reuses these bins must not follow."""
+        and the splat kernel the per-pixel den, which only the backward reads (self.den is
+        left as it was); a later step that reuses these bins must not follow."""
         adv = self.step_block if advance else None
         if rebin:   # one call: the binning's count pass rides on the geometry launch
             kernels.geom_fwd_assign_bins(self.P, self.cams[ci], self.H, self.W, self.S, self.K,
@@ -217,13 +218,15 @@ class TrainStep:
                              advance=adv)
         if self.dtype == "bf16" and rebin and self.use_rec:
             kernels.splat_fwd_mx_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
-                                     self.W, self.S, self.k, self.image, self.den, bf16=True)
+                                     self.W, self.S, self.k, self.image, self.den, bf16=True,
+                                     write_den=grads)
         elif self.dtype == "bf16":
             kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
         elif rebin and self.use_rec:
             kernels.splat_fwd_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
-                                  self.W, self.S, self.k, self.image, self.den)
+                                  self.W, self.S, self.k, self.image, self.den,
+                                  write_den=grads)
         else:
             kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
                               self.k, self.image, self.den, self.order)
