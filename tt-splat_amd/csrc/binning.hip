@@ -552,6 +552,23 @@ __device__ __forceinline__ void rec_store(float* __restrict__ rb, int slot, Slot
   dst[2] = r.r2;
 }
 
+// What a kept survivor writes at its slot `rank` of the tile whose slots start at `base`: its
+// gaussian in idx, valid = 1, its inverse-table entry inv[g][j] (a gaussian reaches a tile through
+// exactly one stencil index j) and, with records (rb), its slot record.  An unused slot s gets
+// idx 0, valid 0.
+__device__ __forceinline__ void put_slot(const SelectArgs& a, int64_t base, float* rb, int rank,
+                                         unsigned long long key, const SlotRec& rec) {
+  const int g = static_cast<int32_t>(key & 0xffffffffull);
+  a.idx[base + rank] = g;
+  if (a.inv) a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
+  a.valid[base + rank] = 1;
+  if (rb) rec_store(rb, rank, rec);
+}
+__device__ __forceinline__ void clear_slot(const SelectArgs& a, int64_t base, int s) {
+  a.idx[base + s] = 0;
+  a.valid[base + s] = 0;
+}
+
 // Slot of tile t (n candidates) in the heaviest-first order: tiles of smaller keys (more kept
 // slots), then this key's tiles of earlier classification blocks, then its rank in its block.
 // A lane sums whole keys (key-major table, no division); full tiles (key 0) need only their
@@ -690,17 +707,8 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
         const int s = h ? sb : sa;
         const unsigned long long key = h ? kb : ka;
         const int rank = h ? rnb : ra;
-        if (s < m) {
-          const int g = static_cast<int32_t>(key & 0xffffffffull);
-          a.idx[base + rank] = g;
-          if (a.inv)
-            a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-          a.valid[base + rank] = 1;
-          if (rb) rec_store(rb, rank, h ? recb : reca);
-        } else if (s < a.K) {
-          a.idx[base + s] = 0;
-          a.valid[base + s] = 0;
-        }
+        if (s < m) put_slot(a, base, rb, rank, key, h ? recb : reca);
+        else if (s < a.K) clear_slot(a, base, s);
       }
     }
   } else {
@@ -736,17 +744,12 @@ __device__ __forceinline__ void select_light(int t, const SelectArgs& a, TileCel
         SlotRec rec{};
         if (rb) rec = rec_load(a.proj, static_cast<int32_t>(key & 0xffffffffull));
         const unsigned w = grp[key_group(key, satq, shift)];
-        const int rank = rank_in_group(key, gat, static_cast<int>(w >> 20),
-                                       static_cast<int>((w >> 10) & 1023u));
-        const int g = static_cast<int32_t>(key & 0xffffffffull);
-        a.idx[base + rank] = g;
-        if (a.inv)
-          a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-        a.valid[base + rank] = 1;
-        if (rb) rec_store(rb, rank, rec);
+        put_slot(a, base, rb,
+                 rank_in_group(key, gat, static_cast<int>(w >> 20),
+                               static_cast<int>((w >> 10) & 1023u)),
+                 key, rec);
       } else {
-        a.idx[base + s] = 0;
-        a.valid[base + s] = 0;
+        clear_slot(a, base, s);
       }
     }
   }
@@ -1049,18 +1052,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(8))) void k_
   const int m = min(s_fill, K);
   const int64_t base = static_cast<int64_t>(t) * K;
   float* rb = a.rec ? a.rec + (int64_t)s_oslot * K * 12 : nullptr;
-  auto put = [&](int rank, unsigned long long key, SlotRec rec) {
-    const int g = static_cast<int32_t>(key & 0xffffffffull);
-    a.idx[base + rank] = g;
-    if (a.inv)
-      a.inv[(int64_t)g * 9 + ((key >> kJShift) & 15ull)] = static_cast<int32_t>(base + rank);
-    a.valid[base + rank] = 1;
-    if (rb) rec_store(rb, rank, rec);
+  auto put = [&](int rank, unsigned long long key, const SlotRec& rec) {
+    put_slot(a, base, rb, rank, key, rec);
   };
-  auto clear = [&](int s) {
-    a.idx[base + s] = 0;
-    a.valid[base + s] = 0;
-  };
+  auto clear = [&](int s) { clear_slot(a, base, s); };
   if (K <= 128) {
     // All pairs: two adjacent lanes share a survivor, each counting over half of them; the keys
     // are padded to a multiple of 16 with the largest key (never below a survivor) and read 8 at
