@@ -135,8 +135,9 @@ int tts_theta_u_gathered(const float* proj, const int32_t* idx, const uint8_t* v
  * straight into the image.  Replaces tools/bh_views.py:65-71 on _operands
  * (tools/m4_train_binned.py:189-212) and the device chain tools/resident_traced.py:358-370.
  * den may be NULL (it is needed by tts_splat_bwd).  order (tts_tile_order) may be NULL.
- * For S = 16 the quadratic form runs on the fp32 matrix cores (images within the fp32
- * contract, 1e-4 of the reference; they round differently from tts_splat_fwd_theta). */
+ * For S = 16 each wave walks the whole tile for a quarter of the slots, u factored per pixel
+ * column (images within the fp32 contract, 1e-4 of the reference; they round differently from
+ * tts_splat_fwd_theta). */
 int tts_splat_fwd(const float* proj, const int32_t* idx, const uint8_t* valid,
                   const int32_t* order, int H, int W, int S, int K, float k, const float* bg,
                   float* image, float* den, hipStream_t stream);

@@ -51,8 +51,9 @@ def test_c5_splat_sampled_tiles(c5):
                       device="cuda")
     th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, cfg.k)
     img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k)
-    # the fused kernel (u on fp32 matrix cores) and the pre-gathered-operand kernel (u on the
-    # VALU) round differently; over the whole frame they agree within the fp32 contract, and the
+    # the fused 16x16 kernel (u factored per column, wave sums joined) and the
+    # pre-gathered-operand kernel round differently; over the whole frame they agree within the
+    # fp32 contract, and the
     # tiles where they differ most join the sample checked against the oracle below
     img2, _ = kernels.splat_fwd_theta(th, col, oc, bg, cfg.H, cfg.W, cfg.S)
     assert max_abs(img, img2) <= 1e-4

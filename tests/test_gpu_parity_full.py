@@ -1,6 +1,6 @@
 """The kernels the training step runs, against the oracle at the headline sizes.
 
-G = 100k clustered, 1264x832, K = 128 (k_splat_fwd_mf, the fused k_splat_bwd, the loss kernels,
+G = 100k clustered, 1264x832, K = 128 (k_splat_fwd_tile, the fused k_splat_bwd, the loss kernels,
 the fused geometry backward + Adam, one whole training step) and G = 1M, 1920x1072, K = 256
 (the bf16 matrix-core forward over the whole frame, the fused backward on sampled tiles), the
 loss at 800x800, 1264x832 and 1072x1920, and slot budgets above 256 (K = 512).  The oracle
@@ -50,7 +50,7 @@ def test_c4_forward_full_frame(c4):
     tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
     ref, rden = oracle_render_chunked(P, cam_dict(cam), tmap, (idx, valid), cfg.k)
     err = max_abs(img, ref)
-    print(f"[c4] fwd_mf max|err| {err:.2e}, pairs {int(count.sum()) * 256}", flush=True)
+    print(f"[c4] fwd max|err| {err:.2e}, pairs {int(count.sum()) * 256}", flush=True)
     assert err <= 1e-4
     assert max_abs(den, rden) <= 1e-4 * float(rden.abs().max())
 
@@ -115,7 +115,7 @@ def c5():
 
 
 def test_c5_forward_full_frame(c5):
-    """Whole frame: the bf16 render variant within 1e-2, the fp32 matrix-core forwards within
+    """Whole frame: the bf16 render variant within 1e-2, the fp32 forwards within
     1e-4 (the oracle takes the GPU's geometry records, so only the splat is compared)."""
     cfg, P, cam, camera, proj, keep, idx, valid, count, inv, order, bg = c5
     tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
@@ -199,7 +199,7 @@ def test_loss_at_full_size(H, W):
 
 def test_slot_budget_512_forward_and_backward():
     """K = 512 on a crowded small scene (G = 20k clustered on 160x160, most tiles full): the
-    matrix-core forward, the VALU theta forward and the oracle agree; the fused backward's
+    fused 16x16 forward, the theta forward and the oracle agree; the fused backward's
     second 256-slot prologue round gives oracle parameter gradients."""
     cfg = scenes.Config("k512", 20000, 160, 160, K=512, S=16, k=4.0, means="clustered")
     P = cfg.params(0)

@@ -48,8 +48,9 @@ def test_splat_fwd_parity(name, k):
 
 @pytest.mark.parametrize("K", [1, 30, 61])
 def test_splat_fwd_ragged_budgets(K):
-    """Slot budgets that are not multiples of the matrix-core forward's 4-slot groups (its LDS is
-    sized from K rounded up, the padding slots zeroed), down to a single slot per tile."""
+    """Slot budgets that are not multiples of 4 (the 16x16 forward's LDS is sized from K rounded
+    up to 4, the padding slots zeroed; its waves take the slots 4 apart), down to a single slot
+    per tile."""
     cfg, P, cam = config_inputs("c1_ref")
     camera = cam.device_block("cuda")
     proj, keep = kernels.geom_fwd(P.cuda(), camera)

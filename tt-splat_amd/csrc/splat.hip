@@ -7,9 +7,8 @@
 // each thread owns S*S/256 pixels and walks the slots:
 //     u = theta . [lx^2, ly^2, lx*ly, lx, ly, 1],  w = max(u,0)^2,  num += w*col, den += w*oc
 // and writes C = (num + w_b c_b) / (den + w_b) straight into the [H,W,3] image.  For S = 16
-// from proj (tts_splat_fwd) u is formed on the fp32 matrix cores instead (k_splat_fwd_mf: per
-// pixel row u is a quadratic in lx, evaluated for 4 rows x 4 slots x 16 pixels per
-// v_mfma_f32_16x16x4f32), the rest of the walk staying on the VALU.
+// from proj or slot records (k_splat_fwd_tile) each wave walks the whole tile for a quarter of
+// the slots instead, u factored per column.
 //
 // Backward: per-pixel gnum = gC/den, gden = -(gC.C)/den are staged in LDS (rows padded to S+1
 // entries); the slots are then contracted over the tile's pixels slot-parallel (tps adjacent
@@ -643,29 +642,29 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
   }
 }
 
-// Forward on fp32 matrix cores (S = 16, slots from proj).  Along one pixel row (ly fixed) the
-// quadratic form is a quadratic in lx alone:
-//   u = theta0 lx^2 + (theta2 ly + theta3) lx + (theta1 ly^2 + theta4 ly + theta5),
-// so one v_mfma_f32_16x16x4f32 evaluates it for 4 pixel rows x 4 slots (the 16 A rows, i = 4 row
-// + slot) against the 16 pixels of a row (B columns: lx^2, lx, 1, 0).  Lane layout of the
-// instruction (checked on gfx950): A[i][k] in lane i + 16k, B[k][j] in lane j + 16k, D[i][j] in
-// lane j + 16*(i/4), element i % 4 -- so lane (q, j) receives u of its own pixel (row q of the
-// wave's four, column j) for the group's four slots and sums them without any cross-lane step.
-// Each A entry is (p ly + q) ly + r with (p, q, r) per (slot, depth k) staged in LDS:
-// k = 0: (0, 0, theta0), k = 1: (0, theta2, theta3), k = 2: (theta1, theta4, theta5), k = 3: 0.
-// The VALU keeps relu^2 and the colour / density sums (6 instructions per pair, 2 more per
-// 256 pairs for A).  Slot s is staged at LDS entry s (zero when invalid: u = 0, w = 0) and the
-// walk runs to the highest valid slot, so bins whose valid slots form a prefix (tts_assign_bins)
-// are summed in slot order with no zero terms beyond the last group.
+// Forward for 16x16 tiles from proj (tts_splat_fwd) or from slot records (tts_splat_fwd_rec).
+// Each wave walks the whole tile for a quarter of the slots (slot s to wave s mod 4), 4 pixels
+// per lane (column j = lane % 16, rows 4m + lane / 16): per slot and column the quadratic form
+// is u = (theta1 ly + P) ly + Q with P = theta2 lx + theta4 and Q = (theta0 lx + theta3) lx +
+// theta5, so a pixel costs 2 FMA for u, relu^2 as an integer max and a multiply, and 4 FMA for
+// the colour and density sums.  The four waves' sums are then joined through LDS in wave order.
+// (u on the fp32 matrix cores -- one v_mfma_f32_16x16x4f32 for 4 rows x 4 slots x 16 pixels --
+// was 0.7 us slower at 1264x832 once the slot records had shortened the prologue.)  Slot s is
+// staged at LDS entry s (zero when invalid: u = 0, w = 0) and the walk runs to the highest
+// valid slot, so bins whose valid slots form a prefix (tts_assign_bins) add no zero terms
+// beyond it.
 // REC: the slots come from slot records (src = slot_rec [T][K][12] in dispatch order, block b
 // reads src[b], its kept count pos_count[b] and its tile order[b] in one round trip); otherwise
 // src = proj and the slots from idx / valid of tile order[b].
-inline size_t fwd_mf_lds(int K) {
+// LDS: the staged slots (theta0..3, colour, theta4..5: 40 bytes each), reused afterwards for
+// the join of the four waves' sums (4 waves x 4 rows x 64 lanes x float4 = 16 KB).
+inline size_t fwd_tile_lds(int K) {
   const int k4 = (K + 3) & ~3;
-  return (size_t)k4 * 5 * sizeof(float4);
+  const size_t a = (size_t)k4 * 40, r = 16 * 64 * sizeof(float4);
+  return a > r ? a : r;
 }
 template <bool REC>
-__global__ __launch_bounds__(256) void k_splat_fwd_mf(
+__global__ __launch_bounds__(256) void k_splat_fwd_tile(
     const float* __restrict__ src, const int32_t* __restrict__ idx,
     const uint8_t* __restrict__ valid, const int32_t* __restrict__ pos_count,
     const int32_t* __restrict__ order, int ntx, int W, int K, float inv_k,
@@ -673,8 +672,9 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   extern __shared__ __attribute__((aligned(16))) unsigned char s_dyn[];
   __shared__ int s_hi[2][4];
   const int k4 = (K + 3) & ~3;
-  float4* s_coef = reinterpret_cast<float4*>(s_dyn);  // [k4][4]: (p, q, r, 0) per depth k
-  float4* s_col = s_coef + (size_t)k4 * 4;           // [k4]: col_o r, g, b, o_col
+  float4* s_th = reinterpret_cast<float4*>(s_dyn);         // [k4]: theta0..3
+  float4* s_col = s_th + k4;                               // [k4]: col_o r, g, b, o_col
+  float2* s_th2 = reinterpret_cast<float2*>(s_col + k4);   // [k4]: theta4, theta5
   const int t = order ? order[blockIdx.x] : blockIdx.x;
   const int nb = REC ? min(pos_count[blockIdx.x], K) : 0;
   const int tx = t % ntx, ty = t / ntx;
@@ -685,23 +685,17 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   // slot s's coefficients go to LDS entry s (zero for an invalid slot)
   auto stage = [&](int s, int v, const float4& r0, const float4& r1, const float4& r2) {
     if (s >= k4) return;
-    float4* c = s_coef + (size_t)s * 4;
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
       bad = bad || theta_poisons(ta, tb);
-      c[0] = make_float4(0.f, 0.f, ta.x, 0.f);
-      c[1] = make_float4(0.f, ta.z, ta.w, 0.f);
-      c[2] = make_float4(ta.y, tb.x, tb.y, 0.f);
-      c[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_th[s] = ta;
+      s_th2[s] = make_float2(tb.x, tb.y);
       s_col[s] = cl;
     } else {
-      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-      c[0] = z;
-      c[1] = z;
-      c[2] = z;
-      c[3] = z;
-      s_col[s] = z;
+      s_th[s] = make_float4(0.f, 0.f, 0.f, 0.f);
+      s_th2[s] = make_float2(0.f, 0.f);
+      s_col[s] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   // g: the gaussian (from idx), or with REC the slot of this block's records
@@ -744,39 +738,32 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
   if (more && wave > 0 && v) gather(g, r0, r1, r2);
 
   const int j = lane & 15, q = lane >> 4;
-  // A side of this lane: row (lane >> 2) & 3 of the wave, slot lane & 3 of a group, depth q
-  const float ly_a = (float)(4 * wave + ((lane >> 2) & 3)) + 0.5f;
-  const int a_off = (lane & 3) * 4 + q;  // float4 index inside a group's coefficients
-  // B side: pixel column j at depth q: (lx^2, lx, 1, 0)[q]
-  const float lx = (float)j + 0.5f;
-  const float bq = q == 0 ? lx * lx : (q == 1 ? lx : (q == 2 ? 1.0f : 0.0f));
-  float ar = 0.f, ag = 0.f, ab = 0.f, ad = 0.f;
-  const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
-  auto walk = [&](int g0, int g1) {
-#pragma unroll 4
-    for (int gi = g0; gi < g1; ++gi) {
-      const float4 pc = s_coef[(size_t)gi * 16 + a_off];
-      const float a = fmaf(fmaf(pc.x, ly_a, pc.y), ly_a, pc.z);
-      const floatx4 u = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq, zero4, 0, 0, 0);
-      // elements copied out before their bits are reinterpreted (a bit cast applied to the
-      // vector-element expression itself compiled to element 0 for every e)
-      const float ue[4] = {u[0], u[1], u[2], u[3]};
+  const float lx = (float)j + 0.5f, lyq = (float)q + 0.5f;
+  float acc[4][4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float4 cl = s_col[gi * 4 + e];
-        // relu as one integer max on the bit pattern (a float max would first canonicalise the
-        // matrix-core result): u >= +0 keeps its bits, negative u becomes +0; a NaN u (a
-        // poisoned tile, whatever its sign bit) is overwritten by the NaN store below
-        const float rl = __int_as_float(max(__float_as_int(ue[e]), 0));
+  for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = acc[m][2] = acc[m][3] = 0.f;
+  auto walk = [&](int s0, int s1) {
+#pragma unroll 2
+    for (int sl = s0 + wave; sl < s1; sl += 4) {
+      const float4 th = s_th[sl];
+      const float2 th2 = s_th2[sl];
+      const float4 cl = s_col[sl];
+      const float P = fmaf(th.z, lx, th2.x);
+      const float Q = fmaf(fmaf(th.x, lx, th.w), lx, th2.y);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const float ly = lyq + (float)(4 * m);
+        const float u = fmaf(fmaf(th.y, ly, P), ly, Q);
+        const float rl = __int_as_float(max(__float_as_int(u), 0));
         const float w = rl * rl;
-        ar += w * cl.x;
-        ag += w * cl.y;
-        ab += w * cl.z;
-        ad += w * cl.w;
+        acc[m][0] += w * cl.x;
+        acc[m][1] += w * cl.y;
+        acc[m][2] += w * cl.z;
+        acc[m][3] += w * cl.w;
       }
     }
   };
-  walk(0, (min(n0, 64) + 3) >> 2);
+  walk(0, min(n0, 64));
   if (more) {
     if (wave > 0) stage(s, v, r0, r1, r2);
     int hi = 0;
@@ -802,8 +789,25 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mf(
     poisoned = __syncthreads_or(bad) || poisoned;
     const int n = REC ? nb
                       : max(n0, max(max(s_hi[1][0], s_hi[1][1]), max(s_hi[1][2], s_hi[1][3])));
-    walk(16, (n + 3) >> 2);
+    walk(64, n);
   }
+  // join the four waves' sums in wave order; the slot LDS is reused
+  float4* red = reinterpret_cast<float4*>(s_dyn);
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    red[(wave * 4 + m) * 64 + lane] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+  __syncthreads();
+  float4 sum = red[wave * 64 + lane];
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) {
+    const float4 o = red[(w2 * 4 + wave) * 64 + lane];
+    sum.x += o.x;
+    sum.y += o.y;
+    sum.z += o.z;
+    sum.w += o.w;
+  }
+  const float ar = sum.x, ag = sum.y, ab = sum.z, ad = sum.w;
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
   const float nanv = __builtin_nanf("");
@@ -859,8 +863,8 @@ int launch_fwd(const float* proj, const int32_t* idx, const uint8_t* valid, cons
   const int ntx = W / S, T = (H / S) * ntx;
   const float inv_k = (float)(1.0 / (double)k);
   if (S == 16 && FROM_PROJ)
-    k_splat_fwd_mf<false><<<T, 256, fwd_mf_lds(K), stream>>>(proj, idx, valid, nullptr, order,
-                                                              ntx, W, K, inv_k, bg, image, den);
+    k_splat_fwd_tile<false><<<T, 256, fwd_tile_lds(K), stream>>>(
+        proj, idx, valid, nullptr, order, ntx, W, K, inv_k, bg, image, den);
   else if (S == 16)
     k_splat_fwd<16, FROM_PROJ, OT><<<T, 256, fwd_lds(K), stream>>>(
         proj, idx, valid, theta, col, oc, order, ntx, W, K, inv_k, bg, image, den);
@@ -965,7 +969,7 @@ int tts_splat_fwd_rec(const float* slot_rec, const int32_t* pos_count, const int
   if (S != 16) return TTS_ETILE;
   if (!slot_rec || !pos_count || !order || !bg || !image) return TTS_EINVAL;
   const int ntx = W / S, T = (H / S) * ntx;
-  k_splat_fwd_mf<true><<<T, 256, fwd_mf_lds(K), stream>>>(
+  k_splat_fwd_tile<true><<<T, 256, fwd_tile_lds(K), stream>>>(
       slot_rec, nullptr, nullptr, pos_count, order, ntx, W, K, (float)(1.0 / (double)k), bg,
       image, den);
   return launch_status();
