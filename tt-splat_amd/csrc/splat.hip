@@ -680,7 +680,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
   const int tx = t % ntx, ty = t / ntx;
   const int ox = tx * 16, oy = ty * 16;
   const float oxf = (float)ox, oyf = (float)oy;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index is uniform: read it into a scalar register so the walk's slot loop is scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   bool bad = false;
   // slot s's coefficients go to LDS entry s (zero for an invalid slot)
   auto stage = [&](int s, int v, const float4& r0, const float4& r1, const float4& r2) {
