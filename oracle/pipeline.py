@@ -6,7 +6,7 @@ Follows the op order of the device-resident step, tools/resident_traced.py:667-7
 geometry fwd -> binning -> gather/theta -> splat fwd -> loss gradient -> splat bwd ->
 theta bwd -> slot->gaussian reduce -> geometry bwd -> Adam, with the gradient of everything
 after binning taken by autograd of the restated forward (the reference's manual chain,
-tools/operands_manual.py:83-111, equals that autograd to 1e-3, :476-493).
+tools/operands_manual.py:83-111, equals that autograd to 1e-3, :114-144).
 w_b is held fixed, as in that trainer (tools/resident_traced.py:220).
 """
 import torch

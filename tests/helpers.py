@@ -9,6 +9,12 @@ def cam_dict(cam: Camera):
     return cam.as_dict()
 
 
+def anisotropic(cam: Camera, ratio=1.13, px=0.46, py=0.53):
+    """The same pose with fx = ratio * fy and the principal point off the image centre (at
+    px * W, py * H), as COLMAP's PINHOLE / OPENCV models give (spike/data.py:127-150)."""
+    return Camera(cam.R_v, cam.t_v, ratio * cam.fy, cam.fy, px * cam.W, py * cam.H, cam.H, cam.W)
+
+
 def rel_l2(a, b):
     a = a.detach().double().cpu()
     b = b.detach().double().cpu()
@@ -19,14 +25,26 @@ def max_abs(a, b):
     return float((a.detach().double().cpu() - b.detach().double().cpu()).abs().max())
 
 
-def config_inputs(name, seed=0, cam_index=0, G=None):
-    """(config, params[G,14] CPU, camera) for a named configuration (G optionally reduced)."""
+def update_error_ok(p_gpu, p0, ref, rtol=1e-4):
+    """|(p - p0) - (ref - p0)| <= rtol |ref - p0| + 2 ulp(p) per entry: the update, not the
+    parameter, is compared (updates ~ lr << |p|), with the fp32 rounding of p itself allowed."""
+    pf = p_gpu.detach().cpu().float()
+    ulp = (torch.nextafter(pf, torch.full_like(pf, float("inf"))) - pf).double()
+    du = pf.double() - p0.double()
+    dref = ref.double() - p0.double()
+    bad = (du - dref).abs() > rtol * dref.abs() + 2.0 * ulp
+    return int(bad.sum())
+
+
+def config_inputs(name, seed=0, cam_index=0, G=None, aniso=False):
+    """(config, params[G,14] CPU, camera) for a named configuration (G optionally reduced;
+    aniso: the camera with fx = 1.13 fy and an off-centre principal point)."""
     cfg = scenes.CONFIGS[name]
     if G is not None:
         cfg = scenes.Config(**{**cfg.__dict__, "G": G, "span": cfg.span})
     P = cfg.params(seed)
     cam = cfg.cameras()[cam_index]
-    return cfg, P, cam
+    return cfg, P, (anisotropic(cam) if aniso else cam)
 
 
 def bins_equal_report(idx_a, valid_a, idx_b, valid_b):

@@ -10,6 +10,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 REF = "/root/reference"
 CITE = re.compile(r"((?:spike|tools|docs|outputs)/[\w./-]+?\.(?:py|md|json|sh|txt))"
                   r"((?::\d+(?:-\d+)?)(?:,\d+(?:-\d+)?)*)?")
+# a bare ":N-M" later on a line that cites a path refers to that path ("a.py:1-5, :9-12")
+BARE = re.compile(r"(?<![\w.\[/:])(:\d+(?:-\d+)?(?:,\d+(?:-\d+)?)*)(?![\w.])")
 # driver-written records and the survey quote the reference too, but are not this build's text
 SKIP_PREFIX = ("SURVEY", "VERDICT", "ADVICE", "BASELINE", "BENCH_", "GPUTEST_", "SCALE_",
                "MULTICHIP_", "PROGRESS")
@@ -28,8 +30,12 @@ def test_reference_citations_point_at_existing_lines():
         except (UnicodeDecodeError, FileNotFoundError):
             continue
         for ln, line in enumerate(text.splitlines(), 1):
-            for m in CITE.finditer(line):
-                path, rng = m.group(1), m.group(2)
+            cites = [(m.start(), m.end(), m.group(1), m.group(2)) for m in CITE.finditer(line)]
+            for b in BARE.finditer(line):
+                prev = [c for c in cites if c[1] <= b.start()]
+                if prev and not any(s <= b.start() < e for s, e, _, _ in cites):
+                    cites.append((b.start(), b.end(), prev[-1][2], b.group(1)))
+            for _, _, path, rng in cites:
                 full = os.path.join(REF, path)
                 if not os.path.isfile(full):
                     bad.append(f"{f}:{ln} {path}: no such reference file")

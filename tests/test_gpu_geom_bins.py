@@ -99,3 +99,16 @@ def test_geom_fwd_assign_bins_sh_depth_weight_advance():
                     sh_degree=3, depth_bt=bt, advance=True)
     check_equal(a, b, cfg.K)
     assert int(a["adv"][0]) == 1
+
+
+def test_geom_fwd_assign_bins_largest_grid():
+    """The largest grid the binning takes, 38912 tiles (4096 x 2432 at S = 16): the fused
+    launch's count histogram is then largest (4608 + 4 * 38912 = 160256 bytes of LDS, within the
+    160 KiB a workgroup has), and the fused call equals the two calls."""
+    from ttsplat import scenes
+    cfg = scenes.Config("grid38912", 5000, 2432, 4096, K=128, S=16, k=4.0)
+    P, cam = cfg.params(0), cfg.cameras()[0]
+    assert (cfg.H // 16) * (cfg.W // 16) == 38912
+    print(f"[geom+bins] {cfg.W}x{cfg.H} G={cfg.G}", flush=True)
+    a, b = two_ways(cfg, P.cuda(), cam)
+    check_equal(a, b, cfg.K)

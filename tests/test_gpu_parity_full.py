@@ -10,7 +10,8 @@ separately.  Contract: images 1e-4 max-abs (fp32) / 1e-2 (bf16), gradients 1e-3 
 import pytest
 import torch
 
-from helpers import cam_dict, config_inputs, max_abs, oracle_render_chunked, rel_l2
+from helpers import (anisotropic, cam_dict, config_inputs, max_abs, oracle_render_chunked, rel_l2,
+                     update_error_ok)
 from oracle import adam as oadam
 from oracle import binning as obin
 from oracle import loss as oloss
@@ -72,10 +73,14 @@ def test_c4_backward_full_frame(c4):
         assert e <= 1e-3, name
 
 
-def test_c4_training_step(c4):
+@pytest.mark.parametrize("aniso", [False, True], ids=["fx=fy", "fx=1.13fy"])
+def test_c4_training_step(c4, aniso):
     """One graph-captured training step, camera 0, against the oracle's step on the GPU's bins:
-    image, loss, the gradient Adam received, and the Adam update applied to it."""
+    image, loss, the gradient Adam received, and the Adam update applied to it.  Also through a
+    camera with fx = 1.13 fy and an off-centre principal point."""
     cfg, P, cam = c4[:3]
+    if aniso:
+        cam = anisotropic(cam)
     P1 = cfg.params(seed=1)
     tg = TrainStep(P1, [cam], [torch.zeros(cfg.H, cfg.W, 3)], K=cfg.K, S=cfg.S, k=cfg.k)
     target = tg.forward(0).clone()
@@ -90,7 +95,8 @@ def test_c4_training_step(c4):
     _, _, gref = oracle_render_chunked(P, cam_dict(cam), tmap, bins, cfg.k, R=gimg)
     err = max_abs(ts.image, img)
     lg = float(ts.loss())
-    print(f"[c4 step] image max|err| {err:.2e}, loss {lg:.6f} vs {float(L):.6f}", flush=True)
+    print(f"[c4 step aniso={aniso}] image max|err| {err:.2e}, loss {lg:.6f} vs {float(L):.6f}",
+          flush=True)
     assert err <= 1e-4
     assert abs(lg - float(L)) <= 1e-5
     gP = ts.gparams.cpu()
@@ -102,7 +108,7 @@ def test_c4_training_step(c4):
     Pa = P.clone().double()
     m, v = torch.zeros_like(Pa), torch.zeros_like(Pa)
     oadam.adam_step(Pa, m, v, gP.double(), lr_vector(device="cpu").double(), 1)
-    assert max_abs(ts.P, Pa) <= 1e-6
+    assert update_error_ok(ts.P, P, Pa) == 0
 
 
 @pytest.fixture(scope="module")
@@ -137,13 +143,22 @@ def test_c5_forward_full_frame(c5):
         assert max_abs(den, rden) <= tol * float(rden.abs().max()), name
 
 
-def test_c5_fused_backward_sampled_tiles(c5):
+@pytest.mark.parametrize("fwd", ["fp32", "bf16"])
+def test_c5_fused_backward_sampled_tiles(c5, fwd):
     """The fused backward (what the step runs) on the heaviest tiles, the tiles where the
     matrix-core and VALU forwards differ most, and random tiles: per-slot gradients of
-    (a, b, c, mu_x, mu_y, col_o, o_col) against oracle autograd."""
+    (a, b, c, mu_x, mu_y, col_o, o_col) against oracle autograd.  fwd = "bf16": the backward is
+    fed the image and den of the bf16 matrix-core forward, as the G = 1M bf16 step runs it; its
+    contract is the bf16 render's, 1e-2 (image and relative L2 of the gradients)."""
     cfg, P, cam, camera, proj, keep, idx, valid, count, inv, order, bg = c5
     T = idx.shape[0]
-    img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k, order=order)
+    tol = 1e-3 if fwd == "fp32" else 1e-2
+    if fwd == "fp32":
+        img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k,
+                                     order=order)
+    else:
+        img, den = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, cfg.k,
+                                        order=order, bf16=True)
     g = torch.Generator().manual_seed(43)
     R = torch.randn(cfg.H, cfg.W, 3, generator=g)
     gslot = torch.zeros(T, cfg.K, 9, device="cuda")
@@ -169,7 +184,7 @@ def test_c5_fused_backward_sampled_tiles(c5):
                               torch.ones(3, dtype=torch.float64))
     pix = tmap.gidx.reshape(T, -1)[sel]
     mine = img.reshape(-1, 3)[pix.reshape(-1).cuda()].reshape(C.shape)
-    assert max_abs(mine, C) <= 1e-4
+    assert max_abs(mine, C) <= (1e-4 if fwd == "fp32" else 1e-2)
     (C * R.reshape(-1, 3)[pix.reshape(-1)].reshape(C.shape).double()).sum().backward()
     gs = gslot.cpu()[sel][vv]
     for name, mine_g, ref_g in (("conic", gs[:, 0:3], conic.grad[vv]),
@@ -177,8 +192,8 @@ def test_c5_fused_backward_sampled_tiles(c5):
                                 ("col_o", gs[:, 5:8], colo.grad[vv]),
                                 ("o_col", gs[:, 8], ocol.grad[vv])):
         e = rel_l2(mine_g, ref_g)
-        print(f"[c5] {len(sel)} tiles d{name}: rel L2 {e:.2e}", flush=True)
-        assert e <= 1e-3, name
+        print(f"[c5 {fwd}] {len(sel)} tiles d{name}: rel L2 {e:.2e}", flush=True)
+        assert e <= tol, name
 
 
 @pytest.mark.parametrize("H,W", [(800, 800), (832, 1264), (1072, 1920)])
@@ -267,3 +282,82 @@ def test_nan_covariance_poisons_its_tiles():
     assert bool(torch.isnan(gP[17]).all())
     assert bool(torch.isfinite(gP[clean]).all()) and bool(torch.isfinite(gref[clean]).all())
     assert rel_l2(gP[clean], gref[clean]) <= 1e-3
+
+
+def test_overflowing_theta_terms_follow_torch_relu():
+    """A gaussian with a finite theta whose terms overflow at some pixels: conic a = -3e38,
+    c = 3e38, b = 0 at k = 1, mean at the origin of tile (3, 2) (G = 2000, 128 x 128).  In that
+    tile theta0 = 3e38, theta1 = -3e38: u = +inf - inf = NaN where lx, ly >= 1.5, +inf where
+    only lx >= 1.5, -inf where only ly >= 1.5 -- torch.relu keeps the NaN and maps -inf to 0.
+    In the neighbouring tiles the folded mean overflows theta3..5 to infinities (some tiles'
+    theta sums are NaN: poisoned whole; others give NaN or -inf per pixel).  Every forward kernel
+    gives the fp32 oracle's NaN set and its values elsewhere (pixel (48, 32) left out: there u is
+    7.5e37 - 7.5e37 + 1, which the order of the sum decides); the backward writes NaN gradients
+    for every kept slot of a tile with a NaN pixel and the oracle's gradients elsewhere."""
+    cfg, P, cam = config_inputs("c1_ref")
+    k, bad = 1.0, 5
+    camera = cam.device_block("cuda")
+    proj, keep = kernels.geom_fwd(P.cuda(), camera)
+    row = proj[bad].clone()
+    row[0:5] = torch.tensor([48.0, 32.0, -3e38, 0.0, 3e38])
+    proj[bad] = row
+    keep[bad] = 1
+    T = (cfg.H // cfg.S) * (cfg.W // cfg.S)
+    inv = torch.empty(cfg.G, 9, device="cuda", dtype=torch.int32)
+    order = torch.empty(T, device="cuda", dtype=torch.int32)
+    idx, valid, count, ncand = kernels.assign_bins(proj[:, 0:2], keep, cfg.H, cfg.W, cfg.S, cfg.K,
+                                                   cfg.span, inv=inv, order=order)
+    bg = torch.tensor(BG, device="cuda")
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    pc = proj.cpu()
+    pr = dict(mu2d=pc[:, 0:2], conic=pc[:, 2:5], color_o=pc[:, 6:9], o_col=pc[:, 9])
+    ref, rden = oracle_render_chunked(None, None, tmap, (idx, valid), k, proj=pr,
+                                      dtype=torch.float32)
+    keep_px = torch.ones(cfg.H, cfg.W, dtype=torch.bool)
+    keep_px[32, 48] = False
+    nan_ref = torch.isnan(ref).any(-1) & keep_px
+    assert bool(nan_ref.any()) and bool((~torch.isnan(ref).any(-1)).any())
+    th, col, oc = kernels.theta_gather(proj, idx, valid, cfg.H, cfg.W, cfg.S, k)
+    outs = {"tile": kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, order=order),
+            "theta": kernels.splat_fwd_theta(th, col, oc, bg, cfg.H, cfg.W, cfg.S),
+            "mx": kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k,
+                                       order=order)}
+    for name, (img, den) in outs.items():
+        im = img.cpu()
+        nan_gpu = torch.isnan(im).any(-1) & keep_px
+        print(f"[overflow] {name}: NaN pixels {int(nan_gpu.sum())} (oracle {int(nan_ref.sum())}),"
+              f" differing {int((nan_gpu != nan_ref).sum())}", flush=True)
+        assert torch.equal(nan_gpu, nan_ref), name
+        fin = keep_px & ~nan_ref
+        assert max_abs(im[fin], ref[fin]) <= 1e-4, name
+    img, den = outs["tile"]
+    R = torch.randn(cfg.H, cfg.W, 3, generator=torch.Generator().manual_seed(46))
+    gslot = torch.zeros(T, cfg.K, 9, device="cuda")
+    kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R.cuda(),
+                      gslot=gslot, order=order)
+    gs, vv = gslot.cpu(), valid.cpu().bool()
+    nan_tile = torch.isnan(ref.reshape(-1, 3)[tmap.gidx].reshape(T, -1)).any(1)
+    assert int(nan_tile.sum()) >= 3
+    assert bool(torch.isnan(gs[nan_tile][vv[nan_tile]]).all())
+    clean = ~nan_tile
+    assert bool(torch.isfinite(gs[clean][vv[clean]]).all())
+    # the clean tiles' slot gradients against fp64 oracle autograd (no overflow there)
+    ii = idx.cpu().long()[clean]
+    vf = vv[clean].double()
+    pd = pc.double()
+    conic = pd[:, 2:5][ii].clone().requires_grad_(True)
+    mu = pd[:, 0:2][ii].clone().requires_grad_(True)
+    colo = pd[:, 6:9][ii].clone().requires_grad_(True)
+    ocol = pd[:, 9][ii].clone().requires_grad_(True)
+    theta = osplat.theta_u_gathered(conic, mu, tmap.origins.double()[clean], k) * vf[:, None]
+    C, _ = osplat.splat_tiles(theta, colo * vf[..., None], (ocol * vf)[..., None],
+                              tmap.Phi.double(), torch.tensor(BG[0], dtype=torch.float64),
+                              torch.ones(3, dtype=torch.float64))
+    pix = tmap.gidx.reshape(T, -1)[clean]
+    (C * R.reshape(-1, 3)[pix.reshape(-1)].reshape(C.shape).double()).sum().backward()
+    gc = gs[clean][vv[clean]]
+    for name, mine_g, ref_g in (("conic", gc[:, 0:3], conic.grad[vv[clean]]),
+                                ("mean2d", gc[:, 3:5], mu.grad[vv[clean]]),
+                                ("col_o", gc[:, 5:8], colo.grad[vv[clean]]),
+                                ("o_col", gc[:, 8], ocol.grad[vv[clean]])):
+        assert rel_l2(mine_g, ref_g) <= 1e-3, name

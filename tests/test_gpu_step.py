@@ -2,7 +2,7 @@
 import pytest
 import torch
 
-from helpers import cam_dict, config_inputs, rel_l2
+from helpers import cam_dict, config_inputs, rel_l2, update_error_ok
 from oracle import adam as oadam
 from oracle import binning as obin
 from oracle import pipeline as opipe
@@ -11,6 +11,9 @@ from ttsplat import kernels
 from ttsplat.step import TrainStep, lr_vector
 
 pytestmark = pytest.mark.gpu
+
+GROUPS = {"means": slice(0, 3), "quats": slice(3, 7), "scales": slice(7, 10),
+          "color": slice(10, 13), "opacity": slice(13, 14)}
 
 
 def target_for(cfg, cam):
@@ -245,3 +248,84 @@ def test_run_graphs_match_single_steps(bin_every):
                  (runs.step_block, single.step_block)):
         assert torch.equal(a, b)
     assert float(runs.loss()) == float(single.loss())
+
+
+def test_bf16_step_gradient_matches_oracle():
+    """The gradient the bf16 step trains on -- the bf16 matrix-core forward, then the fp32 loss
+    gradient and fp32 splat backward on that forward's image and den -- against fp64 oracle
+    autograd on the same bins (G = 2000, 128 x 128): within 1e-2 relative L2 per parameter
+    group, the bf16 render's contract; the loss within 1e-3; the Adam update applied to the
+    gradient the kernel received, per entry."""
+    cfg, P, cam = config_inputs("c2")
+    tgt = target_for(cfg, cam)
+    ts = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, dtype="bf16", keep_grad=True)
+    ts.enqueue(0)
+    torch.cuda.synchronize()
+    bins = (ts.idx.cpu().long(), ts.valid.cpu().bool())
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    img, L, g, _ = opipe.render_and_grad(P.double(), cam_dict(cam), tmap, tgt.cpu().double(),
+                                         K=cfg.K, k=cfg.k, bins=bins)
+    err = float((ts.image.cpu().double() - img).abs().max())
+    dl = abs(float(ts.loss()) - float(L))
+    print(f"[c2 bf16 step] image max|err| {err:.2e}, |dloss| {dl:.2e}", flush=True)
+    assert err <= 1e-2 and dl <= 1e-3
+    gP = ts.gparams.cpu()
+    for name, sl in GROUPS.items():
+        e = rel_l2(gP[:, sl], g[:, sl])
+        print(f"[c2 bf16 step] d{name}: rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-2, name
+    Pa, m, v = P.clone().double(), torch.zeros(P.shape, dtype=torch.float64), \
+        torch.zeros(P.shape, dtype=torch.float64)
+    oadam.adam_step(Pa, m, v, gP.double(), lr_vector(device="cpu").double(), 1)
+    assert update_error_ok(ts.P, P, Pa) == 0
+
+
+def test_fp32_step_gradient_matches_oracle():
+    """The fp32 step's gradient (G = 2000, 128 x 128) against fp64 oracle autograd on the same
+    bins: within 1e-3 relative L2 per parameter group; the fused Adam update per entry."""
+    cfg, P, cam = config_inputs("c1_ref")
+    tgt = target_for(cfg, cam)
+    ts = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, keep_grad=True)
+    ts.enqueue(0)
+    torch.cuda.synchronize()
+    bins = (ts.idx.cpu().long(), ts.valid.cpu().bool())
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    _, _, g, _ = opipe.render_and_grad(P.double(), cam_dict(cam), tmap, tgt.cpu().double(),
+                                       K=cfg.K, k=cfg.k, bins=bins)
+    gP = ts.gparams.cpu()
+    for name, sl in GROUPS.items():
+        e = rel_l2(gP[:, sl], g[:, sl])
+        print(f"[c1_ref step] d{name}: rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-3, name
+    Pa, m, v = P.clone().double(), torch.zeros(P.shape, dtype=torch.float64), \
+        torch.zeros(P.shape, dtype=torch.float64)
+    oadam.adam_step(Pa, m, v, gP.double(), lr_vector(device="cpu").double(), 1)
+    assert update_error_ok(ts.P, P, Pa) == 0
+
+
+def test_render_between_steps_with_bin_every():
+    """bin_every = 5: a step, a render of another camera that rebins without the inverse table
+    (forward(grads=False)), then a step.  The render replaced the shared bins, so the second step
+    rebins; its gradient matches the oracle's on the bins it used (with the render's bins and
+    the first step's inverse table the slot gather would hand gaussians other slots' gradients)."""
+    from ttsplat import scenes
+    from ttsplat.camera import pinhole
+    cfg, P, _ = config_inputs("c1_ref")
+    cams = [pinhole(cfg.H, cfg.W, e) for e in scenes.orbit_eyes(2)]
+    tgts = [target_for(cfg, c) for c in cams]
+    ts = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5, keep_grad=True)
+    ts.capture()
+    ts.step(0)
+    ts.forward(1, grads=False)
+    P1 = ts.P.cpu().clone()
+    ts.step(0)
+    torch.cuda.synchronize()
+    bins = (ts.idx.cpu().long(), ts.valid.cpu().bool())
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    _, _, g, _ = opipe.render_and_grad(P1.double(), cam_dict(cams[0]), tmap,
+                                       tgts[0].cpu().double(), K=cfg.K, k=cfg.k, bins=bins)
+    gP = ts.gparams.cpu()
+    for name, sl in GROUPS.items():
+        e = rel_l2(gP[:, sl], g[:, sl])
+        print(f"[bin_every render] d{name}: rel L2 {e:.2e}", flush=True)
+        assert e <= 1e-3, name

@@ -301,20 +301,35 @@ def test_loss_window_size_rule():
 
 
 # ------------------------------------------------------------------------------------ adam
-def test_adam_matches_torch_optim():
-    g = torch.Generator().manual_seed(5)
-    p0 = torch.randn(50, 14, generator=g, dtype=DT)
-    grads = [torch.randn(50, 14, generator=g, dtype=DT) for _ in range(5)]
-    lr = torch.full((14,), 1e-3, dtype=DT)
+def adam_case(seed, n=50, steps=5, dtype=DT):
+    """p0, per-step gradients whose magnitudes span 1e-9 .. 1 (so eps = 1e-8 decides the
+    update of the smallest ones), and the per-column learning rates."""
+    g = torch.Generator().manual_seed(seed)
+    p0 = torch.randn(n, 14, generator=g, dtype=dtype)
+    scale = 10.0 ** (-9.0 * torch.rand(n, 14, generator=g, dtype=dtype))
+    grads = [torch.randn(n, 14, generator=g, dtype=dtype) * scale for _ in range(steps)]
+    lr = torch.full((14,), 1e-3, dtype=dtype)
     lr[:3] = 1.6e-4
+    return p0, grads, lr
+
+
+def test_adam_matches_torch_optim():
+    p0, grads, lr = adam_case(5)
     p, m, v = p0.clone(), torch.zeros_like(p0), torch.zeros_like(p0)
     for t, gr in enumerate(grads, 1):
         oadam.adam_step(p, m, v, gr, lr, t)
     ref = oadam.torch_adam_reference(p0, grads, lr)
-    assert torch.allclose(p, ref, atol=1e-12)
-    # first step moves every entry by ~lr (|m/sqrt(v)| = 1)
+    # the updates, not the parameters: |update| ~ lr << |p|
+    assert torch.allclose(p - p0, ref - p0, rtol=1e-9, atol=0.0)
+    # the inputs are sensitive to eps: ten times eps moves the small-gradient updates
+    pe, me, ve = p0.clone(), torch.zeros_like(p0), torch.zeros_like(p0)
+    for t, gr in enumerate(grads, 1):
+        oadam.adam_step(pe, me, ve, gr, lr, t, eps=1e-7)
+    assert not torch.allclose(pe - p0, ref - p0, rtol=1e-3, atol=0.0)
+    # with unit-scale gradients the first step moves every entry by ~lr (|m/sqrt(v)| = 1)
+    g1 = torch.randn(50, 14, generator=torch.Generator().manual_seed(6), dtype=DT)
     p1, m1, v1 = p0.clone(), torch.zeros_like(p0), torch.zeros_like(p0)
-    oadam.adam_step(p1, m1, v1, grads[0], lr, 1)
+    oadam.adam_step(p1, m1, v1, g1, lr, 1)
     assert torch.allclose((p0 - p1).abs(), lr.expand_as(p0), rtol=1e-4)
 
 

@@ -117,13 +117,25 @@ def _scipy_rot(q_wxyz):
     return torch.tensor(Rotation.from_quat([x, y, z, w]).as_matrix(), dtype=DT)
 
 
-def test_ewa_off_axis_matches_autograd_of_the_pinhole_map():
+def anisotropic(cam, ratio=1.13, px=0.46, py=0.53):
+    """The same pose with fx = ratio * fy and the principal point off the image centre (at
+    px * W, py * H), as COLMAP's PINHOLE / OPENCV models give (spike/data.py:127-150)."""
+    return {**cam, "fx": ratio * cam["fy"], "cx": px * cam["W"], "cy": py * cam["H"]}
+
+
+@pytest.mark.parametrize("aniso", [False, True], ids=["fx=fy", "fx=1.13fy"])
+def test_ewa_off_axis_matches_autograd_of_the_pinhole_map(aniso):
     """At points well off the optical axis: mu2d = pi(mu_cam) with pi(x, y, z) =
     (fx x / z + cx, fy y / z + cy), J = d pi / d mu_cam (autograd), Sigma2d = J Sigma_cam J^T +
-    0.3 I with Sigma_cam = R_v R diag(s^2) R^T R_v^T (R from scipy), conic = Sigma2d^-1."""
+    0.3 I with Sigma_cam = R_v R diag(s^2) R^T R_v^T (R from scipy), conic = Sigma2d^-1.
+    With fx != fy and an off-centre principal point, fx in place of fy (or cx in place of cy)
+    anywhere in the projection or its Jacobian fails."""
     gen = torch.Generator().manual_seed(21)
     cam = ogeo.make_camera(96, 160, (0.4, -0.3, 2.8))
     cam = {k: (v.to(DT) if torch.is_tensor(v) else v) for k, v in cam.items()}
+    if aniso:
+        cam = anisotropic(cam)
+        assert abs(cam["fx"] - cam["fy"]) > 0.1 * cam["fy"] and cam["cx"] != cam["W"] / 2
     G = 12
     P = torch.zeros(G, 14, dtype=DT)
     P[:, 0:3] = torch.rand(G, 3, generator=gen, dtype=DT) * 1.6 - 0.8

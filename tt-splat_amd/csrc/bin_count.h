@@ -234,7 +234,10 @@ __device__ __forceinline__ void count_body(const float (&mx)[PER], const float (
 
 // Host side: the fused geometry forward + count pass (geometry.hip), for count blocks of
 // CountSmall (count_block(G) == CountSmall::kBlock); proj/keep as tts_geom_fwd_ex, mat and
-// cell_slot as k_bin_count.
+// cell_slot as k_bin_count.  geom_fwd_count_lds: its dynamic LDS request in bytes; callers fall
+// back to the two-kernel path when that exceeds kMaxLdsBytes (one workgroup's LDS on gfx950).
+constexpr size_t kMaxLdsBytes = 160 * 1024;
+size_t geom_fwd_count_lds(int NB, int Tpad);
 int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degree,
                           const float* depth_bt, int G, const float* camera, float near_z,
                           float blur, float* proj, uint8_t* keep, int32_t* step_adv, float b1,

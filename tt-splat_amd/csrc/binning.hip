@@ -1424,7 +1424,8 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
     return TTS_EWORKSPACE;
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
-  const bool fused = G > 0 && ws.cblock == CountSmall::kBlock;
+  const bool fused = G > 0 && ws.cblock == CountSmall::kBlock &&
+                     geom_fwd_count_lds(ws.NB, ws.Tpad) <= kMaxLdsBytes;
   const int e = fused ? launch_geom_fwd_count(params, sh_rest, sh_degree, depth_bt, G, camera,
                                                near_z, blur, proj, keep, step_adv, beta1, beta2,
                                                ntx, nty, static_cast<float>(S), span, ws.NB,

@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void k_render_dense(const float* __restrict__ 
         const float2 O = s_o[j];
         const float dx = px - A.x, dy = py - A.y;
         const float Q = (A.z * dx + A.w * dy) * dx + (B.x * dy) * dy;
-        const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
+        const float r = relu_nan(1.0f - Q * inv_k);
         float w = r * r;
         if (ARM == kArmSZ && pass == 0) {
           nd += w * O.x;
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void k_wsr_dense(const float* __restrict__ the
     for (int j = 0; j < n; ++j) {
       const float4 A = s_a[j], B = s_b[j], Cc = s_c[j];
       const float u = f[0] * A.x + f[1] * A.y + f[2] * A.z + f[3] * A.w + f[4] * B.x + f[5] * B.y;
-      const float r = fmaxf(u, 0.0f);
+      const float r = relu_nan(u);
       const float w = r * r;
       nr += w * Cc.x;
       ng += w * Cc.y;
@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void k_softz_pre(const float* __restrict__ pro
       const float2 O = s_o[j];
       const float dx = px - A.x, dy = py - A.y;
       const float Q = (A.z * dx + A.w * dy) * dx + (B.x * dy) * dy;
-      const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
+      const float r = relu_nan(1.0f - Q * inv_k);
       const float h = sigmoidf_(-beta * (O.y - zs));
       Z += r * r * (q0 * B.y + q1 * B.z + q2 * B.w + q3 * O.x) * h * (1.0f - h);
     }
@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void k_render_dense_bwd(
       const float2 xy = s_xy[j];
       const float dx = xy.x - mx, dy = xy.y - my;
       const float Q = (a * dx + b2 * dy) * dx + (c * dy) * dy;
-      const float r = fmaxf(1.0f - Q * inv_k, 0.0f);
+      const float r = relu_nan(1.0f - Q * inv_k);
       const float w = r * r;
       const float gw = q.x * cr + q.y * cg + q.z * cb + q.w * oc;  // dL/dw_geo of arm A
       float dw;                                                   // dL/dw_geo of this arm
@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256) void k_wsr_dense_bwd(
       const float2 fb2 = s_fb[j];
       const float u = fa2.x * th[0] + fa2.y * th[1] + fa2.z * th[2] + fa2.w * th[3] +
                       fb2.x * th[4] + fb2.y * th[5];
-      const float r = fmaxf(u, 0.0f);
+      const float r = relu_nan(u);
       const float w = r * r;
       gr += w * q.x;
       gg += w * q.y;

@@ -1014,15 +1014,21 @@ __global__ __launch_bounds__(256) void k_zero(float* __restrict__ buf, int64_t n
   if (i < n) buf[i] = 0.0f;
 }
 
+// means + keep flags of 512 gaussians, then the row staging or the count histogram
+size_t geom_fwd_count_lds(int NB, int Tpad) {
+  const size_t stage = sizeof(float) * 2 * kGeoBlock * (15 + 13);
+  const size_t cnt = sizeof(int) * ((size_t)Tpad + (size_t)CountFused::kWaves * NB);
+  return (sizeof(float2) + 1) * 2 * kGeoBlock + (stage > cnt ? stage : cnt);
+}
+
 int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degree,
                           const float* depth_bt, int G, const float* camera, float near_z,
                           float blur, float* proj, uint8_t* keep, int32_t* step_adv, float b1,
                           float b2, int ntx, int nty, float S, int span, int NB, int Tpad,
                           int* mat, int2* cell_slot, hipStream_t stream) {
   const int nblk = (G + CountFused::kBlock - 1) / CountFused::kBlock;
-  const size_t stage = sizeof(float) * 2 * kGeoBlock * (15 + 13);
-  const size_t cnt = sizeof(int) * ((size_t)Tpad + (size_t)CountFused::kWaves * NB);
-  const size_t lds = (sizeof(float2) + 1) * 2 * kGeoBlock + (stage > cnt ? stage : cnt);
+  const size_t lds = geom_fwd_count_lds(NB, Tpad);
+  if (lds > kMaxLdsBytes) return TTS_EINVAL;  // callers check first and take the two-kernel path
   const bool sh = sh_degree > 0;
   const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count<true>)
                       : reinterpret_cast<const void*>(&k_geom_fwd_count<false>);

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
       const float u = A.x * xx[i] + A.y * yy[i] + A.z * xy[i] + A.w * lx[i] + B.x * ly[i] + B.y;
-      const float r = fmaxf(u, 0.0f);
+      const float r = relu_bits(u);
       const float w = r * r;
       ar[i] += w * C.x;
       ag[i] += w * C.y;
@@ -277,7 +277,7 @@ __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const flo
           for (int x8 = 0; x8 < 8; ++x8) {
             const float lx = xbf + ((float)x8 + 0.5f);
             const float u = (A.x * lx + cc1) * lx + cc0;
-            const float r = fmaxf(u, 0.0f);
+            const float r = relu_bits(u);
             const float w = r * r;
             const float4 q = row[xb + x8];
             const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
@@ -608,7 +608,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
       float w[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float r0 = fmaxf(u0[e], 0.0f), r1 = fmaxf(u1[e], 0.0f);
+        const float r0 = relu_bits(u0[e]), r1 = relu_bits(u1[e]);
         w[e] = r0 * r0;
         w[4 + e] = r1 * r1;
       }
@@ -755,7 +755,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
       for (int m = 0; m < 4; ++m) {
         const float ly = lyq + (float)(4 * m);
         const float u = fmaf(fmaf(th.y, ly, P), ly, Q);
-        const float rl = __int_as_float(max(__float_as_int(u), 0));
+        const float rl = relu_bits(u);
         const float w = rl * rl;
         acc[m][0] += w * cl.x;
         acc[m][1] += w * cl.y;

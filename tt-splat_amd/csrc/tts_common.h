@@ -33,6 +33,19 @@ __device__ __forceinline__ long long f2i64_x86(float f) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// relu with torch's NaN rule (torch.relu and clamp(min=0) keep a NaN):
+//   relu_nan: u <= 0 -> +0, else u; a NaN of either sign fails the compare and passes through.
+//   relu_bits: one integer max on the bit pattern.  Equal to relu_nan for every u except a NaN
+//   with the sign bit set, which it maps to +0.  The binned splat kernels use it: the NaN the GPU
+//   generates (inf - inf, 0 * inf, as when theta terms overflow at some pixels of a tile) is the
+//   default NaN, sign bit clear, so it passes through as torch.relu keeps it; a u can only be a
+//   NaN with the sign bit set when theta holds a NaN, and those tiles are written NaN whole by
+//   the kernels' poison rule (a NaN theta makes u NaN at every pixel).
+__device__ __forceinline__ float relu_nan(float u) { return u <= 0.0f ? 0.0f : u; }
+__device__ __forceinline__ float relu_bits(float u) {
+  return __int_as_float(max(__float_as_int(u), 0));
+}
+
 // Wave64 inclusive prefix sum of an int, on DPP lane moves (VALU only; a shuffle would take six
 // dependent LDS-crossbar round trips): Hillis-Steele inside each row of 16 lanes (row_shr 1, 2,
 // 4, 8, lanes shifted in from outside the row read 0), then lane 15 of rows 0 and 2 is added

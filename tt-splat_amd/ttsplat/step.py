@@ -200,10 +200,21 @@ class TrainStep:
         rebin=False: the bins last computed are reused (the binning kernels are not run).
         grads=False: a render only -- the binning skips the inverse table (gaussian -> slots)
         and the splat kernel the per-pixel den, which only the backward reads (self.den is
-        left as it was); a later step that reuses these bins must not follow."""
+        left as it was).  A forward that rebins replaces the shared bin table (with
+        grads=False, without its inverse table), so the next step() rebins whatever its
+        bin_every count says."""
+        self._forward(ci, advance, rebin, grads)
+        if rebin:
+            self._force_rebin = True
+        return self.image
+
+    def _forward(self, ci, advance=False, rebin=True, grads=True, camera=None):
+        """forward() as a training step enqueues it (no forced rebin); camera: a [16] device
+        camera block to render instead of camera ci's."""
         adv = self.step_block if advance else None
+        cam = self.cams[ci] if camera is None else camera
         if rebin:   # one call: the binning's count pass rides on the geometry launch
-            kernels.geom_fwd_assign_bins(self.P, self.cams[ci], self.H, self.W, self.S, self.K,
+            kernels.geom_fwd_assign_bins(self.P, cam, self.H, self.W, self.S, self.K,
                                          self.span, proj=self.proj, keep=self.keep,
                                          sh_rest=self.sh, sh_degree=self.sh_degree,
                                          depth_bt=self.dw, advance=adv,
@@ -213,7 +224,7 @@ class TrainStep:
                                          order=self.order, slot_rec=self.slot_rec,
                                          pos_count=self.pos_count)
         else:
-            kernels.geom_fwd(self.P, self.cams[ci], proj=self.proj, keep=self.keep,
+            kernels.geom_fwd(self.P, cam, proj=self.proj, keep=self.keep,
                              sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
                              advance=adv)
         if self.dtype == "bf16" and rebin and self.use_rec:
@@ -239,7 +250,7 @@ class TrainStep:
 
     def _view_backward(self, ci, advance=False, rebin=True):
         """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
-        self.forward(ci, advance, rebin)
+        self._forward(ci, advance, rebin)
         kernels.loss_grad_stats(self.image, self.targets[ci], self.target_stats[ci], self.lam,
                                 self.gimage, self.partials)
         if rebin and self.use_rec:
