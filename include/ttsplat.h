@@ -248,9 +248,20 @@ size_t tts_loss_workspace_bytes(int H, int W);
 int tts_loss_partials_count(int H, int W, int* n_ssim);
 
 /* The target's SSIM statistics (stats: tts_loss_stats_bytes bytes, written whole), computed
- * once per target: the per-view target maps muy/sy of tools/resident_traced.py:431-464.
- * Size limits as tts_loss_grad. */
+ * whenever the target changes: the target maps muy/sy that tools/resident_traced.py:305-325
+ * builds and recompute_gt_stats refreshes on each view switch (:677-678).  Size limits as
+ * tts_loss_grad. */
 int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipStream_t stream);
+
+/* A training target composited over a random background (the --random-bg mode of
+ * tools/resident_traced.py:182-185,671-674, whose background is torch.rand(3) on the host):
+ * bg = three uniforms in (0,1), ((w >> 8) + 0.5) * 2^-24 of words 0..2 of Philox4x32-10 with
+ * counter (view, step[0], 4, 0) and key (seed, 0), step read on the device (a replayed graph
+ * draws anew each step); target[H,W,3] = rgba_pm[..., c] + rgba_pm[..., 3] * bg[c], where
+ * rgba_pm [H,W,4] (16-byte aligned) holds (alpha r, alpha g, alpha b, 1 - alpha); bg4[1..3] = bg
+ * (the splat kernels' numerator background colour; bg4[0] = w_b is not written). */
+int tts_composite_random_bg(const float* rgba_pm, int H, int W, const int32_t* step, int view,
+                            unsigned seed, float* bg4, float* target, hipStream_t stream);
 
 /* dL/dimage of L = (1-lambda)*mean|x-y| + lambda*(1 - mean SSIM(clamp(x,0,1), clamp(y,0,1))),
  * 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4, with the target's

@@ -16,15 +16,17 @@ from . import adam, loss, splat
 
 def render_and_grad(P, cam, tmap, target, R=1, K=128, k=4.0, blur_eps=0.3, near=0.2,
                     w_b_raw=-3.0, lambda_ssim=0.2, bins=None, span=2048, stable=False, rest=None,
-                    sh_degree=0, depth_bt=None):
+                    sh_degree=0, depth_bt=None, c_b=None):
     """Forward + loss + autograd backward.  Returns (img, loss, dL/dP[G,14], extras); with
     SH rest coefficients (rest [G,15,3], sh_degree > 0) extras["grest"] is dL/drest, with a
-    depth weight (depth_bt = (beta, tau)) extras["gdepth"] is dL/d(beta, tau)."""
+    depth weight (depth_bt = (beta, tau)) extras["gdepth"] is dL/d(beta, tau).  c_b: the
+    background colour (white if None; a random-background step's draw,
+    tools/resident_traced.py:671-674)."""
     Pg = P.detach().clone().requires_grad_(True)
     rg = None if rest is None else rest.detach().clone().requires_grad_(True)
     bt = (None if depth_bt is None
           else torch.as_tensor(depth_bt, dtype=P.dtype).detach().clone().requires_grad_(True))
-    img, ex = splat.render_binned(Pg, cam, tmap, R, K, k, blur_eps, near, w_b_raw, None, bins,
+    img, ex = splat.render_binned(Pg, cam, tmap, R, K, k, blur_eps, near, w_b_raw, c_b, bins,
                                   span, stable, return_all=True, rest=rg, sh_degree=sh_degree,
                                   depth_bt=bt)
     L = loss.loss_fn(img, target, lambda_ssim)

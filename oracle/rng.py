@@ -27,6 +27,7 @@ MASK = 0xFFFFFFFF
 TAG_SGLD = 1           # SGLD noise on the means
 TAG_RELOC_PICK = 2     # relocation: which live gaussian a dead slot copies
 TAG_RELOC_OFFSET = 3   # relocation: the position offset of the copy
+TAG_BG = 4             # random training background of a view
 
 
 def philox4x32_10(ctr, key):
@@ -75,3 +76,12 @@ def normals3(index, step, tag, seed):
 def uniform1(index, step, tag, seed):
     """One uniform in (0, 1) per index (word 0)."""
     return uniform(draws(index, step, tag, seed)[..., 0])
+
+
+def random_bg(view, step, seed):
+    """The background colour a random-background training step draws for `view` after `step`
+    completed steps: words 0..2 of Philox (view, step, TAG_BG, 0; key (seed, 0)) as uniforms in
+    (0, 1), rounded to fp32 (the reference draws torch.rand(3) on the host,
+    tools/resident_traced.py:672)."""
+    w = draws(np.array([view]), step, TAG_BG, seed)[0]
+    return uniform(w[:3]).astype(np.float32)

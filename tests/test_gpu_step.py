@@ -12,6 +12,10 @@ from ttsplat.step import TrainStep, lr_vector
 
 pytestmark = pytest.mark.gpu
 
+# the bf16 step's gradient contract against fp64 autograd: the bf16 render's image error (up to
+# ~5e-3 here) moves dL/dimage -- the L1 term's sign flips where |x - y| is below it -- and the
+# splat backward's C and den, so the gradient gets 2e-2 relative L2 per parameter group
+BF16_GRAD_TOL = 2e-2
 GROUPS = {"means": slice(0, 3), "quats": slice(3, 7), "scales": slice(7, 10),
           "color": slice(10, 13), "opacity": slice(13, 14)}
 
@@ -253,9 +257,9 @@ def test_run_graphs_match_single_steps(bin_every):
 def test_bf16_step_gradient_matches_oracle():
     """The gradient the bf16 step trains on -- the bf16 matrix-core forward, then the fp32 loss
     gradient and fp32 splat backward on that forward's image and den -- against fp64 oracle
-    autograd on the same bins (G = 2000, 128 x 128): within 1e-2 relative L2 per parameter
-    group, the bf16 render's contract; the loss within 1e-3; the Adam update applied to the
-    gradient the kernel received, per entry."""
+    autograd on the same bins (G = 2000, 128 x 128): within BF16_GRAD_TOL relative L2 per
+    parameter group; the image within the bf16 render's 1e-2; the loss within 1e-3; the Adam
+    update applied to the gradient the kernel received, per entry."""
     cfg, P, cam = config_inputs("c2")
     tgt = target_for(cfg, cam)
     ts = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, dtype="bf16", keep_grad=True)
@@ -270,10 +274,11 @@ def test_bf16_step_gradient_matches_oracle():
     print(f"[c2 bf16 step] image max|err| {err:.2e}, |dloss| {dl:.2e}", flush=True)
     assert err <= 1e-2 and dl <= 1e-3
     gP = ts.gparams.cpu()
-    for name, sl in GROUPS.items():
-        e = rel_l2(gP[:, sl], g[:, sl])
-        print(f"[c2 bf16 step] d{name}: rel L2 {e:.2e}", flush=True)
-        assert e <= 1e-2, name
+    errs = {name: rel_l2(gP[:, sl], g[:, sl]) for name, sl in GROUPS.items()}
+    print("[c2 bf16 step] rel L2 " + ", ".join(f"d{n} {e:.2e}" for n, e in errs.items()),
+          flush=True)
+    for name, e in errs.items():
+        assert e <= BF16_GRAD_TOL, name
     Pa, m, v = P.clone().double(), torch.zeros(P.shape, dtype=torch.float64), \
         torch.zeros(P.shape, dtype=torch.float64)
     oadam.adam_step(Pa, m, v, gP.double(), lr_vector(device="cpu").double(), 1)
@@ -329,3 +334,100 @@ def test_render_between_steps_with_bin_every():
         e = rel_l2(gP[:, sl], g[:, sl])
         print(f"[bin_every render] d{name}: rel L2 {e:.2e}", flush=True)
         assert e <= 1e-3, name
+
+
+def rgba_target(cfg, cam):
+    """An RGBA target: the seed-1 render with a soft-edged disc of alpha (0 outside, 1 inside,
+    partial on the rim)."""
+    rgb = target_for(cfg, cam).cpu()
+    yy, xx = torch.meshgrid(torch.arange(cfg.H, dtype=torch.float32),
+                            torch.arange(cfg.W, dtype=torch.float32), indexing="ij")
+    r = ((xx - 0.47 * cfg.W) ** 2 + (yy - 0.55 * cfg.H) ** 2).sqrt()
+    alpha = (1.2 - r / (0.3 * cfg.W)).clamp(0, 1)
+    return torch.cat([rgb, alpha[..., None]], -1)
+
+
+def test_random_bg_step_matches_oracle():
+    """random_bg: each step draws its background on the device (Philox keyed by the completed
+    steps, the view and the seed; a replayed graph draws anew), composites the RGBA target over
+    it and renders with it as c_b.  The draws equal the oracle's, the composited target is exact,
+    and the second step's image, loss and gradient match the oracle's step on that background."""
+    import numpy as np
+    from oracle import rng as orng
+    cfg, P, cam = config_inputs("c1_ref")
+    rgba = rgba_target(cfg, cam)
+    ts = TrainStep(P, [cam], [rgba], K=cfg.K, S=cfg.S, k=cfg.k, random_bg=True, bg_seed=7,
+                   keep_grad=True)
+    assert ts.stats_mode == "per_step"
+    ts.capture()
+    ts.step(0)
+    torch.cuda.synchronize()
+    bg1 = ts.bg.cpu().clone()
+    P1 = ts.P.cpu().clone()
+    ts.step(0)
+    torch.cuda.synchronize()
+    bg2 = ts.bg.cpu().clone()
+    for step, bg in ((0, bg1), (1, bg2)):
+        assert torch.equal(bg[1:], torch.from_numpy(orng.random_bg(0, step, 7))), step
+    assert not torch.equal(bg1, bg2)
+    pm = kernels.rgba_premult(rgba)
+    target = pm[..., :3] + pm[..., 3:4] * bg2[1:]
+    assert torch.equal(ts.target_buf.cpu(), target)
+    bins = (ts.idx.cpu().long(), ts.valid.cpu().bool())
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    img, L, g, _ = opipe.render_and_grad(P1.double(), cam_dict(cam), tmap, target.double(),
+                                         K=cfg.K, k=cfg.k, bins=bins, c_b=bg2[1:].double())
+    err = float((ts.image.cpu().double() - img).abs().max())
+    print(f"[random bg] bg {bg2[1:].tolist()}, image max|err| {err:.2e}", flush=True)
+    assert err <= 1e-4
+    assert abs(float(ts.loss()) - float(L)) <= 1e-5
+    gP = ts.gparams.cpu()
+    for name, sl in GROUPS.items():
+        assert rel_l2(gP[:, sl], g[:, sl]) <= 1e-3, name
+
+
+def test_per_step_target_stats_equal_per_view():
+    """target_stats = "per_step" (one statistics buffer, recomputed at every view backward, as
+    the reference's recompute_gt_stats) gives the per-view mode's state to the bit."""
+    from ttsplat import scenes
+    from ttsplat.camera import pinhole
+    cfg, P, _ = config_inputs("c1_ref")
+    cams = [pinhole(cfg.H, cfg.W, e) for e in scenes.orbit_eyes(3)]
+    tgts = [target_for(cfg, c) for c in cams]
+    a = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k)
+    b = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, target_stats="per_step")
+    b.capture()
+    for i in range(6):
+        a.step(i % 3)
+        b.step(i % 3)
+        assert float(a.loss()) == float(b.loss())
+    assert torch.equal(a.P, b.P)
+
+
+def test_eval_psnr_renders_on_white():
+    """eval_psnr: the binned render of each view on a white background against its image
+    (RGBA composited over white), psnr on clamped images; the training state is untouched and
+    the next step rebins."""
+    cfg, P, cam = config_inputs("c1_ref")
+    rgba = rgba_target(cfg, cam)
+    ts = TrainStep(P, [cam], [rgba], K=cfg.K, S=cfg.S, k=cfg.k, random_bg=True, bg_seed=3)
+    ts.capture()
+    for _ in range(5):
+        ts.step(0)
+    torch.cuda.synchronize()
+    state = [t.clone() for t in (ts.P, ts.m, ts.v, ts.step_block)]
+    psnr = ts.eval_psnr([cam], [rgba])
+    for t, s0 in zip((ts.P, ts.m, ts.v, ts.step_block), state):
+        assert torch.equal(t, s0)
+    white = rgba[..., :3] * rgba[..., 3:4] + (1 - rgba[..., 3:4])
+    tmap = obin.TileMap(cfg.H, cfg.W, cfg.S)
+    ref = osplat.render_binned(ts.P.cpu().double(), cam_dict(cam), tmap, K=cfg.K, k=cfg.k,
+                               stable=True)
+    mse = (ref.clamp(0, 1) - white.double().clamp(0, 1)).pow(2).mean()
+    want = float(-10 * torch.log10(mse))
+    print(f"[eval] psnr {psnr:.4f} dB, oracle {want:.4f} dB", flush=True)
+    assert abs(psnr - want) <= 1e-3
+    assert ts._force_rebin
+    ts.step(0)
+    torch.cuda.synchronize()
+    assert int(ts.step_block[0]) == 6

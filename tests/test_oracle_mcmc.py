@@ -135,3 +135,34 @@ def test_pick_targets_frequencies_follow_opacity():
     want = torch.zeros(7, dtype=D)
     want[alive] = o[alive] / o[alive].sum()
     assert torch.allclose(freq, want, atol=0.005)
+
+
+def test_random_background_draws():
+    """The random-background colour: three uniforms in (0, 1) per (view, step, seed), fp32,
+    different for another view, step or seed, uniform over many steps (mean 1/2, variance
+    1/12)."""
+    a = rng.random_bg(0, 5, 7)
+    assert a.dtype == np.float32 and a.shape == (3,)
+    assert bool(((a > 0) & (a < 1)).all())
+    for other in (rng.random_bg(1, 5, 7), rng.random_bg(0, 6, 7), rng.random_bg(0, 5, 8)):
+        assert not np.array_equal(a, other)
+    many = np.stack([rng.random_bg(0, s, 3) for s in range(20000)])
+    assert abs(float(many.mean()) - 0.5) < 0.01
+    assert abs(float(many.var()) - 1.0 / 12.0) < 0.005
+    w = rng.draws(np.array([0]), 5, rng.TAG_BG, 7)[0]
+    assert np.array_equal(a, rng.uniform(w[:3]).astype(np.float32))
+
+
+def test_rgba_premult_composites_over_a_background():
+    """(alpha r, alpha g, alpha b, 1 - alpha): alpha = 1 gives the colour, alpha = 0 the
+    background, and pm + (1 - alpha) bg is straight compositing."""
+    from ttsplat import kernels
+    gen = torch.Generator().manual_seed(3)
+    rgb = torch.rand(5, 7, 3, generator=gen)
+    alpha = torch.rand(5, 7, 1, generator=gen)
+    alpha[0, 0], alpha[0, 1] = 1.0, 0.0
+    pm = kernels.rgba_premult(torch.cat([rgb, alpha], -1))
+    bg = torch.tensor([0.2, 0.5, 0.9])
+    out = pm[..., :3] + pm[..., 3:4] * bg
+    assert torch.allclose(out, rgb * alpha + (1 - alpha) * bg, atol=1e-6)
+    assert torch.equal(out[0, 0], rgb[0, 0]) and torch.allclose(out[0, 1], bg)

@@ -31,9 +31,11 @@ __device__ __forceinline__ int quant_dist2(float mx, float my, int tx, int ty, f
   // dist2 = fl(fl(dx*dx) + fl(dy*dy)), no contraction (tools/m4_train_binned.py:112-114)
   const float cx = (static_cast<float>(tx) + 0.5f) * S;
   const float cy = (static_cast<float>(ty) + 0.5f) * S;
-  const float dx = __fsub_rn(mx, cx);
-  const float dy = __fsub_rn(my, cy);
-  const float d2 = __fadd_rn(__fmul_rn(dx, dx), __fmul_rn(dy, dy));
+  // plain operators: the pragma governs the expressions written in this scope (the bodies of
+  // __fmul_rn / __fadd_rn, plain * and + in a header, keep the including file's contraction)
+  const float dx = mx - cx;
+  const float dy = my - cy;
+  const float d2 = dx * dx + dy * dy;
   long long q = f2i64_x86(d2);
   return static_cast<int>(q < 0 ? 0 : (q > span - 1 ? span - 1 : q));
 }

@@ -2,10 +2,11 @@
 // SSIM: 11-tap gaussian window (sigma 1.5), valid borders, C1 = 1e-4, C2 = 9e-4
 // (spike/metrics.py:6-28; the manual gradient of tools/loss_manual.py:76-103).
 //
-// The target's statistics mu_y = G*y and s_y = G*y^2 - mu_y^2 depend on the target only: a
-// training loop computes them once per view (k_loss_target_stats, with a channel-planar copy
-// of the target), as the reference's resident trainer keeps muy/sy per view
-// (tools/resident_traced.py:431-464).  The step kernel then filters x, x^2 and xy only.
+// The target's statistics mu_y = G*y and s_y = G*y^2 - mu_y^2 depend on the target only:
+// k_loss_target_stats computes them (with a channel-planar copy of the target) whenever the
+// target changes -- the reference's resident trainer recomputes its muy/sy maps on each view
+// switch (recompute_gt_stats, tools/resident_traced.py:320-325,677-678); a caller may also keep
+// one set per view.  The step kernel then filters x, x^2 and xy only.
 //
 // k_loss_fused: a block owns a TH x 64 tile of gradient pixels of one colour channel and runs
 // the whole chain on it, the SSIM map region it needs (the tile plus the 10-pixel halo above and
@@ -146,6 +147,35 @@ __global__ __launch_bounds__(256) void k_loss_target_planar(const float* __restr
   yp[i] = y[i * 3];
   yp[n + i] = y[i * 3 + 1];
   yp[2 * n + i] = y[i * 3 + 2];
+}
+
+// Random-background compositing of a training target (the reference's --random-bg,
+// tools/resident_traced.py:182-185,671-674): bg = three uniforms from Philox4x32-10, counter
+// (view, step[0], kTagBg, 0), key (seed, 0) -- the step count is read on the device, so a
+// replayed graph draws a new background every step; target = premult + trans * bg per channel,
+// from rgba_pm [H,W,4] = (alpha r, alpha g, alpha b, 1 - alpha), each product and sum rounded
+// once as torch's CPU arithmetic does; bg4[1..3] = bg, the numerator background colour the splat
+// forward reads (bg4[0], w_b, is left alone).
+__global__ __launch_bounds__(256) void k_composite_random_bg(const float4* __restrict__ rgba_pm,
+                                                             int64_t n,
+                                                             const int32_t* __restrict__ step,
+                                                             uint32_t view, uint32_t seed,
+                                                             float* __restrict__ bg4,
+                                                             float* __restrict__ target) {
+#pragma clang fp contract(off)  // pm + tr * bg rounded twice, as torch's CPU ops round it
+  const Philox4 p = philox4x32_10(view, (uint32_t)step[0], kTagBg, 0u, seed, 0u);
+  const float b0 = (float)u01d(p.w[0]), b1 = (float)u01d(p.w[1]), b2 = (float)u01d(p.w[2]);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i == 0) {
+    bg4[1] = b0;
+    bg4[2] = b1;
+    bg4[3] = b2;
+  }
+  if (i >= n) return;
+  const float4 v = rgba_pm[i];
+  target[i * 3 + 0] = v.x + v.w * b0;
+  target[i * 3 + 1] = v.y + v.w * b1;
+  target[i * 3 + 2] = v.z + v.w * b2;
 }
 
 // ------------------------------------------------------------------ fused step kernel ------
@@ -456,6 +486,17 @@ int tts_loss_target_stats(const float* target, int H, int W, float* stats, hipSt
   const int64_t n = (int64_t)H * W;
   k_loss_target_planar<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
       target, n, stats + 6 * (size_t)(H - kHalo) * (size_t)(W - kHalo));
+  return launch_status();
+}
+
+int tts_composite_random_bg(const float* rgba_pm, int H, int W, const int32_t* step, int view,
+                            unsigned seed, float* bg4, float* target, hipStream_t stream) {
+  if (!rgba_pm || !step || !bg4 || !target || H <= 0 || W <= 0 || view < 0) return TTS_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(rgba_pm) & 15) != 0) return TTS_EINVAL;  // float4 rows
+  const int64_t n = (int64_t)H * W;
+  k_composite_random_bg<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      reinterpret_cast<const float4*>(rgba_pm), n, step, (uint32_t)view, (uint32_t)seed, bg4,
+      target);
   return launch_status();
 }
 

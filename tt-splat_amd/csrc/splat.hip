@@ -21,6 +21,8 @@
 // slots is a gather through the inverse bin table, in a fixed order, done by the geometry
 // backward).
 
+#include <type_traits>
+
 #include "tts_common.h"
 
 namespace tts {
@@ -67,6 +69,18 @@ __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, 
 __device__ __forceinline__ bool theta_poisons(const float4 ta, const float4 tb) {
   return __builtin_isnan(((ta.x + ta.y) + (ta.z + ta.w)) + (tb.x + tb.y));
 }
+// A slot whose u can be infinite or NaN at some pixel: some |theta| >= 1e34, an infinity or a
+// NaN.  Below that, at pixel coordinates under 32 every product, partial sum and u stays under
+// 3.2e37 < FLT_MAX whatever the order of evaluation, so u is finite and relu_bits is exact.  A
+// tile with such a slot walks with relu_nan: where u comes out NaN (inf - inf, in this kernel's
+// order of evaluation -- torch's own order is its BLAS's), the pixel is NaN, as torch.relu
+// keeps it, and -inf gives 0.  (The GPU's generated NaN can carry the sign bit, which
+// relu_bits would map to 0.)
+__device__ __forceinline__ bool theta_wild(const float4 ta, const float4 tb) {
+  const float m = fmaxf(fmaxf(fmaxf(fabsf(ta.x), fabsf(ta.y)), fmaxf(fabsf(ta.z), fabsf(ta.w))),
+                        fmaxf(fabsf(tb.x), fabsf(tb.y)));
+  return !(m < 1e34f) || theta_poisons(ta, tb);
+}
 
 __device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
                                            float oy, float inv_k, float4& ta, float4& tb,
@@ -103,7 +117,7 @@ __device__ __forceinline__ int load_slots_proj(const float* __restrict__ proj,
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, ox, oy, inv_k, ta, tb, cl);
-      *bad = *bad || theta_poisons(ta, tb);
+      *bad = *bad || theta_wild(ta, tb);
       sl.ta[pos] = ta;
       sl.tb[pos] = tb;
       sl.cl[pos] = cl;
@@ -131,7 +145,7 @@ __device__ __forceinline__ int load_slots_rec(const float* __restrict__ rec,
     if (s < nb) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, ox, oy, inv_k, ta, tb, cl);
-      *bad = *bad || theta_poisons(ta, tb);
+      *bad = *bad || theta_wild(ta, tb);
       sl.ta[s] = ta;
       sl.tb[s] = tb;
       sl.cl[s] = cl;
@@ -158,7 +172,7 @@ __device__ __forceinline__ void load_slots_theta(const OT* __restrict__ theta,
   for (int s = threadIdx.x; s < K; s += blockDim.x) {
     sl.ta[s] = make_float4(opf(th[s]), opf(th[K + s]), opf(th[2 * K + s]), opf(th[3 * K + s]));
     sl.tb[s] = make_float4(opf(th[4 * K + s]), opf(th[5 * K + s]), 0.0f, 0.0f);
-    *bad = *bad || theta_poisons(sl.ta[s], sl.tb[s]);
+    *bad = *bad || theta_wild(sl.ta[s], sl.tb[s]);
     const OT* c = col + ((int64_t)t * K + s) * 3;
     sl.cl[s] = make_float4(opf(c[0]), opf(c[1]), opf(c[2]), opf(oc[(int64_t)t * K + s]));
     sl.gid[s] = s;
@@ -188,7 +202,9 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
     load_slots_theta(theta, col, oc, t, K, sl, &bad);
     n = K;
   }
-  const bool poisoned = __syncthreads_or(bad);
+  // a tile with a wild slot (theta_wild) walks with relu_nan; a NaN or mixed-infinity theta
+  // then makes u NaN at every pixel (the monomials are positive), so its tile comes out NaN
+  const bool wild = __syncthreads_or(bad);
 
   float lx[PPT], ly[PPT], xx[PPT], yy[PPT], xy[PPT];
   float ar[PPT], ag[PPT], ab[PPT], ad[PPT];
@@ -202,30 +218,37 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
     xy[i] = lx[i] * ly[i];
     ar[i] = ag[i] = ab[i] = ad[i] = 0.0f;
   }
-  for (int s = 0; s < n; ++s) {
-    const float4 A = sl.ta[s], B = sl.tb[s], C = sl.cl[s];
+  auto walk = [&](auto exact) {
+    for (int s = 0; s < n; ++s) {
+      const float4 A = sl.ta[s], B = sl.tb[s], C = sl.cl[s];
 #pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const float u = A.x * xx[i] + A.y * yy[i] + A.z * xy[i] + A.w * lx[i] + B.x * ly[i] + B.y;
-      const float r = relu_bits(u);
-      const float w = r * r;
-      ar[i] += w * C.x;
-      ag[i] += w * C.y;
-      ab[i] += w * C.z;
-      ad[i] += w * C.w;
+      for (int i = 0; i < PPT; ++i) {
+        // one fixed order of evaluation (it decides where overflowing terms give NaN)
+        const float u = fmaf(A.x, xx[i], fmaf(A.y, yy[i], fmaf(A.z, xy[i],
+                             fmaf(A.w, lx[i], fmaf(B.x, ly[i], B.y)))));
+        const float r = decltype(exact)::value ? relu_nan(u) : relu_bits(u);
+        const float w = r * r;
+        ar[i] += w * C.x;
+        ag[i] += w * C.y;
+        ab[i] += w * C.z;
+        ad[i] += w * C.w;
+      }
     }
-  }
+  };
+  if (wild)
+    walk(std::true_type{});
+  else
+    walk(std::false_type{});
   const float wb = bg[0];
   const float cbr = wb * bg[1], cbg = wb * bg[2], cbb = wb * bg[3];
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
     const int p = threadIdx.x + 256 * i;
     const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
-    const float nanv = __builtin_nanf("");
-    const float d = poisoned ? nanv : ad[i] + wb;
-    image[pix * 3 + 0] = poisoned ? nanv : (ar[i] + cbr) / d;
-    image[pix * 3 + 1] = poisoned ? nanv : (ag[i] + cbg) / d;
-    image[pix * 3 + 2] = poisoned ? nanv : (ab[i] + cbb) / d;
+    const float d = ad[i] + wb;
+    image[pix * 3 + 0] = (ar[i] + cbr) / d;
+    image[pix * 3 + 1] = (ag[i] + cbg) / d;
+    image[pix * 3 + 2] = (ab[i] + cbb) / d;
     if (den_out) den_out[pix] = d;
   }
 }
@@ -608,7 +631,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_mx(
       float w[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float r0 = relu_bits(u0[e]), r1 = relu_bits(u1[e]);
+        // relu_nan: the matrix-core walk's relu is a small share of its VALU work
+        const float r0 = relu_nan(u0[e]), r1 = relu_nan(u1[e]);
         w[e] = r0 * r0;
         w[4 + e] = r1 * r1;
       }
@@ -689,7 +713,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
     if (v) {
       float4 ta, tb, cl;
       slot_from_rec(r0, r1, r2, oxf, oyf, inv_k, ta, tb, cl);
-      bad = bad || theta_poisons(ta, tb);
+      bad = bad || theta_wild(ta, tb);
       s_th[s] = ta;
       s_th2[s] = make_float2(tb.x, tb.y);
       s_col[s] = cl;
@@ -732,7 +756,9 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
     if (v || REC) gather(g, r0, r1, r2);
     stage(s, v, r0, r1, r2);
   }
-  bool poisoned = __syncthreads_or(bad);
+  // a wild slot (theta_wild) among slots 0..63: that walk uses relu_nan (a NaN or mixed-
+  // infinity theta then makes u NaN at every pixel, so the tile comes out NaN)
+  const bool wild0 = __syncthreads_or(bad);
   const int n0 = REC ? min(nb, 256)
                      : max(max(s_hi[0][0], s_hi[0][1]), max(s_hi[0][2], s_hi[0][3]));
   const bool more = n0 > 64 || k4 > 256;
@@ -743,7 +769,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
   float acc[4][4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) acc[m][0] = acc[m][1] = acc[m][2] = acc[m][3] = 0.f;
-  auto walk = [&](int s0, int s1) {
+  auto walk = [&](auto exact, int s0, int s1) {
 #pragma unroll 2
     for (int sl = s0 + wave; sl < s1; sl += 4) {
       const float4 th = s_th[sl];
@@ -755,7 +781,7 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
       for (int m = 0; m < 4; ++m) {
         const float ly = lyq + (float)(4 * m);
         const float u = fmaf(fmaf(th.y, ly, P), ly, Q);
-        const float rl = relu_bits(u);
+        const float rl = decltype(exact)::value ? relu_nan(u) : relu_bits(u);
         const float w = rl * rl;
         acc[m][0] += w * cl.x;
         acc[m][1] += w * cl.y;
@@ -764,7 +790,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
       }
     }
   };
-  walk(0, min(n0, 64));
+  if (wild0)
+    walk(std::true_type{}, 0, min(n0, 64));
+  else
+    walk(std::false_type{}, 0, min(n0, 64));
   if (more) {
     if (wave > 0) stage(s, v, r0, r1, r2);
     int hi = 0;
@@ -787,10 +816,13 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
       if (m) hi = s0 + wave * 64 + 64 - __clzll((long long)m);
     }
     if (lane == 0) s_hi[1][wave] = hi;
-    poisoned = __syncthreads_or(bad) || poisoned;
+    const bool wild1 = __syncthreads_or(bad);
     const int n = REC ? nb
                       : max(n0, max(max(s_hi[1][0], s_hi[1][1]), max(s_hi[1][2], s_hi[1][3])));
-    walk(64, n);
+    if (wild1)
+      walk(std::true_type{}, 64, n);
+    else
+      walk(std::false_type{}, 64, n);
   }
   // join the four waves' sums in wave order; the slot LDS is reused
   float4* red = reinterpret_cast<float4*>(s_dyn);
@@ -811,11 +843,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
   const float ar = sum.x, ag = sum.y, ab = sum.z, ad = sum.w;
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
-  const float nanv = __builtin_nanf("");
-  const float d = poisoned ? nanv : ad + wb;
-  image[pix * 3 + 0] = poisoned ? nanv : (ar + wb * bg[1]) / d;
-  image[pix * 3 + 1] = poisoned ? nanv : (ag + wb * bg[2]) / d;
-  image[pix * 3 + 2] = poisoned ? nanv : (ab + wb * bg[3]) / d;
+  const float d = ad + wb;
+  image[pix * 3 + 0] = (ar + wb * bg[1]) / d;
+  image[pix * 3 + 1] = (ag + wb * bg[2]) / d;
+  image[pix * 3 + 2] = (ab + wb * bg[3]) / d;
   if (den_out) den_out[pix] = d;
 }
 

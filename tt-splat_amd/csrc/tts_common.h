@@ -36,11 +36,10 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 // relu with torch's NaN rule (torch.relu and clamp(min=0) keep a NaN):
 //   relu_nan: u <= 0 -> +0, else u; a NaN of either sign fails the compare and passes through.
 //   relu_bits: one integer max on the bit pattern.  Equal to relu_nan for every u except a NaN
-//   with the sign bit set, which it maps to +0.  The binned splat kernels use it: the NaN the GPU
-//   generates (inf - inf, 0 * inf, as when theta terms overflow at some pixels of a tile) is the
-//   default NaN, sign bit clear, so it passes through as torch.relu keeps it; a u can only be a
-//   NaN with the sign bit set when theta holds a NaN, and those tiles are written NaN whole by
-//   the kernels' poison rule (a NaN theta makes u NaN at every pixel).
+//   with the sign bit set, which it maps to +0 -- and the NaN the GPU generates (inf - inf) can
+//   carry the sign bit.  The splat kernels use it only where u is finite: the forward walks of
+//   tiles without a wild slot (theta_wild), and the backward, whose tiles with a NaN u have a NaN
+//   den from the forward, so every gradient of such a tile is NaN whatever relu gives.
 __device__ __forceinline__ float relu_nan(float u) { return u <= 0.0f ? 0.0f : u; }
 __device__ __forceinline__ float relu_bits(float u) {
   return __int_as_float(max(__float_as_int(u), 0));
@@ -156,6 +155,8 @@ __device__ __forceinline__ Philox4 philox4x32_10(uint32_t c0, uint32_t c1, uint3
 
 // Stream tags (counter word 2) of the MCMC draws; counter = (index, step, tag, 0), key = (seed, 0).
 constexpr uint32_t kTagSgld = 1, kTagRelocPick = 2, kTagRelocOffset = 3;
+// Random training backgrounds: counter = (view, step, kTagBg, 0), key = (seed, 0).
+constexpr uint32_t kTagBg = 4;
 
 // Uniform in (0, 1) from the top 24 bits: ((x >> 8) + 0.5) * 2^-24 (exact in double).
 __device__ __forceinline__ double u01d(uint32_t x) {

@@ -53,6 +53,8 @@ SIGNATURES = {
     "tts_loss_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "tts_loss_target_stats": (_c_int, [_vp, _c_int, _c_int, _vp, _vp]),
     "tts_loss_grad_stats": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_float, _vp, _vp, _vp]),
+    "tts_composite_random_bg": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _c_u32, _vp, _vp,
+                                         _vp]),
     "tts_loss_partials_count": (_c_int, [_c_int, _c_int, ctypes.POINTER(_c_int)]),
     "tts_loss_grad": (_c_int, [_vp, _vp, _c_int, _c_int, _c_float, _vp, _vp, _vp, _c_size, _vp]),
     "tts_adam_advance": (_c_int, [_vp, _c_float, _c_float, _vp]),

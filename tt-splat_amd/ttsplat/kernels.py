@@ -481,9 +481,17 @@ def loss_grad(image, target, lam=0.2, gimage=None, partials=None, workspace=None
     return gimage
 
 
+def loss_stats_numel(H, W):
+    """fp32 elements of one target's statistics buffer (loss_stats)."""
+    n = _lib.load().tts_loss_stats_bytes(H, W)
+    if n == 0:
+        raise ValueError(f"image {H}x{W} is smaller than the 11x11 SSIM window")
+    return n // 4
+
+
 def loss_stats(target, stats=None):
     """The target's SSIM statistics (mu_y, s_y per channel on the valid map, then the target
-    channel-planar), computed once per target and read by loss_grad_stats."""
+    channel-planar), computed whenever the target changes and read by loss_grad_stats."""
     H, W = target.shape[0], target.shape[1]
     require(target, "target", F32, (H, W, 3))
     n = _lib.load().tts_loss_stats_bytes(H, W)
@@ -493,6 +501,32 @@ def loss_stats(target, stats=None):
     require(stats, "stats", F32, (n // 4,), target.device)
     call("tts_loss_target_stats", ptr(target), H, W, ptr(stats), stream())
     return stats
+
+
+def rgba_premult(rgba):
+    """[H,W,4] straight RGBA (spike's load_blender(keep_alpha=True)) -> [H,W,4] fp32
+    (alpha r, alpha g, alpha b, 1 - alpha): the premultiplied colour and transmittance the
+    random-background target is composited from (tools/resident_traced.py:184-185)."""
+    rgba = torch.as_tensor(rgba, dtype=F32)
+    if rgba.dim() != 3 or rgba.shape[2] != 4:
+        raise ValueError(f"rgba must be [H,W,4], got {tuple(rgba.shape)}")
+    a = rgba[..., 3:4]
+    return torch.cat([rgba[..., :3] * a, 1.0 - a], dim=-1).contiguous()
+
+
+def composite_random_bg(rgba_pm, step, view, seed, bg, target=None):
+    """Draw this step's background (Philox, keyed by the device step count, `view` and `seed`)
+    into bg[1..3] and composite target[H,W,3] = premult + (1 - alpha) * bg."""
+    H, W = rgba_pm.shape[0], rgba_pm.shape[1]
+    dev = rgba_pm.device
+    _aligned16(require(rgba_pm, "rgba_pm", F32, (H, W, 4)), "rgba_pm")
+    require(step, "step", I32, (4,), dev)
+    require(bg, "bg", F32, (4,), dev)
+    target = torch.empty(H, W, 3, device=dev, dtype=F32) if target is None else target
+    require(target, "target", F32, (H, W, 3), dev)
+    call("tts_composite_random_bg", ptr(rgba_pm), H, W, ptr(step), int(view),
+         int(seed) & 0xFFFFFFFF, ptr(bg), ptr(target), stream())
+    return target
 
 
 def loss_grad_stats(image, target, stats, lam=0.2, gimage=None, partials=None):

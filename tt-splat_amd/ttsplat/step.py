@@ -68,7 +68,18 @@ class TrainStep:
     splat, loss, backward and Adam on the bins last computed -- one bin table for all cameras,
     as in that trainer.  Each camera gets a graph with and one without the binning kernels.
     run(i, n) is n step() calls from step i on; with bin_every = 1 and no relocation it replays
-    graphs that each hold run_len consecutive steps (one graph launch per run_len steps)."""
+    graphs that each hold run_len consecutive steps (one graph launch per run_len steps).
+    random_bg = True: the reference trainer's --random-bg (tools/resident_traced.py:182-185,
+    671-674): targets are straight RGBA [H,W,4] (spike's load_blender(keep_alpha=True)); every
+    view backward first draws a background colour (Philox keyed by bg_seed, the device step
+    count and the view; the reference draws torch.rand(3) on the host), composites the target
+    over it and renders with it as the numerator background c_b (w_b unchanged).  eval_psnr()
+    renders on white, as the reference evaluates.
+    target_stats: the loss needs each target's SSIM statistics.  "per_view" keeps one set per
+    view, computed once (36 bytes per pixel per view: 2.3 GB for 100 views at 800x800; the
+    targets must not change after construction); "per_step" keeps one set and recomputes it from
+    the current target at every view backward, as the reference's recompute_gt_stats does on each
+    view switch (tools/resident_traced.py:320-325,677-678).  random_bg implies "per_step"."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
@@ -77,7 +88,8 @@ class TrainStep:
     def __init__(self, params, cameras, targets, K=128, S=16, k=4.0, lr=None, w_b_raw=-3.0,
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
                  dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None,
-                 depth_weight=None, keep_grad=False, bin_every=1):
+                 depth_weight=None, keep_grad=False, bin_every=1, random_bg=False, bg_seed=0,
+                 target_stats="per_view"):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -138,14 +150,30 @@ class TrainStep:
             self.gdw = torch.zeros(G, 2, dtype=F32, device=dev)
             self.dw_ws = kernels.depth_weight_workspace(G, dev)
         self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
+        self.bg_white = torch.tensor([float(w_b), 1.0, 1.0, 1.0], dtype=F32, device=dev)
+        self.random_bg, self.bg_seed = bool(random_bg), int(bg_seed)
+        if target_stats not in ("per_view", "per_step"):
+            raise ValueError(f"target_stats must be 'per_view' or 'per_step', got {target_stats!r}")
+        self.stats_mode = "per_step" if self.random_bg else target_stats
         # per-view inputs
         self.cams = [c.device_block(dev) for c in cameras]
-        self.targets = [t.to(dev, F32).contiguous() for t in targets]
-        if len(self.targets) != len(self.cams):
+        if len(targets) != len(self.cams):
             raise ValueError("one target image per camera is required")
-        # each target's SSIM statistics, computed once (tools/resident_traced.py:431-464 keeps
-        # its target maps per view the same way)
-        self.target_stats = [kernels.loss_stats(t) for t in self.targets]
+        self.targets = self.rgba_pm = self.target_buf = None
+        if self.random_bg:
+            for t in targets:
+                if tuple(t.shape) != (H, W, 4):
+                    raise ValueError(f"random_bg needs RGBA targets [{H},{W},4], got "
+                                     f"{tuple(t.shape)}")
+            self.rgba_pm = [kernels.rgba_premult(t.cpu()).to(dev) for t in targets]
+            self.target_buf = torch.empty(H, W, 3, device=dev, dtype=F32)
+        else:
+            self.targets = [t.to(dev, F32).contiguous() for t in targets]
+        if self.stats_mode == "per_view":
+            self.target_stats = [kernels.loss_stats(t) for t in self.targets]
+        else:
+            self.target_stats = None
+            self.stats_buf = torch.empty(kernels.loss_stats_numel(H, W), device=dev, dtype=F32)
         # work buffers
         self.proj = torch.empty(G, 12, device=dev, dtype=F32)
         self.keep = torch.empty(G, device=dev, dtype=U8)
@@ -208,11 +236,13 @@ class TrainStep:
             self._force_rebin = True
         return self.image
 
-    def _forward(self, ci, advance=False, rebin=True, grads=True, camera=None):
+    def _forward(self, ci, advance=False, rebin=True, grads=True, camera=None, bg=None):
         """forward() as a training step enqueues it (no forced rebin); camera: a [16] device
-        camera block to render instead of camera ci's."""
+        camera block to render instead of camera ci's; bg: a [4] background block instead of
+        self.bg."""
         adv = self.step_block if advance else None
         cam = self.cams[ci] if camera is None else camera
+        bgb = self.bg if bg is None else bg
         if rebin:   # one call: the binning's count pass rides on the geometry launch
             kernels.geom_fwd_assign_bins(self.P, cam, self.H, self.W, self.S, self.K,
                                          self.span, proj=self.proj, keep=self.keep,
@@ -228,18 +258,18 @@ class TrainStep:
                              sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
                              advance=adv)
         if self.dtype == "bf16" and rebin and self.use_rec:
-            kernels.splat_fwd_mx_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
+            kernels.splat_fwd_mx_rec(self.slot_rec, self.pos_count, self.order, bgb, self.H,
                                      self.W, self.S, self.k, self.image, self.den, bf16=True,
                                      write_den=grads)
         elif self.dtype == "bf16":
-            kernels.splat_fwd_mx(self.proj, self.idx, self.valid, self.bg, self.H, self.W,
+            kernels.splat_fwd_mx(self.proj, self.idx, self.valid, bgb, self.H, self.W,
                                  self.S, self.k, self.image, self.den, self.order, bf16=True)
         elif rebin and self.use_rec:
-            kernels.splat_fwd_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
+            kernels.splat_fwd_rec(self.slot_rec, self.pos_count, self.order, bgb, self.H,
                                   self.W, self.S, self.k, self.image, self.den,
                                   write_den=grads)
         else:
-            kernels.splat_fwd(self.proj, self.idx, self.valid, self.bg, self.H, self.W, self.S,
+            kernels.splat_fwd(self.proj, self.idx, self.valid, bgb, self.H, self.W, self.S,
                               self.k, self.image, self.den, self.order)
         return self.image
 
@@ -248,11 +278,24 @@ class TrainStep:
         """Number of distinct steps (views for batch = 1, batches otherwise)."""
         return len(self.cams) // self.batch
 
+    def _loss_target(self, ci):
+        """The target of view ci and its SSIM statistics (recomputed in "per_step" mode)."""
+        if self.stats_mode == "per_view":
+            return self.targets[ci], self.target_stats[ci]
+        tgt = self.target_buf if self.random_bg else self.targets[ci]
+        kernels.loss_stats(tgt, self.stats_buf)
+        return tgt, self.stats_buf
+
     def _view_backward(self, ci, advance=False, rebin=True):
-        """Forward, loss gradient and fused splat backward of camera ci (slot gradients)."""
+        """Forward, loss gradient and fused splat backward of camera ci (slot gradients).  With
+        random_bg the view's background is drawn and its target composited first (before the
+        step advance inside the geometry launch: the draw is keyed by the completed steps)."""
+        if self.random_bg:
+            kernels.composite_random_bg(self.rgba_pm[ci], self.step_block, ci, self.bg_seed,
+                                        self.bg, self.target_buf)
         self._forward(ci, advance, rebin)
-        kernels.loss_grad_stats(self.image, self.targets[ci], self.target_stats[ci], self.lam,
-                                self.gimage, self.partials)
+        tgt, stats = self._loss_target(ci)
+        kernels.loss_grad_stats(self.image, tgt, stats, self.lam, self.gimage, self.partials)
         if rebin and self.use_rec:
             kernels.splat_bwd_rec(self.slot_rec, self.pos_count, self.order, self.bg, self.H,
                                   self.W, self.S, self.k, self.image, self.den, self.gimage,
@@ -314,7 +357,7 @@ class TrainStep:
         bin_every = 1, no relocation and all cameras, run_len > 1 also captures, for every
         starting step, one graph of run_len consecutive steps (used by run())."""
         cams = range(self.n_steps) if cams is None else cams
-        live = [self.P, self.m, self.v, self.step_block]
+        live = [self.P, self.m, self.v, self.step_block, self.bg]
         if self.sh is not None:
             live += [self.sh, self.sh_m, self.sh_v]
         if self.dw is not None:
@@ -389,6 +432,30 @@ class TrainStep:
                 self.enqueue_relocate()
             self._force_rebin = True     # relocated gaussians move: the next step rebins
         self._it += 1
+
+    @torch.no_grad()
+    def eval_psnr(self, cameras, images):
+        """Mean PSNR over (camera, image) pairs of the binned device render, on a white
+        background (c_b = 1: the reference's evaluation of its trainer, tools/resident_traced.py:
+        768-783; psnr as spike/metrics.py:10-12, on clamped images).  images: [H,W,3], or RGBA
+        [H,W,4] composited over white.  Each view is binned and rendered on its own; the next
+        step() rebins.  Parameters and optimiser state are untouched."""
+        if len(cameras) != len(images) or not cameras:
+            raise ValueError("eval_psnr needs one image per camera")
+        vals = []
+        for cam, img in zip(cameras, images):
+            if (cam.H, cam.W) != (self.H, self.W):
+                raise ValueError(f"eval camera is {cam.W}x{cam.H}, the step renders "
+                                 f"{self.W}x{self.H}")
+            self._forward(0, rebin=True, grads=False, camera=cam.device_block(self.dev),
+                          bg=self.bg_white)
+            gt = torch.as_tensor(img).to(self.dev, F32)
+            if gt.shape[-1] == 4:
+                gt = gt[..., :3] * gt[..., 3:4] + (1.0 - gt[..., 3:4])
+            mse = (self.image.clamp(0.0, 1.0) - gt.clamp(0.0, 1.0)).pow(2).mean()
+            vals.append(float(-10.0 * torch.log10(mse.clamp(min=1e-12))))
+        self._force_rebin = True
+        return sum(vals) / len(vals)
 
     def loss(self):
         """Loss of the last step (a device scalar; reading it synchronises)."""
