@@ -23,13 +23,20 @@ graph of 20 back-to-back launches, camera 0 (and each of the 8 cameras for the s
 with their pair counts, so the roofline fraction can be recomputed from a profile of the same
 run, whose kernel durations these agree with: no host time between the launches).
 
-Roofline convention: the splat kernels are priced in the reference's algorithmic flops per
-(pixel, valid slot) pair -- 22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80,
-Phi.theta 12 + relu^2 2 + WSR 8, and the transposed contractions) -- against MI355X's 157.3
-TFLOP/s FP32 peak (the same for vector and matrix FP32; `bound` reads "mfma", the arithmetic
-roof, as opposed to "hbm").  That peak is reachable without packed FP32 instructions on gfx950
-(wave64 FP32 FMAs issue at two cycles each when enough waves are ready), so frac is the
-fraction of the attainable VALU rate.
+Roofline convention: every kernel of the training step gets a row (`extra.kernel_roofline`)
+with the roof that bounds it and its algorithmic units, and `roofline` is the row of the step's
+slowest kernel (HIP events, camera 0):
+- splat forward / backward: the reference's algorithmic flops per (pixel, valid slot) pair --
+  22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80, Phi.theta 12 + relu^2 2 +
+  WSR 8, and the transposed contractions) -- against the 157.3 TFLOP/s FP32 peak, which the
+  VALU reaches without packed FP32 instructions on gfx950 (wave64 FP32 FMAs issue at two
+  cycles each when enough waves are ready): bound "valu";
+- the loss gradient: 1056 flop per pixel (3 channels: the separable filters of the forward
+  and transposed passes) against the same FP32 peak, bound "valu" (1056 flop per 36 algorithmic
+  bytes lies right of the FP32/HBM ridge); its HBM fraction at 36 bytes per pixel (image and
+  target in, gradient out) is reported beside it;
+- geometry forward + binning and geometry backward + Adam: algorithmic HBM bytes against
+  8 TB/s, bound "hbm" (the byte counts are in kernel_bytes below).
 """
 import argparse
 import json
@@ -44,6 +51,9 @@ METRIC = "train it/s + render fps (G2k res128, G100k 1264×832), % of HBM/VALU r
 PEAK_FP32_TFLOPS = 157.3      # MI355X published FP32 vector/matrix peak
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 FLOP_PER_PAIR = {"splat_fwd": 22.0, "splat_bwd": 44.0}
+LOSS_FLOP_PER_PIXEL = 1056.0  # 3 channels x (5 + 3) filtered quantities x 2 passes x 11 taps x 2
+LOSS_BYTES_PER_PIXEL = 36.0   # image and target in, dL/dimage out (fp32, 3 channels)
+STEP_KERNELS = ("geom_fwd_binning", "splat_fwd", "loss_grad", "splat_bwd", "geom_bwd_adam")
 
 
 def parse():
@@ -309,6 +319,45 @@ def splat_bytes(ts, torch):
     T, P = ts.tmap.T, ts.H * ts.W
     fwd = 40 * nvalid + 4 * ts.K * T + 12 * P
     return fwd, fwd + 16 * P + 36 * nvalid
+
+
+def kernel_bytes(ts):
+    """Algorithmic HBM bytes of the step's geometry/binning and backward/Adam launches:
+    geom_fwd_binning reads params (56 B/gaussian) and writes proj (48) and keep (1), the bin
+    table (idx + valid, 5 B per slot), count, ncand and order (12 B per tile), the inverse table
+    (36 B/gaussian) and one 48-byte slot record per kept slot; geom_bwd_adam reads params, m, v
+    and the inverse table and writes params, m, v (56 B each per gaussian), and gathers 36 B per
+    kept slot."""
+    G, T, K = ts.G, ts.tmap.T, ts.K
+    nvalid = int(ts.count.long().sum())
+    fwd = G * (56 + 48 + 1 + 36) + 5 * T * K + 12 * T + 48 * nvalid
+    bwd = G * (6 * 56 + 36) + 36 * nvalid
+    return {"geom_fwd_binning": fwd, "geom_bwd_adam": bwd}
+
+
+def roofline_rows(ts, kt, pairs, cfg_name):
+    """One roofline row per kernel of the step (camera 0 durations)."""
+    rows = {}
+    for name in ("splat_fwd", "splat_bwd"):
+        flops = FLOP_PER_PAIR[name] * pairs
+        tfl = flops / (kt[name] * 1e-6) / 1e12
+        rows[name] = dict(us=kt[name], bound="valu", achieved=tfl, peak=PEAK_FP32_TFLOPS,
+                          unit="TFLOP/s", frac=tfl / PEAK_FP32_TFLOPS,
+                          flops_per_launch=flops, pairs_per_launch=pairs)
+    npix = ts.H * ts.W
+    tfl = LOSS_FLOP_PER_PIXEL * npix / (kt["loss_grad"] * 1e-6) / 1e12
+    gbs = LOSS_BYTES_PER_PIXEL * npix / (kt["loss_grad"] * 1e-6) / 1e9
+    rows["loss_grad"] = dict(us=kt["loss_grad"], bound="valu", achieved=tfl,
+                             peak=PEAK_FP32_TFLOPS, unit="TFLOP/s", frac=tfl / PEAK_FP32_TFLOPS,
+                             flops_per_launch=LOSS_FLOP_PER_PIXEL * npix, hbm_gbs=gbs,
+                             hbm_frac=gbs / PEAK_HBM_GBS)
+    for name, nbytes in kernel_bytes(ts).items():
+        gbs = nbytes / (kt[name] * 1e-6) / 1e9
+        rows[name] = dict(us=kt[name], bound="hbm", achieved=gbs, peak=PEAK_HBM_GBS, unit="GB/s",
+                          frac=gbs / PEAK_HBM_GBS, bytes_per_launch=nbytes)
+    for name, row in rows.items():
+        row["traffic"] = load_traffic(name, cfg_name)
+    return rows
 
 
 def run_c3(args, torch, scenes, TrainStep):
@@ -613,27 +662,20 @@ def main():
     kt = time_kernels(ts, args.kernel_reps, torch, kernels)
     per_cam = time_splat_per_camera(ts, max(10, args.kernel_reps // 2), torch, kernels)
     pairs = per_cam[0]["pairs"]
-    rows = {}
-    for name in ("splat_fwd", "splat_bwd"):
-        flops = FLOP_PER_PAIR[name] * pairs
-        tfl = flops / (kt[name] * 1e-6) / 1e12
-        rows[name] = dict(us=kt[name], tflops=tfl, frac=tfl / PEAK_FP32_TFLOPS)
-    dom = max(("splat_fwd", "splat_bwd"), key=lambda n: kt[n])
-    all_pairs = sum(r["pairs"] for r in per_cam)
-    all_us = sum(r[dom + "_us"] for r in per_cam)
-    roofline = dict(bound="mfma", kernel=dom, achieved=rows[dom]["tflops"], peak=PEAK_FP32_TFLOPS,
-                    unit="TFLOP/s", frac=rows[dom]["frac"], traffic=load_traffic(dom, cfg.name),
-                    flops_per_pair=FLOP_PER_PAIR[dom], flops_per_launch=FLOP_PER_PAIR[dom] * pairs,
-                    pairs_per_launch=pairs, us_per_launch=kt[dom], camera=0,
-                    frac_all_cameras=FLOP_PER_PAIR[dom] * all_pairs / (all_us * 1e-6) / 1e12
-                    / PEAK_FP32_TFLOPS,
-                    convention="compute-bound (bound 'mfma' = the arithmetic roofline, not HBM): "
-                               "algorithmic flops of the reference's GEMM form per (pixel, "
-                               "valid slot) pair (22 fwd / 44 bwd) x pairs of the launch / its "
-                               "HIP-event duration over graph replays of 20 launches, camera 0; peak = MI355X FP32 157.3 TFLOP/s, "
-                               "the same for FP32 vector and matrix issue; the kernel issues "
-                               "its FP32 on the VALU, which reaches that rate without packed "
-                               "FP32 instructions")
+    rows = roofline_rows(ts, kt, pairs, cfg.name)
+    dom = max(STEP_KERNELS, key=lambda n: kt[n])
+    roofline = dict(rows[dom], kernel=dom, camera=0,
+                    convention="the step's slowest kernel (HIP-event duration over graph "
+                               "replays of 20 launches, camera 0) against its bound: algorithmic "
+                               "flops (splat 22/44 per pixel-slot pair, loss 1056 per pixel) over "
+                               "157.3 TFLOP/s FP32, reached on the VALU without packed FP32, or "
+                               "algorithmic bytes over 8 TB/s HBM; every kernel's row in "
+                               "extra.kernel_roofline")
+    if dom in ("splat_fwd", "splat_bwd"):
+        all_pairs = sum(r["pairs"] for r in per_cam)
+        all_us = sum(r[dom + "_us"] for r in per_cam)
+        roofline["frac_all_cameras"] = (FLOP_PER_PAIR[dom] * all_pairs / (all_us * 1e-6) / 1e12
+                                        / PEAK_FP32_TFLOPS)
     small = {} if args.no_small else small_configs(torch, scenes, TrainStep)
     extra_c3 = {} if args.no_c3 else run_c3(args, torch, scenes, TrainStep)
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
