@@ -25,7 +25,8 @@ run, whose kernel durations these agree with: no host time between the launches)
 
 Roofline convention: every kernel of the training step gets a row (`extra.kernel_roofline`)
 with the roof that bounds it and its algorithmic units, and `roofline` is the row of the step's
-slowest kernel (HIP events, camera 0):
+slowest single-kernel launch (HIP events, camera 0; the geometry + binning call launches four
+kernels and its row covers the four together):
 - splat forward / backward: the reference's algorithmic flops per (pixel, valid slot) pair --
   22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80, Phi.theta 12 + relu^2 2 +
   WSR 8, and the transposed contractions) -- against the 157.3 TFLOP/s FP32 peak, which the
@@ -53,7 +54,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 FLOP_PER_PAIR = {"splat_fwd": 22.0, "splat_bwd": 44.0}
 LOSS_FLOP_PER_PIXEL = 1056.0  # 3 channels x (5 + 3) filtered quantities x 2 passes x 11 taps x 2
 LOSS_BYTES_PER_PIXEL = 36.0   # image and target in, dL/dimage out (fp32, 3 channels)
-STEP_KERNELS = ("geom_fwd_binning", "splat_fwd", "loss_grad", "splat_bwd", "geom_bwd_adam")
+# the step's single-kernel launches (roofline picks the slowest of them); geom_fwd_binning is one
+# call of four kernels (geometry + the binning's count pass, column scan, scatter, select) and
+# gets its own row as a group
+STEP_KERNELS = ("splat_fwd", "loss_grad", "splat_bwd", "geom_bwd_adam")
 
 
 def parse():
@@ -354,7 +358,8 @@ def roofline_rows(ts, kt, pairs, cfg_name):
     for name, nbytes in kernel_bytes(ts).items():
         gbs = nbytes / (kt[name] * 1e-6) / 1e9
         rows[name] = dict(us=kt[name], bound="hbm", achieved=gbs, peak=PEAK_HBM_GBS, unit="GB/s",
-                          frac=gbs / PEAK_HBM_GBS, bytes_per_launch=nbytes)
+                          frac=gbs / PEAK_HBM_GBS, bytes_per_launch=nbytes,
+                          launches=4 if name == "geom_fwd_binning" else 1)
     for name, row in rows.items():
         row["traffic"] = load_traffic(name, cfg_name)
     return rows
@@ -516,16 +521,15 @@ def cpu_baseline(args, torch, scenes, kernels):
             tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k,
                                        span=cfg.span)
             nf, df = _rate(lambda: osplat.render_binned(P, cam, tmap, K=cfg.K, k=cfg.k,
-                                                        span=cfg.span), fsec)
+                                                        span=cfg.span), fsec, 3)
         m, v = torch.zeros_like(P), torch.zeros_like(P)
         it = [0]
 
         def step():
             it[0] += 1
             opipe.train_step(P, m, v, it[0], cam, tmap, tgt, lr, K=cfg.K, k=cfg.k, span=cfg.span)
-        if name != "c5":
-            step()                                   # warm-up
-        nt, dt = _rate(step, tsec)
+        step()                                       # warm-up (the target render warmed up
+        nt, dt = _rate(step, tsec, 3)                # the forward); at least 3 timed samples
         rows[name] = dict(fwd_fps=nf / df, fwd_ms=df / nf * 1e3, train_its=nt / dt,
                           train_ms=dt / nt * 1e3, sample=f"{nf} forwards, {nt} train steps")
     rows["c2"] = dict(rows["c1_ref"], note="the c2 shape (G=2000, 128x128, S=16, k=4) in fp32: "
@@ -550,8 +554,10 @@ def cpu_baseline(args, torch, scenes, kernels):
             with torch.no_grad():
                 tgt = osplat.render_binned(cfg.params(seed=1), cam, tmap, K=cfg.K, k=cfg.k)
             m, v = torch.zeros_like(P), torch.zeros_like(P)
-            n1, d1 = _rate(lambda: opipe.train_step(P, m, v, 1, cam, tmap, tgt, lr, K=cfg.K,
-                                                    k=cfg.k), tsec)
+            one_step = lambda: opipe.train_step(P, m, v, 1, cam, tmap, tgt, lr, K=cfg.K,
+                                                k=cfg.k)
+            one_step()                               # warm-up, then at least 3 timed samples
+            n1, d1 = _rate(one_step, tsec, 3)
             one[name] = dict(train_its=n1 / d1, train_ms=d1 / n1 * 1e3, steps=n1)
     finally:
         torch.set_num_threads(use)
@@ -665,7 +671,7 @@ def main():
     rows = roofline_rows(ts, kt, pairs, cfg.name)
     dom = max(STEP_KERNELS, key=lambda n: kt[n])
     roofline = dict(rows[dom], kernel=dom, camera=0,
-                    convention="the step's slowest kernel (HIP-event duration over graph "
+                    convention="the step's slowest single-kernel launch (HIP-event duration over graph "
                                "replays of 20 launches, camera 0) against its bound: algorithmic "
                                "flops (splat 22/44 per pixel-slot pair, loss 1056 per pixel) over "
                                "157.3 TFLOP/s FP32, reached on the VALU without packed FP32, or "

@@ -69,17 +69,18 @@ __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, 
 __device__ __forceinline__ bool theta_poisons(const float4 ta, const float4 tb) {
   return __builtin_isnan(((ta.x + ta.y) + (ta.z + ta.w)) + (tb.x + tb.y));
 }
-// A slot whose u can be infinite or NaN at some pixel: some |theta| >= 1e34, an infinity or a
-// NaN.  Below that, at pixel coordinates under 32 every product, partial sum and u stays under
-// 3.2e37 < FLT_MAX whatever the order of evaluation, so u is finite and relu_bits is exact.  A
-// tile with such a slot walks with relu_nan: where u comes out NaN (inf - inf, in this kernel's
-// order of evaluation -- torch's own order is its BLAS's), the pixel is NaN, as torch.relu
-// keeps it, and -inf gives 0.  (The GPU's generated NaN can carry the sign bit, which
-// relu_bits would map to 0.)
+// A slot whose u can be large, infinite or NaN at some pixel: some |theta| >= 1e15, an
+// infinity or a NaN.  Below that, at pixel coordinates under 32 every product, partial sum and
+// u stays under 3.1e18 whatever the order of evaluation (the monomials sum to under 3100), so u
+// is finite, relu_bits is exact, and so is the fast walks' 2 relu(u) = u + |u| with its square
+// 4 w (under FLT_MAX while u < 9.2e18).  A tile with such a slot walks with relu_nan and w
+// itself: where u comes out NaN (inf - inf, in this kernel's order of evaluation -- torch's own
+// order is its BLAS's), the pixel is NaN, as torch.relu keeps it, and -inf gives 0.  (The GPU's
+// generated NaN can carry the sign bit, which relu_bits would map to 0.)
 __device__ __forceinline__ bool theta_wild(const float4 ta, const float4 tb) {
   const float m = fmaxf(fmaxf(fmaxf(fabsf(ta.x), fabsf(ta.y)), fmaxf(fabsf(ta.z), fabsf(ta.w))),
                         fmaxf(fabsf(tb.x), fabsf(tb.y)));
-  return !(m < 1e34f) || theta_poisons(ta, tb);
+  return !(m < 1e15f) || theta_poisons(ta, tb);
 }
 
 __device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
@@ -256,7 +257,12 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
 // Contraction of one tile's staged slots over its pixels, then the theta backward and the
 // stores (the main loop of the splat backward).  Every thread of the block must call it (it
 // contains barriers when slots share rows).
-template <int S, bool FROM_PROJ>
+// WILD = false (every slot's |theta| < 1e15, theta_wild): the pixel terms q were staged as q/4
+// and the slot colours are doubled here, so with r2 = u + |u| = 2 relu(u) (one full-rate add
+// instead of a half-rate max) r2^2 q/4 = w q and r2 (q/4)(2 C) = relu(u) q.C exactly (scalings
+// by powers of two).  WILD = true: relu_bits on unscaled q (a NaN u only occurs in tiles whose
+// den the forward made NaN, so every gradient there is NaN whatever relu gives).
+template <int S, bool FROM_PROJ, bool WILD>
 __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const float4* s_px,
                                              int t, int K, int ox, int oy,
                                              float inv_k, const float* __restrict__ proj,
@@ -278,6 +284,12 @@ __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const flo
       A = sl.ta[s];
       B = sl.tb[s];
       C = sl.cl[s];
+      if constexpr (!WILD) {
+        C.x *= 2.f;
+        C.y *= 2.f;
+        C.z *= 2.f;
+        C.w *= 2.f;
+      }
     }
     float g0 = 0.f, g1 = 0.f, g2 = 0.f, g3 = 0.f, g4 = 0.f, g5 = 0.f;
     float gr = 0.f, gg = 0.f, gb = 0.f, go = 0.f;
@@ -300,7 +312,7 @@ __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const flo
           for (int x8 = 0; x8 < 8; ++x8) {
             const float lx = xbf + ((float)x8 + 0.5f);
             const float u = (A.x * lx + cc1) * lx + cc0;
-            const float r = relu_bits(u);
+            const float r = WILD ? relu_bits(u) : u + fabsf(u);
             const float w = r * r;
             const float4 q = row[xb + x8];
             const float gw = q.x * C.x + q.y * C.y + q.z * C.z + q.w * C.w;
@@ -406,7 +418,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     }
   }
   int n;
-  bool bad = false;  // a poisoned tile's den is NaN already (the forward wrote it)
+  bool bad = false;  // a wild slot (theta_wild): the contraction keeps relu on unscaled terms
   if constexpr (REC) {
     n = load_slots_rec(proj, pos_count, K, (float)ox, (float)oy, inv_k, sl, &bad);
   } else if constexpr (FROM_PROJ) {
@@ -415,8 +427,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     load_slots_theta(theta, col, oc, t, K, sl, &bad);
     n = K;
   }
-  // Per-pixel WSR backward: gnum = gC/den, gden = -(gC . C)/den.
+  const bool wild = __syncthreads_or(bad);
+  // Per-pixel WSR backward: gnum = gC/den, gden = -(gC . C)/den (staged as a quarter unless the
+  // tile is wild, see bwd_contract).
   const float bg1 = bg[1], bg2 = bg[2], bg3 = bg[3];
+  const float qs = wild ? 1.0f : 0.25f;
   float wpart = 0.0f;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
@@ -424,7 +439,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     const float4 q = make_float4(pg[i][0] * inv, pg[i][1] * inv, pg[i][2] * inv,
                                  -(pg[i][0] * pc[i][0] + pg[i][1] * pc[i][1] + pg[i][2] * pc[i][2]) * inv);
     const int p = threadIdx.x + 256 * i;
-    s_px[(p / S) * (S + 1) + p % S] = q;
+    s_px[(p / S) * (S + 1) + p % S] = make_float4(q.x * qs, q.y * qs, q.z * qs, q.w * qs);
     wpart += q.x * bg1 + q.y * bg2 + q.z * bg3 + q.w;
   }
   if (gwb) {  // per-tile partial of dL/dw_b (summed by the caller)
@@ -433,7 +448,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   }
   __syncthreads();
 
-  bwd_contract<S, FROM_PROJ>(n, sl, s_px, t, K, ox, oy, inv_k, proj, gslot, gtheta, gcol, goc);
+  if (wild)
+    bwd_contract<S, FROM_PROJ, true>(n, sl, s_px, t, K, ox, oy, inv_k, proj, gslot, gtheta, gcol,
+                                     goc);
+  else
+    bwd_contract<S, FROM_PROJ, false>(n, sl, s_px, t, K, ox, oy, inv_k, proj, gslot, gtheta,
+                                      gcol, goc);
 }
 
 // ------------------------------------------------------------------ matrix-core forward --
@@ -716,7 +736,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
       bad = bad || theta_wild(ta, tb);
       s_th[s] = ta;
       s_th2[s] = make_float2(tb.x, tb.y);
-      s_col[s] = cl;
+      // a quarter of the colour: the fast walk's weight is (2 relu(u))^2 = 4 w
+      s_col[s] = make_float4(0.25f * cl.x, 0.25f * cl.y, 0.25f * cl.z, 0.25f * cl.w);
     } else {
       s_th[s] = make_float4(0.f, 0.f, 0.f, 0.f);
       s_th2[s] = make_float2(0.f, 0.f);
@@ -774,14 +795,22 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
     for (int sl = s0 + wave; sl < s1; sl += 4) {
       const float4 th = s_th[sl];
       const float2 th2 = s_th2[sl];
-      const float4 cl = s_col[sl];
+      float4 cl = s_col[sl];
+      if constexpr (decltype(exact)::value) {  // w itself, with the staged quarter undone
+        cl.x *= 4.f;
+        cl.y *= 4.f;
+        cl.z *= 4.f;
+        cl.w *= 4.f;
+      }
       const float P = fmaf(th.z, lx, th2.x);
       const float Q = fmaf(fmaf(th.x, lx, th.w), lx, th2.y);
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const float ly = lyq + (float)(4 * m);
         const float u = fmaf(fmaf(th.y, ly, P), ly, Q);
-        const float rl = decltype(exact)::value ? relu_nan(u) : relu_bits(u);
+        // fast: 2 relu(u) = u + |u| (one full-rate add; a max issues at half rate), exact for
+        // the finite u of a tile without a wild slot; wild: relu with torch's NaN rule
+        const float rl = decltype(exact)::value ? relu_nan(u) : u + fabsf(u);
         const float w = rl * rl;
         acc[m][0] += w * cl.x;
         acc[m][1] += w * cl.y;
