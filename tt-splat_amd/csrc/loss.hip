@@ -231,12 +231,16 @@ __global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
   const bool act2 = tid < G::N2;
   const int gm2 = R0 - kHalo + m2;
   float smu[kHC], ssy[kHC];
+  // one add per load: map pixels outside the valid map are never used (phase 2 masks them), so
+  // their offsets need no clamping -- negative ones wrap past the resource's bound (reading 0),
+  // the others stay inside the statistics buffer or past its bound
   auto load_stats = [&]() {
-    const unsigned row = (unsigned)min(max(gm2, 0), Ho - 1);
+    const unsigned off0 =
+        (unsigned)((C0 - kHalo + q2) * Ho + gm2) * 4u + (unsigned)ch * plane4;
+    const unsigned cstep = (unsigned)Ho * 4u;
 #pragma unroll
     for (int o = 0; o < kHC; ++o) {
-      const unsigned col = (unsigned)min(max(C0 - kHalo + q2 + o, 0), Wo - 1);
-      const unsigned off = (col * (unsigned)Ho + row) * 4u + (unsigned)ch * plane4;
+      const unsigned off = off0 + (unsigned)o * cstep;
       smu[o] = bld(ss, off);
       ssy[o] = bld(ss, off + 3u * plane4);
     }
