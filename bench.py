@@ -21,7 +21,8 @@ change), so every timed region runs at steady clocks; a cold GPU measures severa
 for the first second.  Per-kernel times are HIP events on the launch stream around replays of a
 graph of 20 back-to-back launches, camera 0 (and each of the 8 cameras for the splat kernels,
 with their pair counts, so the roofline fraction can be recomputed from a profile of the same
-run, whose kernel durations these agree with: no host time between the launches).
+run, whose kernel durations these agree with: no host time between the launches); each is the
+best of 3 such averages taken after ~20 ms of warm-up replays of the same graph.
 
 Roofline convention: every kernel of the training step gets a row (`extra.kernel_roofline`)
 with the roof that bounds it and its algorithmic units, and `roofline` is the row of the step's
@@ -29,9 +30,10 @@ slowest single-kernel launch (HIP events, camera 0; the geometry + binning call 
 kernels and its row covers the four together):
 - splat forward / backward: the reference's algorithmic flops per (pixel, valid slot) pair --
   22 forward, 44 backward (the GEMM form of tools/m3_perf.py:80, Phi.theta 12 + relu^2 2 +
-  WSR 8, and the transposed contractions) -- against the 157.3 TFLOP/s FP32 peak, which the
-  VALU reaches without packed FP32 instructions on gfx950 (wave64 FP32 FMAs issue at two
-  cycles each when enough waves are ready): bound "valu";
+  WSR 8, and the transposed contractions) -- against the 157.3 TFLOP/s FP32 peak (1024 SIMDs
+  x 64 lanes x 2 flop per 2 cycles at 2.4 GHz; without packed FP32, which this build does not
+  emit, back-to-back wave64 FMAs measured 2.7 cycles each at the nominal clock on gfx950, so
+  about 0.74 of the peak is what FMAs alone reach): bound "valu";
 - the loss gradient: 1056 flop per pixel (3 channels: the separable filters of the forward
   and transposed passes) against the same FP32 peak, bound "valu" (1056 flop per 36 algorithmic
   bytes lies right of the FP32/HBM ridge); its HBM fraction at 36 bytes per pixel (image and
@@ -191,10 +193,13 @@ def warm_clocks(ts, torch, seconds=1.5):
     return i
 
 
-def graph_time(fn, reps, torch, per_graph=20):
+def graph_time(fn, reps, torch, per_graph=20, samples=3, warm_ms=20.0):
     """Microseconds per launch of fn(): per_graph launches captured back to back in one HIP graph
     (no host work between them), the graph replayed until about reps launches have run, between
-    two HIP events on the stream the launches run on.  Timing eager launches instead would add
+    two HIP events on the stream the launches run on; the smallest of `samples` such averages,
+    taken after about warm_ms of replays.  The host work before a measurement (eager calls,
+    capture) leaves the GPU idle for milliseconds and its clock drops: without the warm-up the
+    first kernel timed after it read up to 2 us slow.  Timing eager launches instead would add
     the host's per-call time to every kernel shorter than it."""
     for _ in range(3):
         fn()
@@ -203,20 +208,27 @@ def graph_time(fn, reps, torch, per_graph=20):
     with torch.cuda.graph(g):
         for _ in range(per_graph):
             fn()
-    g.replay()
-    torch.cuda.synchronize()
-    n = max(1, reps // per_graph)
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(n):
-        g.replay()
+    g.replay()
     e1.record(stream)
     e1.synchronize()
-    us = e0.elapsed_time(e1) / (n * per_graph) * 1e3
+    n_warm = int(warm_ms / max(e0.elapsed_time(e1), 1e-3))
+    for _ in range(min(n_warm, 1000)):
+        g.replay()
+    n = max(1, reps // per_graph)
+    best = float("inf")
+    for _ in range(samples):
+        e0.record(stream)
+        for _ in range(n):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) / (n * per_graph) * 1e3)
     del g
-    return us
+    return best
 
 
 def step_splat_jobs(ts, kernels, gimage):
@@ -672,7 +684,8 @@ def main():
     dom = max(STEP_KERNELS, key=lambda n: kt[n])
     roofline = dict(rows[dom], kernel=dom, camera=0,
                     convention="the step's slowest single-kernel launch (HIP-event duration over graph "
-                               "replays of 20 launches, camera 0) against its bound: algorithmic "
+                               "replays of 20 launches, camera 0, the best of 3 averages after "
+                               "20 ms of warm-up replays) against its bound: algorithmic "
                                "flops (splat 22/44 per pixel-slot pair, loss 1056 per pixel) over "
                                "157.3 TFLOP/s FP32, reached on the VALU without packed FP32, or "
                                "algorithmic bytes over 8 TB/s HBM; every kernel's row in "
