@@ -6,7 +6,7 @@
 // Forward: the tile's valid slots are compacted into LDS as theta_u (6) and (col_o, o_col) (4);
 // each thread owns S*S/256 pixels and walks the slots:
 //     u = theta . [lx^2, ly^2, lx*ly, lx, ly, 1],  w = max(u,0)^2,  num += w*col, den += w*oc
-// and writes C = (num + w_b c_b) / (den + w_b) straight into the [H,W,3] image.  For S = 16
+// and writes C = (num + w_b c_b) * (1 / (den + w_b)) straight into the [H,W,3] image.  For S = 16
 // from proj or slot records (k_splat_fwd_tile) each wave walks the whole tile for a quarter of
 // the slots instead, u factored per column.
 //
@@ -247,9 +247,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
     const int p = threadIdx.x + 256 * i;
     const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
     const float d = ad[i] + wb;
-    image[pix * 3 + 0] = (ar[i] + cbr) / d;
-    image[pix * 3 + 1] = (ag[i] + cbg) / d;
-    image[pix * 3 + 2] = (ab[i] + cbb) / d;
+    const float inv = 1.0f / d;   // one division per pixel (each costs ~10 VALU instructions)
+    image[pix * 3 + 0] = (ar[i] + cbr) * inv;
+    image[pix * 3 + 1] = (ag[i] + cbg) * inv;
+    image[pix * 3 + 2] = (ab[i] + cbb) * inv;
     if (den_out) den_out[pix] = d;
   }
 }
@@ -873,9 +874,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
   const float d = ad + wb;
-  image[pix * 3 + 0] = (ar + wb * bg[1]) / d;
-  image[pix * 3 + 1] = (ag + wb * bg[2]) / d;
-  image[pix * 3 + 2] = (ab + wb * bg[3]) / d;
+  const float inv = 1.0f / d;     // one division per pixel (each costs ~10 VALU instructions)
+  image[pix * 3 + 0] = (ar + wb * bg[1]) * inv;
+  image[pix * 3 + 1] = (ag + wb * bg[2]) * inv;
+  image[pix * 3 + 2] = (ab + wb * bg[3]) * inv;
   if (den_out) den_out[pix] = d;
 }
 
