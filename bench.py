@@ -11,7 +11,8 @@ the GPU before the timed region; the timed region is exactly K steps between two
 synchronisations.
 
 Also reported: forward fps (geometry + binning + splat, graphs of 8 renders) for the same
-scene, the G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from HIP
+scene, the same training at the reference trainer's default bin cadence (bins rebuilt every 5th
+step), the G=2000 128x128, G=10k 800x800 and G=1M 1920x1072 numbers, per-kernel times from HIP
 events on the launch stream, the roofline of the dominant kernel, and the CPU oracle
 (PyTorch-CPU restatement of the reference path) timed on this host's cores, and on one thread,
 on bounded samples of the same workload.
@@ -81,6 +82,8 @@ def parse():
                     help="skip the SH degree 3 run of the headline workload")
     ap.add_argument("--no-mcmc", action="store_true",
                     help="skip the MCMC density-control run of the headline workload")
+    ap.add_argument("--no-bin5", action="store_true",
+                    help="skip the run at the reference trainer's bin cadence (every 5 steps)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="also run a plain device copy of this many MiB 5 times (a known-size "
                          "kernel to calibrate hardware byte counters against)")
@@ -105,7 +108,7 @@ def sh_rest_init(torch, G, seed, scale=0.1):
     return torch.randn(G, 15, 3, generator=g) * scale
 
 
-def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0, mcmc=None):
+def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0, mcmc=None, bin_every=1):
     """TrainStep for the configuration; targets are the GPU render of the seed-1 set (with
     sh_degree > 0: SH rest coefficients drawn from seeds 4 (target) and 3 (trained set))."""
     cams = cfg.cameras()
@@ -120,7 +123,7 @@ def build_step(cfg, torch, TrainStep, batch=1, sh_degree=0, mcmc=None):
         targets.append(tgt_maker.forward(ci).clone())
     del tgt_maker, zero
     ts = TrainStep(P0, cams, targets, K=cfg.K, S=cfg.S, k=cfg.k, batch=batch, dtype=cfg.dtype,
-                   mcmc=mcmc, **sh_0)
+                   mcmc=mcmc, bin_every=bin_every, **sh_0)
     return ts
 
 
@@ -398,6 +401,21 @@ def run_sh(args, torch, scenes, kernels, TrainStep):
     return dict(sh3_train_its=its, sh3_fwd_fps=fps,
                 sh3_kernel_us={k: kt[k] for k in ("geom_fwd", "geom_bwd_adam")},
                 sh3_note="SH degree 3 view-dependent colour on the same workload")
+
+
+def run_bin_every(args, torch, scenes, TrainStep, every=5):
+    """The headline workload at the reference trainer's default bin cadence (--bin-every 5,
+    tools/resident_traced.py:103,683): bins rebuilt on every 5th step and reused between, as
+    graphs of 8 consecutive steps per starting camera and cadence phase.  Reported beside the
+    headline, which rebins every step."""
+    cfg = scenes.CONFIGS[args.config]
+    ts = build_step(cfg, torch, TrainStep, bin_every=every)
+    n = 300
+    its = n / time_train(ts, n, 30, torch)
+    return {f"bin_every{every}_train_its": its,
+            f"bin_every{every}_note": f"bins rebuilt every {every}th step (the reference "
+                                      f"trainer's default cadence); the headline rebins every "
+                                      f"step"}
 
 
 MCMC_OPTS = dict(lambda_o=0.01, lambda_s=0.01, noise_lr=5e5, relocate_every=100,
@@ -700,6 +718,7 @@ def main():
     extra_c5 = {} if args.no_c5 else run_c5(args, torch, scenes, kernels, TrainStep)
     extra_sh = {} if args.no_sh else run_sh(args, torch, scenes, kernels, TrainStep)
     extra_mc = {} if args.no_mcmc else run_mcmc(args, torch, scenes, TrainStep)
+    extra_b5 = {} if args.no_bin5 else run_bin_every(args, torch, scenes, TrainStep)
     if args.copy_mib:
         src = torch.ones(args.copy_mib * (1 << 18), device="cuda")
         dst = torch.empty_like(src)
@@ -743,6 +762,7 @@ def main():
             **extra_c5,
             **extra_sh,
             **extra_mc,
+            **extra_b5,
         },
     }
     print(json.dumps(out))

@@ -229,25 +229,31 @@ def test_bin_every_reuses_bins_between_rebins():
         TrainStep(P, [cam, cam], [tgt, tgt], K=cfg.K, S=cfg.S, k=cfg.k, bin_every=5, batch=2)
 
 
-@pytest.mark.parametrize("bin_every", [1, 2])
+@pytest.mark.parametrize("bin_every", [1, 2, 3])
 def test_run_graphs_match_single_steps(bin_every):
-    """run(i, n) (graphs of run_len consecutive steps, then one-step graphs for the remainder)
-    leaves the same state, bit for bit, as n step() calls from step i; with bin_every > 1 it
-    falls back to step()."""
+    """run(i, n) (graphs of run_len consecutive steps, one per starting camera and bin-cadence
+    phase, then one-step graphs for the remainder) leaves the same state, bit for bit, as n
+    step() calls from step i -- also across a forward() that rebins out of cadence, after which
+    both rebin on the next step."""
     from ttsplat import scenes
     cfg, P, _ = config_inputs("c1_ref")
     cams = scenes.Config(**{**cfg.__dict__, "n_cams": 3}).cameras()
     tgts = [target_for(cfg, c) for c in cams]
     runs = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
     runs.capture(run_len=4)
-    assert bool(runs.run_graphs) == (bin_every == 1)
+    assert sorted(runs.run_graphs) == [(c, ph) for c in range(3) for ph in range(bin_every)]
     single = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
     single.capture(run_len=1)
     runs.run(1, 11)                        # two runs of 4, then 3 single steps
     for i in range(11):
         single.step((1 + i) % 3)
+    for ts in (runs, single):              # a render of camera 2 rebins out of cadence
+        ts.forward(2, grads=False)
+    runs.run(0, 9)                         # one step() (the forced rebin), then runs of 4
+    for i in range(9):
+        single.step(i % 3)
     torch.cuda.synchronize()
-    assert runs.steps_done == single.steps_done == 11
+    assert runs.steps_done == single.steps_done == 20
     for a, b in ((runs.P, single.P), (runs.m, single.m), (runs.v, single.v),
                  (runs.step_block, single.step_block)):
         assert torch.equal(a, b)

@@ -67,8 +67,9 @@ class TrainStep:
     multiple of N (and on the step after an MCMC relocation); the other steps run geometry,
     splat, loss, backward and Adam on the bins last computed -- one bin table for all cameras,
     as in that trainer.  Each camera gets a graph with and one without the binning kernels.
-    run(i, n) is n step() calls from step i on; with bin_every = 1 and no relocation it replays
-    graphs that each hold run_len consecutive steps (one graph launch per run_len steps).
+    run(i, n) is n step() calls from step i on; without relocation it replays graphs that each
+    hold run_len consecutive steps (one graph launch per run_len steps; with bin_every = N, one
+    graph per starting camera and cadence phase).
     random_bg = True: the reference trainer's --random-bg (tools/resident_traced.py:182-185,
     671-674): targets are straight RGBA [H,W,4] (spike's load_blender(keep_alpha=True)); every
     view backward first draws a background colour (Philox keyed by bg_seed, the device step
@@ -353,9 +354,10 @@ class TrainStep:
 
     def capture(self, cams=None, run_len=8):
         """Capture one HIP graph per camera.  A warm-up step runs eagerly first (so every
-        kernel's code object is resident) and its effect on the state is rolled back.  With
-        bin_every = 1, no relocation and all cameras, run_len > 1 also captures, for every
-        starting step, one graph of run_len consecutive steps (used by run())."""
+        kernel's code object is resident) and its effect on the state is rolled back.  Without
+        relocation and with all cameras, run_len > 1 also captures, for every starting step and
+        every phase of the bin cadence (the running step count mod bin_every), one graph of
+        run_len consecutive steps (used by run())."""
         cams = range(self.n_steps) if cams is None else cams
         live = [self.P, self.m, self.v, self.step_block, self.bg]
         if self.sh is not None:
@@ -390,28 +392,36 @@ class TrainStep:
                 self.enqueue_relocate()
             self.reloc_graph = g
         self.run_graphs, self.run_len = {}, 1
-        if (run_len > 1 and self.bin_every == 1 and not self.mc["relocate_every"]
+        if (run_len > 1 and not self.mc["relocate_every"]
                 and list(cams) == list(range(self.n_steps))):
             for c in cams:
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    for j in range(run_len):
-                        self.enqueue((c + j) % self.n_steps, True)
-                self.run_graphs[c] = g
+                for ph in range(self.bin_every):
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        for j in range(run_len):
+                            self.enqueue((c + j) % self.n_steps, (ph + j) % self.bin_every == 0)
+                    self.run_graphs[(c, ph)] = g
             self.run_len = run_len
         torch.cuda.synchronize(self.dev)
 
     def run(self, ci=0, n=1):
         """n training steps: step ci, ci + 1, ... (mod n_steps), as n step() calls would run
-        them; whole runs of run_len steps replay one captured graph each."""
+        them; whole runs of run_len steps replay one captured graph each (the one for their
+        first step and the bin cadence's phase there), the rest and a step that must rebin out
+        of cadence (after forward() or eval_psnr()) run as step() calls."""
         i = 0
-        if self.run_graphs:
-            while n - i >= self.run_len:
-                self.run_graphs[(ci + i) % self.n_steps].replay()
+        while i < n:
+            c = (ci + i) % self.n_steps
+            g = None
+            if n - i >= self.run_len and not self._force_rebin:
+                g = self.run_graphs.get((c, self._it % self.bin_every))
+            if g is not None:
+                g.replay()
                 self._it += self.run_len
                 i += self.run_len
-        for j in range(i, n):
-            self.step((ci + j) % self.n_steps)
+            else:
+                self.step(c)
+                i += 1
 
     def step(self, ci=0):
         """Training step ci: camera ci, or batch ci (graph replay when captured, else eager).
