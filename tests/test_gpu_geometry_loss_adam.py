@@ -61,7 +61,7 @@ def test_loss_grad(H, W):
 
 @pytest.mark.parametrize("H,W", [(11, 11), (33, 75), (96, 130), (200, 300)])
 def test_loss_grad_ragged_sizes(H, W):
-    """Sizes that do not divide the 34 x 64 tiles (ragged tiles, the 11 x 11 minimum), with x
+    """Sizes that do not divide the 40 x 64 tiles (ragged tiles, the 11 x 11 minimum), with x
     outside [0, 1] in places (the clamp gate), against the oracle; a second call into the same
     workspace gives the same result."""
     g = torch.Generator().manual_seed(H * W)

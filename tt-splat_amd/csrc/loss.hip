@@ -19,7 +19,7 @@
 //   4 transposed vertical filter (a thread = one gradient column, a run of rows, so its image
 //     loads and gradient stores are coalesced), combined as dmeanS/dx = (T'A + 2 x T'B +
 //     y T'C) / Ns, gated by 0 <= x <= 1 (the clamp), plus the L1 term (1-l) sign(x-y) / N.
-// V, D and T share one 45 KB LDS buffer (each written after a barrier that ends the reads of
+// V, D and T share one 51 KB LDS buffer (each written after a barrier that ends the reads of
 // the one before; three blocks fit a CU); the loads a phase needs from global memory are issued
 // a phase ahead.  Each block also sums S over the map pixels of its tile and |x - y| over its
 // pixels.  Nothing is exchanged between blocks: the kernel needs no workspace.
@@ -467,7 +467,11 @@ __global__ __launch_bounds__(256) void k_loss_fused(const float* __restrict__ x,
   }
 }
 
-constexpr int kTH = 34;
+// 40 rows: with 256 threads phase 4 takes exactly 4 runs of 10 rows, phases 2 and 3 use 250 of
+// the threads (5 runs on each of the 50 map rows), and V's 51 KB still lets three blocks share
+// a CU.  Measured at 1264x832: 34 rows 32.4 us, 38 rows 32.5, 40 rows 30.4, 41 rows 30.4 (42
+// rows would need 260 threads in phases 2 and 3).
+constexpr int kTH = 40;
 
 inline int fused_tiles_x(int W) { return (W + kTW - 1) / kTW; }
 inline int fused_items(int H, int W) { return 3 * fused_tiles_x(W) * ((H + kTH - 1) / kTH); }
