@@ -6,7 +6,9 @@ Headline (`value`): training iterations per second at G=100k (clustered), 1264x8
 8 orbit cameras round-robin (one camera per step), fp32: each step is geometry fwd, binning,
 fused splat fwd, L1+SSIM loss gradient, fused splat bwd (+theta bwd, per-slot gradients),
 slot gather + geometry bwd + Adam, captured as HIP graphs of 8 consecutive steps (one per
-starting camera; a remainder of K mod 8 steps replays one-step graphs).  Inputs are resident on
+starting camera; a remainder of K mod 8 steps replays one-step graphs); inside such a graph one
+launch joins each step's geometry bwd + Adam to the next step's geometry fwd and binning count
+pass (the step seam).  Inputs are resident on
 the GPU before the timed region; the timed region is exactly K steps between two
 synchronisations.
 
@@ -57,9 +59,10 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 FLOP_PER_PAIR = {"splat_fwd": 22.0, "splat_bwd": 44.0}
 LOSS_FLOP_PER_PIXEL = 1056.0  # 3 channels x (5 + 3) filtered quantities x 2 passes x 11 taps x 2
 LOSS_BYTES_PER_PIXEL = 36.0   # image and target in, dL/dimage out (fp32, 3 channels)
-# the step's single-kernel launches (roofline picks the slowest of them); geom_fwd_binning is one
-# call of four kernels (geometry + the binning's count pass, column scan, scatter, select) and
-# gets its own row as a group
+# the step's single-kernel launches (roofline picks the slowest of them, with geom_seam -- the
+# launch that joins two steps -- when the step has it); geom_fwd_binning is one call of four
+# kernels (geometry + the binning's count pass, column scan, scatter, select) and gets its own
+# row as a group
 STEP_KERNELS = ("splat_fwd", "loss_grad", "splat_bwd", "geom_bwd_adam")
 
 
@@ -308,6 +311,13 @@ def time_kernels(ts, reps, torch, kernels):
                                                        ts.lr, ts.step_block, sh_m=ts.sh_m,
                                                        sh_v=ts.sh_v, lr_sh=ts.lr_sh, **sh),
     }
+    if ts.seamed:
+        # the step seam: camera 0's backward + Adam and camera 1's geometry forward + count pass
+        # in one launch (what the step's graphs launch between two steps)
+        cam_f = ts.cams[1 % len(ts.cams)]
+        jobs["geom_seam"] = lambda: kernels.geom_bwd_adam_fwd_count(
+            ts.P, cam, cam_f, ts.gslot, ts.inv, ts.m, ts.v, ts.lr, ts.step_block, ts.proj,
+            ts.keep, ts.H, ts.W, ts.S, ts.K, ts.span, workspace=ts.bin_ws)
     if ts.batch > 1:
         del jobs["geom_bwd_adam"]
         jobs["geom_bwd_accum"] = lambda: kernels.geom_bwd_accum(ts.P, cam, ts.gslot, ts.inv,
@@ -346,12 +356,16 @@ def kernel_bytes(ts):
     table (idx + valid, 5 B per slot), count, ncand and order (12 B per tile), the inverse table
     (36 B/gaussian) and one 48-byte slot record per kept slot; geom_bwd_adam reads params, m, v
     and the inverse table and writes params, m, v (56 B each per gaussian), and gathers 36 B per
-    kept slot."""
+    kept slot; the step seam (geom_seam) moves geom_bwd_adam's bytes and writes the next view's
+    proj and keep (its forward reads the parameters it has just written, not HBM)."""
     G, T, K = ts.G, ts.tmap.T, ts.K
     nvalid = int(ts.count.long().sum())
     fwd = G * (56 + 48 + 1 + 36) + 5 * T * K + 12 * T + 48 * nvalid
     bwd = G * (6 * 56 + 36) + 36 * nvalid
-    return {"geom_fwd_binning": fwd, "geom_bwd_adam": bwd}
+    out = {"geom_fwd_binning": fwd, "geom_bwd_adam": bwd}
+    if ts.seamed:
+        out["geom_seam"] = bwd + G * (48 + 1)
+    return out
 
 
 def roofline_rows(ts, kt, pairs, cfg_name):
@@ -699,7 +713,7 @@ def main():
     per_cam = time_splat_per_camera(ts, max(10, args.kernel_reps // 2), torch, kernels)
     pairs = per_cam[0]["pairs"]
     rows = roofline_rows(ts, kt, pairs, cfg.name)
-    dom = max(STEP_KERNELS, key=lambda n: kt[n])
+    dom = max(STEP_KERNELS + (("geom_seam",) if ts.seamed else ()), key=lambda n: kt[n])
     roofline = dict(rows[dom], kernel=dom, camera=0,
                     convention="the step's slowest single-kernel launch (HIP-event duration over graph "
                                "replays of 20 launches, camera 0, the best of 3 averages after "

@@ -370,6 +370,37 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
                              int32_t* pos_count, void* workspace, size_t workspace_bytes,
                              hipStream_t stream);
 
+/* The seam between two training steps in one launch: tts_geom_bwd_adam of step i (camera_bwd,
+ * its slot gradients gslot through inv; gparams may be NULL) followed by the geometry forward
+ * of step i+1 (camera_fwd, into proj and keep) and the count pass of its binning into the
+ * workspace -- the first kernel of tts_geom_fwd_assign_bins for that view.  Finish the binning
+ * with tts_assign_bins_counted on the same workspace.  The results equal tts_geom_bwd_adam
+ * followed by tts_geom_fwd_assign_bins.  Supports the plain step only (no SH rest
+ * coefficients, depth weight or MCMC terms: those take the two calls) and G <= 131072
+ * (TTS_EG otherwise); no step advance (tts_assign_bins_counted carries step i+1's).  Replaces
+ * the reference trainer's adam_fused of one iteration (tools/resident_traced.py:383-427,
+ * 739-740) and the geom_fwd + do_bin count of the next (:682-686, geom_fwd :327-346, do_bin
+ * :519-539). */
+int tts_geom_bwd_adam_fwd_count(float* params, int G, const float* camera_bwd,
+                                const float* camera_fwd, float near_z, float blur,
+                                const float* gslot, const int32_t* inv, float* gparams, float* m,
+                                float* v, const float* lr, const int32_t* step, float beta1,
+                                float beta2, float eps, float* proj, uint8_t* keep, int H, int W,
+                                int S, int R, int K, int span, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream);
+
+/* The rest of tts_geom_fwd_assign_bins after tts_geom_bwd_adam_fwd_count ran its count pass
+ * into the workspace: the binning's column scan, scatter and select on proj / keep, with the
+ * same outputs (idx, valid, count, ncand, inv, order, slot records) as that call.  step_adv
+ * (optional): the training step's Adam step block, advanced by the column scan as
+ * tts_adam_advance would (step i+1's advance; tools/resident_traced.py:478-481).  Replaces
+ * do_bin (tools/resident_traced.py:519-539) after its count. */
+int tts_assign_bins_counted(const float* proj, const uint8_t* keep, int G, int H, int W, int S,
+                            int R, int K, int span, int32_t* idx, uint8_t* valid, int32_t* count,
+                            int32_t* ncand, int32_t* inv, int32_t* order, float* slot_rec,
+                            int32_t* pos_count, int32_t* step_adv, float beta1, float beta2,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Geometry backward with SH colour and/or the depth weight: grad9 -> gparams[G,14], gsh_rest
  * (rest layout; rows beyond the degree written as zero; needed when sh_degree > 0), gdepth [G,2]
  * (optional).  Replaces tools/resident_traced.py:397-427 (geom_bwd) with its SH and depth-weight

@@ -112,3 +112,90 @@ def test_geom_fwd_assign_bins_largest_grid():
     print(f"[geom+bins] {cfg.W}x{cfg.H} G={cfg.G}", flush=True)
     a, b = two_ways(cfg, P.cuda(), cam)
     check_equal(a, b, cfg.K)
+
+
+@pytest.mark.parametrize("name,G", [("c4", None), ("c1_ref", 700), ("c3", 131072)])
+def test_step_seam_equals_backward_then_forward_binning(name, G):
+    """The step seam -- tts_geom_bwd_adam_fwd_count (step i's geometry backward + Adam, step
+    i+1's geometry forward and count pass in one launch), then tts_assign_bins_counted (the
+    rest of the binning, carrying step i+1's Adam step advance) -- against tts_geom_bwd_adam
+    followed by tts_geom_fwd_assign_bins with the advance: params, m, v, the step block, the
+    next view's proj, keep, bins, counts and inverse table bit for bit; the tile order a
+    heaviest-first permutation and the slot records those of the bins in that order.  G = 700
+    leaves the last block's second half empty; G = 131072 is the largest G the seam takes."""
+    from helpers import anisotropic
+    cfg, P, cam = config_inputs(name, G=G)
+    dev = "cuda"
+    G = P.shape[0]
+    T = (cfg.H // cfg.S) * (cfg.W // cfg.S)
+    cam_b, cam_f = cam.device_block(dev), anisotropic(cam).device_block(dev)
+    print(f"[seam] {name} G={G}", flush=True)
+    gen = torch.Generator().manual_seed(9)
+    P0 = P.cuda()
+    m0 = (0.01 * torch.randn(G, 14, generator=gen)).cuda()
+    v0 = (1e-4 * torch.rand(G, 14, generator=gen)).cuda()
+    lr = torch.full((14,), 1e-3, device=dev)
+    lr[:3] = 1.6e-4
+    inv_b = torch.empty(G, 9, dtype=torch.int32, device=dev)    # step i's bins (camera b)
+    kernels.geom_fwd_assign_bins(P0, cam_b, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span, inv=inv_b)
+    gslot = torch.randn(T, cfg.K, 9, generator=gen).cuda() * 1e-3
+    outs = []
+    for seam in (False, True):
+        Pw, m, v = P0.clone(), m0.clone(), v0.clone()
+        step = kernels.adam_state(dev)
+        kernels.adam_advance(step)                                # step i's advance
+        inv = torch.full((G, 9), -7, dtype=torch.int32, device=dev)
+        order = torch.empty(T, dtype=torch.int32, device=dev)
+        rec = torch.full((T, cfg.K, 12), float("nan"), device=dev)
+        pos = torch.full((T,), -1, dtype=torch.int32, device=dev)
+        idx = torch.empty(T, cfg.K, dtype=torch.int32, device=dev)
+        valid = torch.empty(T, cfg.K, dtype=torch.uint8, device=dev)
+        count = torch.empty(T, dtype=torch.int32, device=dev)
+        ncand = torch.empty(T, dtype=torch.int32, device=dev)
+        proj = torch.empty(G, 12, device=dev)
+        keep = torch.empty(G, dtype=torch.uint8, device=dev)
+        if seam:
+            ws = kernels.geom_bwd_adam_fwd_count(Pw, cam_b, cam_f, gslot, inv_b, m, v, lr, step,
+                                                 proj, keep, cfg.H, cfg.W, cfg.S, cfg.K,
+                                                 cfg.span)
+            kernels.assign_bins_counted(proj, keep, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span, ws,
+                                        idx, valid, count, ncand, inv=inv, order=order,
+                                        slot_rec=rec, pos_count=pos, advance=step)
+        else:
+            kernels.geom_bwd_adam(Pw, cam_b, gslot, inv_b, m, v, lr, step)
+            kernels.geom_fwd_assign_bins(Pw, cam_f, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span,
+                                         proj=proj, keep=keep, advance=step, idx=idx,
+                                         valid=valid, count=count, ncand=ncand, inv=inv,
+                                         order=order, slot_rec=rec, pos_count=pos)
+        torch.cuda.synchronize()
+        outs.append(dict(P=Pw, m=m, v=v, step=step, proj=proj, keep=keep, idx=idx, valid=valid,
+                         count=count, ncand=ncand, inv=inv, order=order, rec=rec, pos=pos))
+    a, b = outs
+    for k in ("P", "m", "v", "step", "proj", "keep", "idx", "valid", "count", "ncand", "inv"):
+        assert torch.equal(a[k], b[k]), k
+    assert int(b["step"][0]) == 2
+    assert not torch.equal(b["P"], P0)
+    ol = b["order"].long()
+    assert torch.equal(torch.sort(ol).values, torch.arange(T, device=ol.device))
+    kept = b["count"].long()[ol]
+    assert bool((kept[1:] <= kept[:-1]).all())
+    assert torch.equal(b["pos"].long(), kept)
+    s = torch.arange(cfg.K, device=dev)
+    live = s[None, :] < kept[:, None]                             # [T(p), K]
+    want = b["proj"][b["idx"].long()[ol]]                         # [T(p), K, 12]
+    assert torch.equal(b["rec"][live], want[live])
+
+
+def test_step_seam_refuses_large_g():
+    cfg, P, cam = config_inputs("c4", G=131073)
+    camera = cam.device_block("cuda")
+    with pytest.raises(ValueError):
+        kernels.geom_bwd_adam_fwd_count(P.cuda(), camera, camera, torch.zeros(1, 1, 9, device="cuda"),
+                                        torch.zeros(cfg.G, 9, dtype=torch.int32, device="cuda"),
+                                        torch.zeros(cfg.G, 14, device="cuda"),
+                                        torch.zeros(cfg.G, 14, device="cuda"),
+                                        torch.zeros(14, device="cuda"),
+                                        kernels.adam_state("cuda"),
+                                        torch.empty(cfg.G, 12, device="cuda"),
+                                        torch.empty(cfg.G, dtype=torch.uint8, device="cuda"),
+                                        cfg.H, cfg.W)

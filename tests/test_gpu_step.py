@@ -437,3 +437,60 @@ def test_eval_psnr_renders_on_white():
     ts.step(0)
     torch.cuda.synchronize()
     assert int(ts.step_block[0]) == 6
+
+
+@pytest.mark.parametrize("mode", ["random_bg", "keep_grad", "bf16"])
+def test_seamed_runs_match_single_steps(mode):
+    """run() on a plain step joins consecutive steps at the seam (one launch for step i's
+    geometry backward + Adam and step i+1's geometry forward + binning count; step i+1's Adam
+    advance on its column scan).  With a random background (drawn between the two launches,
+    before the advance, as step() draws it), with the per-step gradient kept, and with the bf16
+    render, 2 runs of 5 steps and 3 single steps leave the state step() calls leave, bit for
+    bit: parameters, moments, step block, background, gradient and loss."""
+    from ttsplat import scenes
+    cfg, P, _ = config_inputs("c2" if mode == "bf16" else "c1_ref")
+    cams = scenes.Config(**{**cfg.__dict__, "n_cams": 3}).cameras()
+    kw = dict(K=cfg.K, S=cfg.S, k=cfg.k, dtype=cfg.dtype)
+    if mode == "random_bg":
+        tgts = [rgba_target(cfg, c) for c in cams]
+        kw.update(random_bg=True, bg_seed=5)
+    else:
+        tgts = [target_for(cfg, c) for c in cams]
+    if mode == "keep_grad":
+        kw.update(keep_grad=True)
+    runs = TrainStep(P, cams, tgts, **kw)
+    assert runs.seamed
+    runs.capture(run_len=5)
+    single = TrainStep(P, cams, tgts, **kw)
+    single.capture(run_len=1)
+    runs.run(2, 13)
+    for i in range(13):
+        single.step((2 + i) % 3)
+    torch.cuda.synchronize()
+    for a, b in ((runs.P, single.P), (runs.m, single.m), (runs.v, single.v),
+                 (runs.step_block, single.step_block), (runs.bg, single.bg),
+                 (runs.image, single.image)):
+        assert torch.equal(a, b)
+    if mode == "keep_grad":
+        assert torch.equal(runs.gparams, single.gparams)
+    assert float(runs.loss()) == float(single.loss())
+    assert int(runs.step_block[0]) == 13
+
+
+def test_step_configurations_without_a_seam():
+    """SH colour, the depth weight, MCMC terms, bin_every > 1 and batches keep the two
+    launches (TrainStep.seamed is False), and enqueue_seamed refuses them."""
+    from ttsplat import scenes
+    cfg, P, cam = config_inputs("c1_ref")
+    tgt = target_for(cfg, cam)
+    base = dict(K=cfg.K, S=cfg.S, k=cfg.k)
+    assert TrainStep(P, [cam], [tgt], **base).seamed
+    for kw in (dict(bin_every=2), dict(depth_weight=dict(beta0=1.0, tau0=3.0, lr_bt=0.02)),
+               dict(mcmc=dict(lambda_o=0.01)),
+               dict(sh_degree=1, sh_rest=torch.zeros(cfg.G, 15, 3))):
+        ts = TrainStep(P, [cam], [tgt], **base, **kw)
+        assert not ts.seamed, kw
+        with pytest.raises(ValueError):
+            ts.enqueue_seamed(0, 2)
+    cams = scenes.Config(**{**cfg.__dict__, "n_cams": 2}).cameras()
+    assert not TrainStep(P, cams, [tgt, tgt], batch=2, **base).seamed

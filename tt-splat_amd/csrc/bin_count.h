@@ -245,5 +245,15 @@ int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degr
                           float blur, float* proj, uint8_t* keep, int32_t* step_adv, float b1,
                           float b2, int ntx, int nty, float S, int span, int NB, int Tpad,
                           int* mat, int2* cell_slot, hipStream_t stream);
+// The step seam (geometry.hip): geometry backward + Adam of one view, then the geometry forward
+// of the next view with the count pass, for count blocks of CountSmall.  Its LDS request
+// (geom_seam_lds: the larger of the staged rows and the count pass's histogram) fits whenever
+// bin_check accepts the grid.
+size_t geom_seam_lds(int NB, int Tpad);
+int launch_geom_seam(float* params, int G, const float* cam_b, const float* cam_f, float near_z,
+                     float blur, const float* gslot, const int32_t* inv, float* gparams, float* m,
+                     float* v, const float* lr, const int32_t* step, float b1, float b2,
+                     float eps, float* proj, uint8_t* keep, int ntx, int nty, float S, int span,
+                     int NB, int Tpad, int* mat, int2* cell_slot, hipStream_t stream);
 
 }  // namespace tts

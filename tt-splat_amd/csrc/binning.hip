@@ -107,15 +107,19 @@ __global__ __launch_bounds__(NT) void k_bin_count(
 // exclusive prefix over count blocks (a block's base in the cell).  Also the column totals
 // tot[x], their exclusive prefix inside the chunk within[x], and the chunk's total.  Block 0
 // also zeroes the counters the scatter pass's classification blocks accumulate into.
+// adv (optional): a training step's Adam step block, advanced by block 0 (the step's advance when
+// the count pass ran in the previous step's backward launch).
 __global__ __launch_bounds__(1024) void k_bin_colscan(int* __restrict__ mat, int nblk, int X,
                                                       int* __restrict__ tot,
                                                       int* __restrict__ within,
                                                       int* __restrict__ chunk_tot,
-                                                      int* __restrict__ cls_ctr, int n_ctr) {
+                                                      int* __restrict__ cls_ctr, int n_ctr,
+                                                      int32_t* adv, float b1, float b2) {
   __shared__ int s_seg[16][kChunk];
   // the scatter pass's list counters start from zero
   if (blockIdx.x == 0)
     for (int i = threadIdx.x; i < n_ctr; i += 1024) cls_ctr[i] = 0;
+  if (adv && blockIdx.x == 0 && threadIdx.x == 0) advance_step(adv, b1, b2);
   const int col = threadIdx.x & (kChunk - 1), seg = threadIdx.x >> 6;
   const int x = blockIdx.x * kChunk + col;
   const int rows = (nblk + 15) / 16;
@@ -1279,7 +1283,8 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
                    int G, int H, int W, int S, int K, int span, int32_t* idx, uint8_t* valid,
                    int32_t* count, int32_t* ncand, int32_t* inv, int32_t* order,
                    const float* proj, float* rec, int32_t* pos_count, const BinWorkspace& ws,
-                   bool counted, hipStream_t stream) {
+                   bool counted, hipStream_t stream, int32_t* adv = nullptr, float b1 = 0.f,
+                   float b2 = 0.f) {
   const int ntx = W / S, nty = H / S, T = ntx * nty;
   const float Sf = static_cast<float>(S);
   const int NB = ws.NB, Tpad = ws.Tpad, nblk = ws.nblk;
@@ -1306,7 +1311,7 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
   }
   k_bin_colscan<<<(X + kChunk - 1) / kChunk, 1024, 0, stream>>>(ws.mat, nblk, X, ws.tot,
                                                                 ws.within, ws.chunk_tot,
-                                                                ws.nlist, 2);
+                                                                ws.nlist, 2, adv, b1, b2);
   const int ncls = (T + 1023) / 1024;
   ScatterArgs sc{mu2d, mu_stride, G, ntx, nty, NB, Tpad, K, ws.cblock, ncls, ws.cell_slot,
                  ws.mat, ws.tot, ws.within, ws.chunk_tot, ws.cell_start, ws.far_start, ws.recs,
@@ -1435,6 +1440,59 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
   if (e != TTS_OK) return e;
   return bin_run(proj, 12, keep, 1, G, H, W, S, K, span, idx, valid, count, ncand, inv, order,
                  proj, slot_rec, pos_count, ws, fused, stream);
+}
+
+// The seam between two training steps (k_geom_bwd_adam_fwd_count): tts_geom_bwd_adam for
+// camera_bwd, then tts_geom_fwd_ex for camera_fwd and the binning's count pass of that view
+// into the workspace, in one launch (count blocks of 512 gaussians: G <= 131072).  The binning
+// then finishes with tts_assign_bins_counted on the same workspace.
+int tts_geom_bwd_adam_fwd_count(float* params, int G, const float* camera_bwd,
+                                const float* camera_fwd, float near_z, float blur,
+                                const float* gslot, const int32_t* inv, float* gparams, float* m,
+                                float* v, const float* lr, const int32_t* step, float beta1,
+                                float beta2, float eps, float* proj, uint8_t* keep, int H, int W,
+                                int S, int R, int K, int span, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  if (G <= 0 || !params || !camera_bwd || !camera_fwd || !gslot || !inv || !m || !v || !lr ||
+      !step || !proj || !keep)
+    return TTS_EINVAL;
+  if (count_block(G) != CountSmall::kBlock) return TTS_EG;
+  // bin_check's table arguments are not written here: any non-null pointers pass its check
+  const int rc = bin_check(proj, 12, keep, 1, G, H, W, S, R, K, span,
+                           reinterpret_cast<const int32_t*>(proj), keep);
+  if (rc != TTS_OK) return rc;
+  const int ntx = W / S, nty = H / S;
+  if (!workspace || workspace_bytes < bin_ws_layout(G, ntx, nty, nullptr, nullptr))
+    return TTS_EWORKSPACE;
+  BinWorkspace ws;
+  bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
+  return launch_geom_seam(params, G, camera_bwd, camera_fwd, near_z, blur, gslot, inv, gparams,
+                          m, v, lr, step, beta1, beta2, eps, proj, keep, ntx, nty,
+                          static_cast<float>(S), span, ws.NB, ws.Tpad, ws.mat, ws.cell_slot,
+                          stream);
+}
+
+// The binning passes after a count pass that already ran into the workspace (the seam launch
+// above): column scan, scatter, select -- the rest of tts_geom_fwd_assign_bins, with the same
+// outputs.  step_adv (optional): the training step's Adam step block, advanced by the column
+// scan.
+int tts_assign_bins_counted(const float* proj, const uint8_t* keep, int G, int H, int W, int S,
+                            int R, int K, int span, int32_t* idx, uint8_t* valid, int32_t* count,
+                            int32_t* ncand, int32_t* inv, int32_t* order, float* slot_rec,
+                            int32_t* pos_count, int32_t* step_adv, float beta1, float beta2,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (G <= 0 || !proj || !keep) return TTS_EINVAL;
+  if (slot_rec && (!pos_count || !order)) return TTS_EINVAL;
+  if (count_block(G) != CountSmall::kBlock) return TTS_EG;
+  const int rc = bin_check(proj, 12, keep, 1, G, H, W, S, R, K, span, idx, valid);
+  if (rc != TTS_OK) return rc;
+  const int ntx = W / S, nty = H / S;
+  if (!workspace || workspace_bytes < bin_ws_layout(G, ntx, nty, nullptr, nullptr))
+    return TTS_EWORKSPACE;
+  BinWorkspace ws;
+  bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
+  return bin_run(proj, 12, keep, 1, G, H, W, S, K, span, idx, valid, count, ncand, inv, order,
+                 proj, slot_rec, pos_count, ws, true, stream, step_adv, beta1, beta2);
 }
 
 }  // extern "C"

@@ -20,6 +20,8 @@
 
 #include <math.h>
 
+#include <atomic>
+
 #include "bin_count.h"
 
 namespace tts {
@@ -413,19 +415,23 @@ __device__ __forceinline__ Camera load_camera(const float* __restrict__ cam) {
 // and masks its writes), so all of a thread's loads are in flight before the first LDS write:
 // a loop bounded by rows * W would wait out one memory round trip per word.
 constexpr int kGeoBlock = 256;
+constexpr int kSeamRow = 3 * 15 + 9;  // floats of one staged row of the step seam (params, m, v, inv)
+// tid: the thread's index among the kGeoBlock threads that copy these rows (threadIdx.x, or
+// its index in its half of a 512-thread block).
 template <int W, typename T>
-__device__ __forceinline__ void stage_load(const T* __restrict__ src, int g0, int rows, T (&r)[W]) {
+__device__ __forceinline__ void stage_load(const T* __restrict__ src, int g0, int rows, T (&r)[W],
+                                           int tid = threadIdx.x) {
   const T* base = src + (int64_t)g0 * W;
   const int last = rows * W - 1;
 #pragma unroll
-  for (int k = 0; k < W; ++k) r[k] = base[min((int)threadIdx.x + k * kGeoBlock, last)];
+  for (int k = 0; k < W; ++k) r[k] = base[min(tid + k * kGeoBlock, last)];
 }
 template <int W, int SW, typename T>
-__device__ __forceinline__ void stage_put(const T (&r)[W], int rows, T* s) {
+__device__ __forceinline__ void stage_put(const T (&r)[W], int rows, T* s, int tid = threadIdx.x) {
   const int n = rows * W;
 #pragma unroll
   for (int k = 0; k < W; ++k) {
-    const int i = threadIdx.x + k * kGeoBlock;
+    const int i = tid + k * kGeoBlock;
     if (i < n) s[(i / W) * SW + i % W] = r[k];
   }
 }
@@ -436,18 +442,19 @@ __device__ __forceinline__ void stage_in(const T* __restrict__ src, int g0, int 
   stage_put<W, SW>(r, rows, s);
 }
 template <int W, int SW, typename T>
-__device__ __forceinline__ void stage_out(T* __restrict__ dst, int g0, int rows, const T* s) {
+__device__ __forceinline__ void stage_out(T* __restrict__ dst, int g0, int rows, const T* s,
+                                          int tid = threadIdx.x) {
   T* base = dst + (int64_t)g0 * W;
   const int n = rows * W;
   T r[W];
 #pragma unroll
   for (int k = 0; k < W; ++k) {
-    const int i = min((int)threadIdx.x + k * kGeoBlock, n - 1);
+    const int i = min(tid + k * kGeoBlock, n - 1);
     r[k] = s[(i / W) * SW + i % W];
   }
 #pragma unroll
   for (int k = 0; k < W; ++k) {
-    const int i = threadIdx.x + k * kGeoBlock;
+    const int i = tid + k * kGeoBlock;
     if (i < n) base[i] = r[k];
   }
 }
@@ -492,18 +499,6 @@ __device__ __forceinline__ void gather_slots(const float* __restrict__ gslot, co
   SlotRecs r;
   slot_loads(gslot, e, r);
   slot_sum(e, r, gin);
-}
-
-// Adam step block: step[0] int32 step number; step[1..2] fp32 1/bc1 and 1/sqrt(bc2) for that
-// step (double-precision powers, as torch.optim.Adam's host-side bias corrections).  One thread.
-__device__ __forceinline__ void advance_step(int32_t* step, float b1, float b2) {
-  const int t = step[0] + 1;
-  step[0] = t;
-  const double bc1 = 1.0 - pow((double)b1, (double)t);
-  const double bc2 = 1.0 - pow((double)b2, (double)t);
-  float* f = reinterpret_cast<float*>(step);
-  f[1] = (float)(1.0 / bc1);
-  f[2] = (float)(1.0 / sqrt(bc2));
 }
 
 // adv (optional): a training step's Adam step block, advanced by block 0 after its rows (what a
@@ -768,33 +763,18 @@ struct McmcArgs {
   float reg_o, reg_s, noise_lr;
   uint32_t seed;
 };
+// One row of the geometry backward + Adam: row t of a block's staged rows (s_p, s_m, s_v at
+// stride 15, s_inv at stride 9), gaussian g.  The slot gradients are gathered through the
+// row's inverse-table entries, the forward recomputed, the chain rule applied (plus the MCMC
+// regulariser), and the new parameters and moments written back over the row.
 template <bool SH, bool MC>
-__global__ __launch_bounds__(256) void k_geom_bwd_adam(
-    float* __restrict__ params, int G, float* __restrict__ rest, float* __restrict__ sh_m,
-    float* __restrict__ sh_v, int n_rest, const float* __restrict__ camera, float near_z,
-    float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv,
-    float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
-    const float* __restrict__ lr, const float* __restrict__ lr_sh,
-    const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc, DepthW dwa) {
-  __shared__ float s_p[kGeoBlock * 15], s_m[kGeoBlock * 15], s_v[kGeoBlock * 15];
-  __shared__ int s_inv[kGeoBlock * 9];
-  const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
-  const int g = g0 + threadIdx.x;
-  {  // all four row copies in flight at once
-    int ri[9];
-    float rp[14], rm[14], rv[14];
-    stage_load<9>(inv, g0, rows, ri);
-    stage_load<14>(params, g0, rows, rp);
-    stage_load<14>(m, g0, rows, rm);
-    stage_load<14>(v, g0, rows, rv);
-    stage_put<9, 9>(ri, rows, s_inv);
-    stage_put<14, 15>(rp, rows, s_p);
-    stage_put<14, 15>(rm, rows, s_m);
-    stage_put<14, 15>(rv, rows, s_v);
-  }
-  __syncthreads();
-  if ((int)threadIdx.x < rows) {
-  const int t = threadIdx.x;
+__device__ __forceinline__ void bwd_adam_row(
+    int t, int g, int G, float* s_p, float* s_m, float* s_v, const int* s_inv,
+    float* __restrict__ rest, float* __restrict__ sh_m, float* __restrict__ sh_v, int n_rest,
+    const float* __restrict__ camera, float near_z, float blur, const float* __restrict__ gslot,
+    float* __restrict__ gparams, const float* __restrict__ lr, const float* __restrict__ lr_sh,
+    const int32_t* __restrict__ step, float b1, float b2, float eps, const McmcArgs& mc,
+    const DepthW& dwa) {
   int e[9];
 #pragma unroll
   for (int j = 0; j < 9; ++j) e[j] = s_inv[t * 9 + j];
@@ -857,11 +837,110 @@ __global__ __launch_bounds__(256) void k_geom_bwd_adam(
       }
     }
   }
-  }  // active row
+}
+
+template <bool SH, bool MC>
+__global__ __launch_bounds__(256) void k_geom_bwd_adam(
+    float* __restrict__ params, int G, float* __restrict__ rest, float* __restrict__ sh_m,
+    float* __restrict__ sh_v, int n_rest, const float* __restrict__ camera, float near_z,
+    float blur, const float* __restrict__ gslot, const int32_t* __restrict__ inv,
+    float* __restrict__ gparams, float* __restrict__ m, float* __restrict__ v,
+    const float* __restrict__ lr, const float* __restrict__ lr_sh,
+    const int32_t* __restrict__ step, float b1, float b2, float eps, McmcArgs mc, DepthW dwa) {
+  __shared__ float s_p[kGeoBlock * 15], s_m[kGeoBlock * 15], s_v[kGeoBlock * 15];
+  __shared__ int s_inv[kGeoBlock * 9];
+  const int g0 = blockIdx.x * kGeoBlock, rows = min(kGeoBlock, G - g0);
+  const int g = g0 + threadIdx.x;
+  {  // all four row copies in flight at once
+    int ri[9];
+    float rp[14], rm[14], rv[14];
+    stage_load<9>(inv, g0, rows, ri);
+    stage_load<14>(params, g0, rows, rp);
+    stage_load<14>(m, g0, rows, rm);
+    stage_load<14>(v, g0, rows, rv);
+    stage_put<9, 9>(ri, rows, s_inv);
+    stage_put<14, 15>(rp, rows, s_p);
+    stage_put<14, 15>(rm, rows, s_m);
+    stage_put<14, 15>(rv, rows, s_v);
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < rows)
+    bwd_adam_row<SH, MC>(threadIdx.x, g, G, s_p, s_m, s_v, s_inv, rest, sh_m, sh_v, n_rest, camera,
+                         near_z, blur, gslot, gparams, lr, lr_sh, step, b1, b2, eps, mc, dwa);
   __syncthreads();
   stage_out<14, 15>(params, g0, rows, s_p);
   stage_out<14, 15>(m, g0, rows, s_m);
   stage_out<14, 15>(v, g0, rows, s_v);
+}
+
+// The seam between two training steps in one launch: step i's geometry backward + Adam
+// (camera cam_b, its slot gradients) and step i+1's geometry forward (camera cam_f) with the
+// binning's count pass.  A gaussian's forward needs nothing of step i but its own new
+// parameters, and a count block's rows are its own 512 gaussians, so no block waits on another:
+// each 512-thread block runs k_geom_bwd_adam's row body on its two 256-row halves, writes the
+// rows back, then projects the new rows it still holds in LDS and counts them, as
+// k_geom_fwd_count does (the same proj, keep, count-matrix rows and cell slots).  What this
+// saves against the two launches: one kernel boundary and the parameter reload.  No SH, depth
+// weight or MCMC terms (callers take the two launches for those), and no step advance: step
+// i+1's advance rides on the next binning pass (tts_assign_bins_counted), after every block
+// here has read step i's bias corrections.
+__global__ __launch_bounds__(512) void k_geom_bwd_adam_fwd_count(
+    float* __restrict__ params, int G, const float* __restrict__ cam_b,
+    const float* __restrict__ cam_f, float near_z, float blur, const float* __restrict__ gslot,
+    const int32_t* __restrict__ inv, float* __restrict__ gparams, float* __restrict__ m,
+    float* __restrict__ v, const float* __restrict__ lr, const int32_t* __restrict__ step,
+    float b1, float b2, float eps, float* __restrict__ proj, uint8_t* __restrict__ keep, int ntx,
+    int nty, float S, int span, int NB, int Tpad, int* __restrict__ mat,
+    int2* __restrict__ cell_slot) {
+  static_assert(CountFused::kBlock == 2 * kGeoBlock, "one count block = two row halves");
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  const int half = threadIdx.x / kGeoBlock, lt = threadIdx.x % kGeoBlock;
+  float* s_p = s_dyn + half * kGeoBlock * kSeamRow;   // this half's rows: params, m, v, inv
+  float* s_m = s_p + kGeoBlock * 15;
+  float* s_v = s_m + kGeoBlock * 15;
+  int* s_inv = reinterpret_cast<int*>(s_v + kGeoBlock * 15);
+  const int g0 = blockIdx.x * 2 * kGeoBlock + half * kGeoBlock;
+  const int rows = min(kGeoBlock, G - g0);  // <= 0: the block's second half lies past G
+  if (rows > 0) {  // all four row copies in flight at once
+    int ri[9];
+    float rp[14], rm[14], rv[14];
+    stage_load<9>(inv, g0, rows, ri, lt);
+    stage_load<14>(params, g0, rows, rp, lt);
+    stage_load<14>(m, g0, rows, rm, lt);
+    stage_load<14>(v, g0, rows, rv, lt);
+    stage_put<9, 9>(ri, rows, s_inv, lt);
+    stage_put<14, 15>(rp, rows, s_p, lt);
+    stage_put<14, 15>(rm, rows, s_m, lt);
+    stage_put<14, 15>(rv, rows, s_v, lt);
+  }
+  __syncthreads();
+  if (lt < rows)
+    bwd_adam_row<false, false>(lt, g0 + lt, G, s_p, s_m, s_v, s_inv, nullptr, nullptr, nullptr, 0,
+                               cam_b, near_z, blur, gslot, gparams, lr, nullptr, step, b1, b2,
+                               eps, McmcArgs{0.0f, 0.0f, 0.0f, 0u},
+                               DepthW{nullptr, nullptr, 1.0f, 0, 0});
+  __syncthreads();
+  if (rows > 0) {
+    stage_out<14, 15>(params, g0, rows, s_p, lt);
+    stage_out<14, 15>(m, g0, rows, s_m, lt);
+    stage_out<14, 15>(v, g0, rows, s_v, lt);
+  }
+  __syncthreads();  // every read of s_m is done: its space takes the projection rows
+  float* s_o = s_m;
+  float mux = 0.f, muy = 0.f;
+  uint8_t kept = 0;
+  if (lt < rows) {
+    const Camera cam = load_camera(cam_f);
+    geo_fwd_row<false>(s_p + lt * 15, g0 + lt, G, nullptr, 0, nullptr, cam, near_z, blur,
+                       s_o + lt * 13, keep, &mux, &muy, &kept);
+  }
+  __syncthreads();
+  if (rows > 0) stage_out<12, 13>(proj, g0, rows, s_o, lt);
+  __syncthreads();  // every staging read is done: the count pass reuses the LDS
+  const float mx[1] = {mux}, my[1] = {muy};
+  const uint8_t kv[1] = {kept};
+  count_body<512, 1>(mx, my, kv, G, ntx, nty, S, span, NB, Tpad, reinterpret_cast<int*>(s_dyn),
+                     mat, cell_slot);
 }
 
 // Batch form: gacc[g] += scale * dL/dparams[g] for one view (one writer per gaussian); with SH
@@ -1045,6 +1124,36 @@ int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degr
     k_geom_fwd_count<false><<<nblk, 512, lds, stream>>>(
         params, G, nullptr, 0, depth_bt, camera, near_z, blur, proj, keep, step_adv, b1, b2, ntx,
         nty, S, span, NB, Tpad, mat, cell_slot);
+  return launch_status();
+}
+
+size_t geom_seam_lds(int NB, int Tpad) {
+  const size_t stage = sizeof(float) * 2 * kGeoBlock * kSeamRow;
+  const size_t cnt = sizeof(int) * ((size_t)Tpad + (size_t)CountFused::kWaves * NB);
+  return stage > cnt ? stage : cnt;
+}
+
+int launch_geom_seam(float* params, int G, const float* cam_b, const float* cam_f, float near_z,
+                     float blur, const float* gslot, const int32_t* inv, float* gparams, float* m,
+                     float* v, const float* lr, const int32_t* step, float b1, float b2,
+                     float eps, float* proj, uint8_t* keep, int ntx, int nty, float S, int span,
+                     int NB, int Tpad, int* mat, int2* cell_slot, hipStream_t stream) {
+  const int nblk = (G + CountFused::kBlock - 1) / CountFused::kBlock;
+  const size_t lds = geom_seam_lds(NB, Tpad);
+  if (lds > kMaxLdsBytes) return TTS_EINVAL;
+  // the kernel's dynamic-LDS limit, raised once to the most it can ask for (the first call
+  // should not be under graph capture: TrainStep makes one before it captures)
+  static std::atomic<int> lds_ready{0};
+  if (!lds_ready.load()) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_geom_bwd_adam_fwd_count),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxLdsBytes));
+    if (e != hipSuccess) return static_cast<int>(e);
+    lds_ready.store(1);
+  }
+  k_geom_bwd_adam_fwd_count<<<nblk, 512, lds, stream>>>(
+      params, G, cam_b, cam_f, near_z, blur, gslot, inv, gparams, m, v, lr, step, b1, b2, eps,
+      proj, keep, ntx, nty, S, span, NB, Tpad, mat, cell_slot);
   return launch_status();
 }
 

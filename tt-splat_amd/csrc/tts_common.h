@@ -33,6 +33,18 @@ __device__ __forceinline__ long long f2i64_x86(float f) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Adam step block: step[0] int32 step number; step[1..2] fp32 1/bc1 and 1/sqrt(bc2) for that
+// step (double-precision powers, as torch.optim.Adam's host-side bias corrections).  One thread.
+__device__ __forceinline__ void advance_step(int32_t* step, float b1, float b2) {
+  const int t = step[0] + 1;
+  step[0] = t;
+  const double bc1 = 1.0 - pow((double)b1, (double)t);
+  const double bc2 = 1.0 - pow((double)b2, (double)t);
+  float* f = reinterpret_cast<float*>(step);
+  f[1] = (float)(1.0 / bc1);
+  f[2] = (float)(1.0 / sqrt(bc2));
+}
+
 // relu with torch's NaN rule (torch.relu and clamp(min=0) keep a NaN):
 //   relu_nan: u <= 0 -> +0, else u; a NaN of either sign fails the compare and passes through.
 //   relu_bits: one integer max on the bit pattern.  Equal to relu_nan for every u except a NaN

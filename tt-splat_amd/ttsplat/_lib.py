@@ -73,6 +73,13 @@ SIGNATURES = {
                                           _vp, _vp, _vp, _c_float, _c_float, _c_int, _c_int,
                                           _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
                                           _vp, _vp, _vp, _vp, _vp, _c_size, _vp]),
+    "tts_geom_bwd_adam_fwd_count": (_c_int, [_vp, _c_int, _vp, _vp, _c_float, _c_float, _vp, _vp,
+                                             _vp, _vp, _vp, _vp, _vp, _c_float, _c_float,
+                                             _c_float, _vp, _vp, _c_int, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _vp, _c_size, _vp]),
+    "tts_assign_bins_counted": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                         _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _c_float, _c_float, _vp, _c_size, _vp]),
     "tts_geom_bwd_ex": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _vp, _c_float, _c_float,
                                  _vp, _vp, _vp, _vp, _vp]),
     "tts_geom_bwd_adam_ex": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp, _c_float,

@@ -216,6 +216,79 @@ def geom_fwd_assign_bins(params, camera, H, W, S=16, K=128, span=2048, R=1, near
     return proj, keep, idx, valid, count, ncand
 
 
+SEAM_MAX_G = 131072   # count blocks of 512 gaussians: the seam launch's limit
+
+
+def geom_bwd_adam_fwd_count(params, camera_bwd, camera_fwd, gslot, inv, m, v, lr, step, proj,
+                            keep, H, W, S=16, K=128, span=2048, R=1, workspace=None,
+                            gparams=None, near=NEAR, blur=BLUR, b1=BETA1, b2=BETA2, eps=EPS):
+    """The seam between two training steps, one launch: geom_bwd_adam (camera_bwd) and then
+    the next step's geometry forward (camera_fwd, into proj / keep) with its binning's count
+    pass into workspace -- finish that binning with assign_bins_counted on the same workspace.
+    Equals geom_bwd_adam followed by geom_fwd_assign_bins; plain steps only (no SH, depth weight
+    or MCMC terms) and G <= SEAM_MAX_G."""
+    G = params.shape[0]
+    dev = params.device
+    if not 0 < G <= SEAM_MAX_G:
+        raise ValueError(f"the seam launch takes 0 < G <= {SEAM_MAX_G}, got {G}")
+    for t, n in ((params, "params"), (m, "m"), (v, "v")):
+        require(t, n, F32, (G, 14), dev)
+    require(camera_bwd, "camera_bwd", F32, (16,), dev)
+    require(camera_fwd, "camera_fwd", F32, (16,), dev)
+    require(inv, "inv", I32, (G, 9), dev)
+    if gslot.dim() != 3 or gslot.shape[2] != 9:
+        raise ValueError("gslot must be [T,K,9]")
+    require(gslot, "gslot", F32, tuple(gslot.shape), dev)
+    require(lr, "lr", F32, (14,), dev)
+    require(step, "step", I32, (4,), dev)
+    if gparams is not None:
+        require(gparams, "gparams", F32, (G, 14), dev)
+    _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
+    require(keep, "keep", U8, (G,), dev)
+    if S not in (16, 32) or H % S or W % S:
+        raise ValueError(f"tile side {S} must be 16 or 32 and divide {H}x{W}")
+    workspace = bin_workspace(G, H, W, S, dev) if workspace is None else workspace
+    call("tts_geom_bwd_adam_fwd_count", ptr(params), G, ptr(camera_bwd), ptr(camera_fwd), near,
+         blur, ptr(gslot), ptr(inv), ptr(gparams), ptr(m), ptr(v), ptr(lr), ptr(step), b1, b2,
+         eps, ptr(proj), ptr(keep), H, W, S, R, K, span, ptr(workspace), workspace.numel(),
+         stream())
+    return workspace
+
+
+def assign_bins_counted(proj, keep, H, W, S, K, span, workspace, idx, valid, count, ncand,
+                        inv=None, order=None, slot_rec=None, pos_count=None, advance=None, R=1,
+                        b1=BETA1, b2=BETA2):
+    """The rest of geom_fwd_assign_bins after geom_bwd_adam_fwd_count ran its count pass into
+    workspace (column scan, scatter, select): the same idx, valid, count, ncand, inv, order and
+    slot records.  advance: the Adam step block, advanced by the column scan."""
+    G = proj.shape[0]
+    dev = proj.device
+    if not 0 < G <= SEAM_MAX_G:
+        raise ValueError(f"the seam launch takes 0 < G <= {SEAM_MAX_G}, got {G}")
+    _aligned16(require(proj, "proj", F32, (G, 12), dev), "proj")
+    require(keep, "keep", U8, (G,), dev)
+    T = (H // S) * (W // S)
+    require(idx, "idx", I32, (T, K), dev)
+    require(valid, "valid", U8, (T, K), dev)
+    require(count, "count", I32, (T,), dev)
+    require(ncand, "ncand", I32, (T,), dev)
+    if inv is not None:
+        require(inv, "inv", I32, (G, 9), dev)
+    if order is not None:
+        require(order, "order", I32, (T,), dev)
+    if (slot_rec is None) != (pos_count is None) or (slot_rec is not None and order is None):
+        raise ValueError("slot_rec and pos_count go together, and need order")
+    if slot_rec is not None:
+        _aligned16(require(slot_rec, "slot_rec", F32, (T, K, 12), dev), "slot_rec")
+        require(pos_count, "pos_count", I32, (T,), dev)
+    if advance is not None:
+        require(advance, "advance", I32, (4,), dev)
+    call("tts_assign_bins_counted", ptr(proj), ptr(keep), G, H, W, S, R, K, span, ptr(idx),
+         ptr(valid), ptr(count), ptr(ncand), ptr(inv), ptr(order), ptr(slot_rec), ptr(pos_count),
+         ptr(advance), b1, b2, ptr(workspace), workspace.numel(), stream())
+    return idx, valid, count, ncand
+
+
 # ---------------------------------------------------------------------------------- splat --
 def _bins_check(idx, valid, H, W, S, dev):
     T = (H // S) * (W // S)

@@ -258,6 +258,11 @@ class TrainStep:
             kernels.geom_fwd(self.P, cam, proj=self.proj, keep=self.keep,
                              sh_rest=self.sh, sh_degree=self.sh_degree, depth_bt=self.dw,
                              advance=adv)
+        return self._splat_forward(bgb, rebin, grads)
+
+    def _splat_forward(self, bgb, rebin=True, grads=True):
+        """The fused splat forward on the bins last computed (on the slot records when they were
+        just rebuilt): self.image, and self.den when grads."""
         if self.dtype == "bf16" and rebin and self.use_rec:
             kernels.splat_fwd_mx_rec(self.slot_rec, self.pos_count, self.order, bgb, self.H,
                                      self.W, self.S, self.k, self.image, self.den, bf16=True,
@@ -295,6 +300,10 @@ class TrainStep:
             kernels.composite_random_bg(self.rgba_pm[ci], self.step_block, ci, self.bg_seed,
                                         self.bg, self.target_buf)
         self._forward(ci, advance, rebin)
+        self._loss_and_splat_backward(ci, rebin)
+
+    def _loss_and_splat_backward(self, ci, rebin=True):
+        """Loss gradient of view ci's render, then the fused splat backward (slot gradients)."""
         tgt, stats = self._loss_target(ci)
         kernels.loss_grad_stats(self.image, tgt, stats, self.lam, self.gimage, self.partials)
         if rebin and self.use_rec:
@@ -313,15 +322,7 @@ class TrainStep:
         mc = self.mc
         if self.batch == 1:
             self._view_backward(i, advance=True, rebin=rebin)   # step advance rides on geom_fwd
-            kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
-                                  self.lr, self.step_block, gparams=self.gparams,
-                                  sh_m=self.sh_m, sh_v=self.sh_v,
-                                  lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
-                                  lambda_s=mc["lambda_s"], noise_lr=mc["noise_lr"],
-                                  seed=mc["seed"], depth_bt=self.dw, gdepth=self.gdw, **sh)
-            if self.dw is not None:
-                kernels.depth_weight_adam(self.gdw, self.dw, self.dw_state, self.lr_bt,
-                                          self.step_block, self.dw_ws)
+            self._geometry_backward_adam(i)
             return
         scale = 1.0 / self.batch
         for ci in range(i * self.batch, (i + 1) * self.batch):
@@ -344,6 +345,61 @@ class TrainStep:
             kernels.depth_weight_adam(self.gdw, self.dw, self.dw_state, self.lr_bt,
                                       self.step_block, self.dw_ws)
             kernels.zero_(self.gdw)
+
+    def _geometry_backward_adam(self, i):
+        """Slot gather + geometry backward + Adam of step i (camera i, batch = 1)."""
+        sh = dict(sh_rest=self.sh, sh_degree=self.sh_degree)
+        mc = self.mc
+        kernels.geom_bwd_adam(self.P, self.cams[i], self.gslot, self.inv, self.m, self.v,
+                              self.lr, self.step_block, gparams=self.gparams,
+                              sh_m=self.sh_m, sh_v=self.sh_v,
+                              lr_sh=self.lr_sh, lambda_o=mc["lambda_o"],
+                              lambda_s=mc["lambda_s"], noise_lr=mc["noise_lr"],
+                              seed=mc["seed"], depth_bt=self.dw, gdepth=self.gdw, **sh)
+        if self.dw is not None:
+            kernels.depth_weight_adam(self.gdw, self.dw, self.dw_state, self.lr_bt,
+                                      self.step_block, self.dw_ws)
+
+    @property
+    def seamed(self):
+        """Whether run() joins consecutive steps at the seam: step i's geometry backward + Adam
+        and step i+1's geometry forward + binning count pass in one launch.  The plain step
+        (batch = 1, rebinning every step on 16 x 16 tiles, no SH, depth weight or MCMC) with
+        G <= kernels.SEAM_MAX_G."""
+        mc = self.mc
+        return (self.batch == 1 and self.bin_every == 1 and self.use_rec
+                and self.sh_degree == 0 and self.dw is None
+                and not (mc["lambda_o"] or mc["lambda_s"] or mc["noise_lr"]
+                         or mc["relocate_every"])
+                and 0 < self.P.shape[0] <= kernels.SEAM_MAX_G)
+
+    def enqueue_seamed(self, ci, n):
+        """Enqueue n training steps from camera ci (as n enqueue() calls would run them, with
+        the same results) where each step's backward + Adam and the next step's geometry forward
+        + binning count pass share one launch; the next step's Adam step advance then rides on
+        its binning's column scan.  Requires self.seamed."""
+        if not self.seamed:
+            raise ValueError("this step configuration has no seam launch (see TrainStep.seamed)")
+        ns = self.n_steps
+        self._view_backward(ci % ns, advance=True, rebin=True)
+        for j in range(n - 1):
+            cb, cf = (ci + j) % ns, (ci + j + 1) % ns
+            kernels.geom_bwd_adam_fwd_count(self.P, self.cams[cb], self.cams[cf], self.gslot,
+                                            self.inv, self.m, self.v, self.lr, self.step_block,
+                                            self.proj, self.keep, self.H, self.W, self.S, self.K,
+                                            self.span, workspace=self.bin_ws,
+                                            gparams=self.gparams)
+            if self.random_bg:   # drawn before the step advance, as in enqueue()
+                kernels.composite_random_bg(self.rgba_pm[cf], self.step_block, cf, self.bg_seed,
+                                            self.bg, self.target_buf)
+            kernels.assign_bins_counted(self.proj, self.keep, self.H, self.W, self.S, self.K,
+                                        self.span, self.bin_ws, self.idx, self.valid, self.count,
+                                        self.ncand, inv=self.inv, order=self.order,
+                                        slot_rec=self.slot_rec, pos_count=self.pos_count,
+                                        advance=self.step_block)
+            self._splat_forward(self.bg)
+            self._loss_and_splat_backward(cf)
+        self._geometry_backward_adam((ci + n - 1) % ns)
 
     def enqueue_relocate(self):
         """Enqueue one MCMC relocation (dead slots onto live gaussians, moments reset)."""
@@ -374,6 +430,8 @@ class TrainStep:
                     self.enqueue(ci, rebin)
             if self.mc["relocate_every"]:
                 self.enqueue_relocate()
+            if run_len > 1 and self.seamed:   # the seam launch's first call, outside capture
+                self.enqueue_seamed(0, 2)
         torch.cuda.current_stream(self.dev).wait_stream(side)
         for dst, src in zip(live, state):
             dst.copy_(src)
@@ -398,8 +456,12 @@ class TrainStep:
                 for ph in range(self.bin_every):
                     g = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(g):
-                        for j in range(run_len):
-                            self.enqueue((c + j) % self.n_steps, (ph + j) % self.bin_every == 0)
+                        if self.seamed:
+                            self.enqueue_seamed(c, run_len)
+                        else:
+                            for j in range(run_len):
+                                self.enqueue((c + j) % self.n_steps,
+                                             (ph + j) % self.bin_every == 0)
                     self.run_graphs[(c, ph)] = g
             self.run_len = run_len
         torch.cuda.synchronize(self.dev)
