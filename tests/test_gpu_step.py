@@ -239,7 +239,8 @@ def test_run_graphs_match_single_steps(bin_every):
     cfg, P, _ = config_inputs("c1_ref")
     cams = scenes.Config(**{**cfg.__dict__, "n_cams": 3}).cameras()
     tgts = [target_for(cfg, c) for c in cams]
-    runs = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
+    runs = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every, seam=True)
+    assert runs.seamed == (bin_every == 1)
     runs.capture(run_len=4)
     assert sorted(runs.run_graphs) == [(c, ph) for c in range(3) for ph in range(bin_every)]
     single = TrainStep(P, cams, tgts, K=cfg.K, S=cfg.S, k=cfg.k, bin_every=bin_every)
@@ -450,7 +451,7 @@ def test_seamed_runs_match_single_steps(mode):
     from ttsplat import scenes
     cfg, P, _ = config_inputs("c2" if mode == "bf16" else "c1_ref")
     cams = scenes.Config(**{**cfg.__dict__, "n_cams": 3}).cameras()
-    kw = dict(K=cfg.K, S=cfg.S, k=cfg.k, dtype=cfg.dtype)
+    kw = dict(K=cfg.K, S=cfg.S, k=cfg.k, dtype=cfg.dtype, seam=True)
     if mode == "random_bg":
         tgts = [rgba_target(cfg, c) for c in cams]
         kw.update(random_bg=True, bg_seed=5)
@@ -478,18 +479,26 @@ def test_seamed_runs_match_single_steps(mode):
 
 
 def test_step_configurations_without_a_seam():
-    """SH colour, the depth weight, MCMC terms, bin_every > 1 and batches keep the two
-    launches (TrainStep.seamed is False), and enqueue_seamed refuses them."""
+    """The seam is used by default from G = kernels.SEAM_MIN_G on, with seam=True for any G,
+    never with seam=False; SH colour, the depth weight, MCMC terms, bin_every > 1 and batches
+    keep the two launches whatever seam says, and enqueue_seamed refuses them."""
     from ttsplat import scenes
     cfg, P, cam = config_inputs("c1_ref")
     tgt = target_for(cfg, cam)
-    base = dict(K=cfg.K, S=cfg.S, k=cfg.k)
+    base = dict(K=cfg.K, S=cfg.S, k=cfg.k, seam=True)
     assert TrainStep(P, [cam], [tgt], **base).seamed
+    small = TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k)
+    assert small.seam_possible and not small.seamed          # G = 2000 < SEAM_MIN_G
+    assert not TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, seam=False).seamed
+    cfg_b, P_b, _ = config_inputs("c1_ref", G=kernels.SEAM_MIN_G)
+    assert TrainStep(P_b, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k).seamed
+    with pytest.raises(ValueError):
+        TrainStep(P, [cam], [tgt], K=cfg.K, S=cfg.S, k=cfg.k, seam="yes")
     for kw in (dict(bin_every=2), dict(depth_weight=dict(beta0=1.0, tau0=3.0, lr_bt=0.02)),
                dict(mcmc=dict(lambda_o=0.01)),
                dict(sh_degree=1, sh_rest=torch.zeros(cfg.G, 15, 3))):
         ts = TrainStep(P, [cam], [tgt], **base, **kw)
-        assert not ts.seamed, kw
+        assert not ts.seamed and not ts.seam_possible, kw
         with pytest.raises(ValueError):
             ts.enqueue_seamed(0, 2)
     cams = scenes.Config(**{**cfg.__dict__, "n_cams": 2}).cameras()

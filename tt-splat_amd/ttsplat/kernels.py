@@ -217,6 +217,9 @@ def geom_fwd_assign_bins(params, camera, H, W, S=16, K=128, span=2048, R=1, near
 
 
 SEAM_MAX_G = 131072   # count blocks of 512 gaussians: the seam launch's limit
+# below this the two launches are as fast or faster (train it/s at 1264x832, seam vs two
+# launches: G = 10k +0.1 %, 25k +0.6 %, 50k +1.6 %, 100k +2.8 %; 800x800, G = 10k -1.7 %)
+SEAM_MIN_G = 32768
 
 
 def geom_bwd_adam_fwd_count(params, camera_bwd, camera_fwd, gslot, inv, m, v, lr, step, proj,

@@ -80,7 +80,10 @@ class TrainStep:
     view, computed once (36 bytes per pixel per view: 2.3 GB for 100 views at 800x800; the
     targets must not change after construction); "per_step" keeps one set and recomputes it from
     the current target at every view backward, as the reference's recompute_gt_stats does on each
-    view switch (tools/resident_traced.py:320-325,677-678).  random_bg implies "per_step"."""
+    view switch (tools/resident_traced.py:320-325,677-678).  random_bg implies "per_step".
+    seam: run()'s multi-step graphs join each step's geometry backward + Adam to the next
+    step's geometry forward + binning count pass in one launch (see seamed).  None (default):
+    when that pays, G >= kernels.SEAM_MIN_G; True: whenever the step allows it; False: never."""
 
     MCMC_DEFAULTS = dict(lambda_o=0.0, lambda_s=0.0, noise_lr=0.0, relocate_every=0,
                          dead_thr=0.005, offset=0.005, seed=0)
@@ -90,7 +93,7 @@ class TrainStep:
                  c_b=(1.0, 1.0, 1.0), lambda_ssim=0.2, span=None, device="cuda", batch=1,
                  dtype="fp32", sh_degree=0, sh_rest=None, lr_sh=None, mcmc=None,
                  depth_weight=None, keep_grad=False, bin_every=1, random_bg=False, bg_seed=0,
-                 target_stats="per_view"):
+                 target_stats="per_view", seam=None):
         dev = torch.device(device)
         if dtype not in ("fp32", "bf16"):
             raise ValueError(f"dtype must be 'fp32' or 'bf16', got {dtype!r}")
@@ -153,6 +156,9 @@ class TrainStep:
         self.bg = torch.tensor([float(w_b), *c_b], dtype=F32, device=dev)
         self.bg_white = torch.tensor([float(w_b), 1.0, 1.0, 1.0], dtype=F32, device=dev)
         self.random_bg, self.bg_seed = bool(random_bg), int(bg_seed)
+        if seam not in (None, True, False):
+            raise ValueError(f"seam must be None, True or False, got {seam!r}")
+        self.seam = seam
         if target_stats not in ("per_view", "per_step"):
             raise ValueError(f"target_stats must be 'per_view' or 'per_step', got {target_stats!r}")
         self.stats_mode = "per_step" if self.random_bg else target_stats
@@ -361,11 +367,9 @@ class TrainStep:
                                       self.step_block, self.dw_ws)
 
     @property
-    def seamed(self):
-        """Whether run() joins consecutive steps at the seam: step i's geometry backward + Adam
-        and step i+1's geometry forward + binning count pass in one launch.  The plain step
-        (batch = 1, rebinning every step on 16 x 16 tiles, no SH, depth weight or MCMC) with
-        G <= kernels.SEAM_MAX_G."""
+    def seam_possible(self):
+        """Whether the step has a seam launch: the plain step (batch = 1, rebinning every step
+        on 16 x 16 tiles, no SH, depth weight or MCMC) with 0 < G <= kernels.SEAM_MAX_G."""
         mc = self.mc
         return (self.batch == 1 and self.bin_every == 1 and self.use_rec
                 and self.sh_degree == 0 and self.dw is None
@@ -373,13 +377,24 @@ class TrainStep:
                          or mc["relocate_every"])
                 and 0 < self.P.shape[0] <= kernels.SEAM_MAX_G)
 
+    @property
+    def seamed(self):
+        """Whether run() joins consecutive steps at the seam: step i's geometry backward + Adam
+        and step i+1's geometry forward + binning count pass in one launch (seam_possible, and
+        seam=True or, by default, G >= kernels.SEAM_MIN_G: a seam block carries 512 gaussians
+        through both halves, so with few blocks the two launches' wider spread wins)."""
+        if not self.seam_possible or self.seam is False:
+            return False
+        return self.seam is True or self.P.shape[0] >= kernels.SEAM_MIN_G
+
     def enqueue_seamed(self, ci, n):
         """Enqueue n training steps from camera ci (as n enqueue() calls would run them, with
         the same results) where each step's backward + Adam and the next step's geometry forward
         + binning count pass share one launch; the next step's Adam step advance then rides on
         its binning's column scan.  Requires self.seamed."""
-        if not self.seamed:
-            raise ValueError("this step configuration has no seam launch (see TrainStep.seamed)")
+        if not self.seam_possible:
+            raise ValueError("this step configuration has no seam launch (see "
+                             "TrainStep.seam_possible)")
         ns = self.n_steps
         self._view_backward(ci % ns, advance=True, rebin=True)
         for j in range(n - 1):
