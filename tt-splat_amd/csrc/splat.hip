@@ -6,7 +6,7 @@
 // Forward: the tile's valid slots are compacted into LDS as theta_u (6) and (col_o, o_col) (4);
 // each thread owns S*S/256 pixels and walks the slots:
 //     u = theta . [lx^2, ly^2, lx*ly, lx, ly, 1],  w = max(u,0)^2,  num += w*col, den += w*oc
-// and writes C = (num + w_b c_b) * (1 / (den + w_b)) straight into the [H,W,3] image.  For S = 16
+// and writes C = (num + w_b c_b) * rcp(den + w_b) straight into the [H,W,3] image.  For S = 16
 // from proj or slot records (k_splat_fwd_tile) each wave walks the whole tile for a quarter of
 // the slots instead, u factored per column.
 //
@@ -69,18 +69,20 @@ __device__ __forceinline__ void slot_from_rec(const float4 r0, const float4 r1, 
 __device__ __forceinline__ bool theta_poisons(const float4 ta, const float4 tb) {
   return __builtin_isnan(((ta.x + ta.y) + (ta.z + ta.w)) + (tb.x + tb.y));
 }
-// A slot whose u can be large, infinite or NaN at some pixel: some |theta| >= 1e15, an
-// infinity or a NaN.  Below that, at pixel coordinates under 32 every product, partial sum and
-// u stays under 3.1e18 whatever the order of evaluation (the monomials sum to under 3100), so u
-// is finite, relu_bits is exact, and so is the fast walks' 2 relu(u) = u + |u| with its square
-// 4 w (under FLT_MAX while u < 9.2e18).  A tile with such a slot walks with relu_nan and w
-// itself: where u comes out NaN (inf - inf, in this kernel's order of evaluation -- torch's own
-// order is its BLAS's), the pixel is NaN, as torch.relu keeps it, and -inf gives 0.  (The GPU's
-// generated NaN can carry the sign bit, which relu_bits would map to 0.)
+// A slot whose u can be large, infinite or NaN at some pixel: the sum of its |theta| is 1e15 or
+// more, infinite or NaN (a NaN or an infinity among the six makes the sum NaN or infinite).
+// Below that, at pixel coordinates under 32 every product, partial sum and u stays under 1.1e18
+// whatever the order of evaluation (no monomial exceeds 1024), so u is finite, relu_bits is
+// exact, and so is the fast walks' 2 relu(u) = u + |u| with its square 4 w (under FLT_MAX while
+// u < 9.2e18).  A tile with such a slot walks with relu_nan and w itself: where u comes out NaN
+// (inf - inf, in this kernel's order of evaluation -- torch's own order is its BLAS's), the
+// pixel is NaN, as torch.relu keeps it, and -inf gives 0.  (The GPU's generated NaN can carry
+// the sign bit, which relu_bits would map to 0.)  The sum of absolute values is five full-rate
+// adds; the largest of them, five maxes at half rate and a NaN test besides.
 __device__ __forceinline__ bool theta_wild(const float4 ta, const float4 tb) {
-  const float m = fmaxf(fmaxf(fmaxf(fabsf(ta.x), fabsf(ta.y)), fmaxf(fabsf(ta.z), fabsf(ta.w))),
-                        fmaxf(fabsf(tb.x), fabsf(tb.y)));
-  return !(m < 1e15f) || theta_poisons(ta, tb);
+  const float q = ((fabsf(ta.x) + fabsf(ta.y)) + (fabsf(ta.z) + fabsf(ta.w))) +
+                  (fabsf(tb.x) + fabsf(tb.y));
+  return !(q < 1e15f);
 }
 
 __device__ __forceinline__ void build_slot(const float* __restrict__ proj, int g, float ox,
@@ -247,7 +249,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
     const int p = threadIdx.x + 256 * i;
     const int64_t pix = (int64_t)(oy + p / S) * W + ox + p % S;
     const float d = ad[i] + wb;
-    const float inv = 1.0f / d;   // one division per pixel (each costs ~10 VALU instructions)
+    // one hardware reciprocal per pixel (1 ulp; an IEEE division costs ~10 VALU instructions)
+    const float inv = __builtin_amdgcn_rcpf(d);
     image[pix * 3 + 0] = (ar[i] + cbr) * inv;
     image[pix * 3 + 1] = (ag[i] + cbg) * inv;
     image[pix * 3 + 2] = (ab[i] + cbb) * inv;
@@ -258,10 +261,10 @@ __global__ __launch_bounds__(256) void k_splat_fwd(
 // Contraction of one tile's staged slots over its pixels, then the theta backward and the
 // stores (the main loop of the splat backward).  Every thread of the block must call it (it
 // contains barriers when slots share rows).
-// WILD = false (every slot's |theta| < 1e15, theta_wild): the pixel terms q were staged as q/4
-// and the slot colours are doubled here, so with r2 = u + |u| = 2 relu(u) (one full-rate add
-// instead of a half-rate max) r2^2 q/4 = w q and r2 (q/4)(2 C) = relu(u) q.C exactly (scalings
-// by powers of two).  WILD = true: relu_bits on unscaled q (a NaN u only occurs in tiles whose
+// WILD = false (no slot theta_wild: each sum of |theta| < 1e15): the pixel terms q were staged
+// as q/4 and the slot colours are doubled here, so with r2 = u + |u| = 2 relu(u) (one full-rate
+// add instead of a half-rate max) r2^2 q/4 = w q and r2 (q/4)(2 C) = relu(u) q.C exactly
+// (scalings by powers of two).  WILD = true: relu_bits on unscaled q (a NaN u only occurs in tiles whose
 // den the forward made NaN, so every gradient there is NaN whatever relu gives).
 template <int S, bool FROM_PROJ, bool WILD>
 __device__ __forceinline__ void bwd_contract(int n, const SlotLDS& sl, const float4* s_px,
@@ -874,7 +877,8 @@ __global__ __launch_bounds__(256) void k_splat_fwd_tile(
   const float wb = bg[0];
   const int64_t pix = (int64_t)(oy + 4 * wave + q) * W + ox + j;
   const float d = ad + wb;
-  const float inv = 1.0f / d;     // one division per pixel (each costs ~10 VALU instructions)
+  // one hardware reciprocal per pixel (1 ulp; an IEEE division costs ~10 VALU instructions)
+  const float inv = __builtin_amdgcn_rcpf(d);
   image[pix * 3 + 0] = (ar + wb * bg[1]) * inv;
   image[pix * 3 + 1] = (ag + wb * bg[2]) * inv;
   image[pix * 3 + 2] = (ab + wb * bg[3]) * inv;
