@@ -439,7 +439,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
   float wpart = 0.0f;
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
-    const float inv = 1.0f / pd[i];
+    const float inv = __builtin_amdgcn_rcpf(pd[i]);   // hardware reciprocal, 1 ulp
     const float4 q = make_float4(pg[i][0] * inv, pg[i][1] * inv, pg[i][2] * inv,
                                  -(pg[i][0] * pc[i][0] + pg[i][1] * pc[i][1] + pg[i][2] * pc[i][2]) * inv);
     const int p = threadIdx.x + 256 * i;
