@@ -380,7 +380,8 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
  * (TTS_EG otherwise); no step advance (tts_assign_bins_counted carries step i+1's).  Replaces
  * the reference trainer's adam_fused of one iteration (tools/resident_traced.py:383-427,
  * 739-740) and the geom_fwd + do_bin count of the next (:682-686, geom_fwd :327-346, do_bin
- * :519-539). */
+ * :519-539).  The first call on a device raises the kernel's LDS limit
+ * (hipFuncSetAttribute): make it outside stream capture. */
 int tts_geom_bwd_adam_fwd_count(float* params, int G, const float* camera_bwd,
                                 const float* camera_fwd, float near_z, float blur,
                                 const float* gslot, const int32_t* inv, float* gparams, float* m,

@@ -1143,15 +1143,21 @@ int launch_geom_seam(float* params, int G, const float* cam_b, const float* cam_
   const int nblk = (G + CountFused::kBlock - 1) / CountFused::kBlock;
   const size_t lds = geom_seam_lds(NB, Tpad);
   if (lds > kMaxLdsBytes) return TTS_EINVAL;
-  // the kernel's dynamic-LDS limit, raised once to the most it can ask for (the first call
-  // should not be under graph capture: TrainStep makes one before it captures)
-  static std::atomic<int> lds_ready{0};
-  if (!lds_ready.load()) {
+  // the kernel's dynamic-LDS limit, raised once per device to the most it can ask for (the
+  // first call on a device should not be under graph capture: TrainStep makes one before it
+  // captures)
+  constexpr int kDevices = 64;
+  static std::atomic<int> lds_ready[kDevices] = {};
+  int dev = 0;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return static_cast<int>(de);
+  if (dev < 0 || dev >= kDevices) return TTS_EINVAL;
+  if (!lds_ready[dev].load()) {
     const hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&k_geom_bwd_adam_fwd_count),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxLdsBytes));
     if (e != hipSuccess) return static_cast<int>(e);
-    lds_ready.store(1);
+    lds_ready[dev].store(1);
   }
   k_geom_bwd_adam_fwd_count<<<nblk, 512, lds, stream>>>(
       params, G, cam_b, cam_f, near_z, blur, gslot, inv, gparams, m, v, lr, step, b1, b2, eps,
