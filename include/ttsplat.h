@@ -350,9 +350,10 @@ int tts_geom_fwd_ex(const float* params, const float* sh_rest, int sh_degree,
 /* tts_geom_fwd_ex followed by tts_assign_bins on its output (mu2d = proj, mu_stride 12, keep
  * stride 1), as one call with the results of the two: the geometry trace and the rebin that
  * follows it in the reference trainer (tools/resident_traced.py:682-686, geom_fwd :327-346,
- * do_bin :519-539 on the projected means cache["mu2d_x/y"] and keep).  For
- * G <= 131072 the binning's count pass runs inside the geometry launch, on the means it has
- * just projected (one launch and one read of proj fewer); larger G launch the two as usual.
+ * do_bin :519-539 on the projected means cache["mu2d_x/y"] and keep).  The binning's count
+ * pass runs inside the geometry launch, on the means it has just projected (one launch and one
+ * read of proj fewer), in blocks of 512 gaussians up to G = 131072 and of 4096 above; grids whose
+ * count histogram would not fit the launch's LDS take the two launches.
  * Arguments and errors as the two entry points'.
  * slot_rec [T][K][12] and pos_count [T] (optional, together, and only with order): the slot
  * records of the bins -- the projection record proj[idx[t][s]] of every kept slot s, stored at

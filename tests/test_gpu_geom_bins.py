@@ -1,5 +1,6 @@
-"""tts_geom_fwd_assign_bins (geometry forward + binning as one call; for G <= 131072 the
-binning's count pass runs inside the geometry launch) against tts_geom_fwd_ex followed by
+"""tts_geom_fwd_assign_bins (geometry forward + binning as one call; the binning's count pass
+runs inside the geometry launch, in blocks of 512 gaussians up to G = 131072 and of 4096 above)
+against tts_geom_fwd_ex followed by
 tts_assign_bins on the same inputs: proj, keep, bins, counts and the inverse table equal bit for
 bit; the tile order is a heaviest-first permutation either way (ties in no fixed order).  The
 fused call also writes the slot records: slot_rec[p][s] = proj[idx[order[p]][s]] for every kept
@@ -72,7 +73,8 @@ def check_records(o):
 
 
 @pytest.mark.parametrize("name,G", [("c4", None), ("c3", None), ("c1_ref", None), ("c3", 1),
-                                    ("c3", 257), ("c3", 511), ("c3", 513), ("c4", 150000)])
+                                    ("c3", 257), ("c3", 511), ("c3", 513), ("c4", 131073),
+                                    ("c4", 150000), ("c4", 300017)])
 def test_geom_fwd_assign_bins_equals_two_calls(name, G):
     cfg, P, cam = config_inputs(name, G=G)
     print(f"[geom+bins] {name} G={cfg.G}", flush=True)
@@ -90,8 +92,10 @@ def test_geom_fwd_assign_bins_records_large_k(K):
     check_equal(a, b, cfg.K)
 
 
-def test_geom_fwd_assign_bins_sh_depth_weight_advance():
-    cfg, P, cam = config_inputs("c4", G=60000)
+@pytest.mark.parametrize("G", [60000, 140000])
+def test_geom_fwd_assign_bins_sh_depth_weight_advance(G):
+    cfg, P, cam = config_inputs("c4", G=G)
+    print(f"[geom+bins] c4 SH-3 depth weight G={G}", flush=True)
     gen = torch.Generator().manual_seed(4)
     rest = torch.randn(cfg.G, 15, 3, generator=gen) * 0.1
     bt = torch.tensor([1.5, 4.0], device="cuda")
@@ -101,12 +105,14 @@ def test_geom_fwd_assign_bins_sh_depth_weight_advance():
     assert int(a["adv"][0]) == 1
 
 
-def test_geom_fwd_assign_bins_largest_grid():
+@pytest.mark.parametrize("G", [5000, 140000])
+def test_geom_fwd_assign_bins_largest_grid(G):
     """The largest grid the binning takes, 38912 tiles (4096 x 2432 at S = 16): the fused
-    launch's count histogram is then largest (4608 + 4 * 38912 = 160256 bytes of LDS, within the
-    160 KiB a workgroup has), and the fused call equals the two calls."""
+    launch's count histogram is then largest (4608 + 4 * 38912 = 160256 bytes of LDS with blocks
+    of 512 gaussians, 4 * 38912 = 155648 with blocks of 4096), and the fused call equals the two
+    calls."""
     from ttsplat import scenes
-    cfg = scenes.Config("grid38912", 5000, 2432, 4096, K=128, S=16, k=4.0)
+    cfg = scenes.Config("grid38912", G, 2432, 4096, K=128, S=16, k=4.0)
     P, cam = cfg.params(0), cfg.cameras()[0]
     assert (cfg.H // 16) * (cfg.W // 16) == 38912
     print(f"[geom+bins] {cfg.W}x{cfg.H} G={cfg.G}", flush=True)

@@ -245,6 +245,13 @@ int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degr
                           float blur, float* proj, uint8_t* keep, int32_t* step_adv, float b1,
                           float b2, int ntx, int nty, float S, int span, int NB, int Tpad,
                           int* mat, int2* cell_slot, hipStream_t stream);
+// The same for the large count blocks (CountLarge: 1024 threads, 4096 gaussians per block).
+size_t geom_fwd_count_large_lds(int NB, int Tpad);
+int launch_geom_fwd_count_large(const float* params, const float* sh_rest, int sh_degree,
+                                const float* depth_bt, int G, const float* camera, float near_z,
+                                float blur, float* proj, uint8_t* keep, int32_t* step_adv,
+                                float b1, float b2, int ntx, int nty, float S, int span, int NB,
+                                int Tpad, int* mat, int2* cell_slot, hipStream_t stream);
 // The step seam (geometry.hip): geometry backward + Adam of one view, then the geometry forward
 // of the next view with the count pass, for count blocks of CountSmall.  Its LDS request
 // (geom_seam_lds: the larger of the staged rows and the count pass's histogram) fits whenever

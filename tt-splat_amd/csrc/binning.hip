@@ -1429,14 +1429,23 @@ int tts_geom_fwd_assign_bins(const float* params, const float* sh_rest, int sh_d
     return TTS_EWORKSPACE;
   BinWorkspace ws;
   bin_ws_layout(G, ntx, nty, static_cast<char*>(workspace), &ws);
-  const bool fused = G > 0 && ws.cblock == CountSmall::kBlock &&
-                     geom_fwd_count_lds(ws.NB, ws.Tpad) <= kMaxLdsBytes;
-  const int e = fused ? launch_geom_fwd_count(params, sh_rest, sh_degree, depth_bt, G, camera,
-                                               near_z, blur, proj, keep, step_adv, beta1, beta2,
-                                               ntx, nty, static_cast<float>(S), span, ws.NB,
-                                               ws.Tpad, ws.mat, ws.cell_slot, stream)
-                      : tts_geom_fwd_ex(params, sh_rest, sh_degree, depth_bt, G, camera, near_z,
-                                        blur, proj, keep, step_adv, beta1, beta2, stream);
+  // the count pass inside the geometry launch: blocks of 512 (small) or 4096 (large) gaussians
+  const bool small = ws.cblock == CountSmall::kBlock;
+  const bool fused = G > 0 && (small ? geom_fwd_count_lds(ws.NB, ws.Tpad)
+                                     : geom_fwd_count_large_lds(ws.NB, ws.Tpad)) <= kMaxLdsBytes;
+  const float Sf = static_cast<float>(S);
+  int e;
+  if (fused && small)
+    e = launch_geom_fwd_count(params, sh_rest, sh_degree, depth_bt, G, camera, near_z, blur, proj,
+                              keep, step_adv, beta1, beta2, ntx, nty, Sf, span, ws.NB, ws.Tpad,
+                              ws.mat, ws.cell_slot, stream);
+  else if (fused)
+    e = launch_geom_fwd_count_large(params, sh_rest, sh_degree, depth_bt, G, camera, near_z, blur,
+                                    proj, keep, step_adv, beta1, beta2, ntx, nty, Sf, span, ws.NB,
+                                    ws.Tpad, ws.mat, ws.cell_slot, stream);
+  else
+    e = tts_geom_fwd_ex(params, sh_rest, sh_degree, depth_bt, G, camera, near_z, blur, proj, keep,
+                        step_adv, beta1, beta2, stream);
   if (e != TTS_OK) return e;
   return bin_run(proj, 12, keep, 1, G, H, W, S, K, span, idx, valid, count, ncand, inv, order,
                  proj, slot_rec, pos_count, ws, fused, stream);

@@ -635,6 +635,85 @@ __global__ __launch_bounds__(512) void k_geom_fwd_count(
                      mat, cell_slot);
 }
 
+// The same for the large count blocks (CountLarge: 1024 threads, 4096 gaussians; G above the
+// small blocks' 131072): wave w takes its four rounds of 64 gaussians one after another, each
+// through a wave-private LDS staging area (rows in, then the projection rows out in place), and
+// keeps its means and keep flags in registers for the count pass, which then reuses the LDS.
+// Replaces k_geom_fwd followed by k_bin_count<1024, 4> (one launch and one strided read of
+// proj's means fewer).
+using CountBig = CountLarge;
+template <bool SH>
+__global__ __launch_bounds__(1024) void k_geom_fwd_count_large(
+    const float* __restrict__ params, int G, const float* __restrict__ rest, int n_rest,
+    const float* __restrict__ dw, const float* __restrict__ camera, float near_z, float blur,
+    float* __restrict__ proj, uint8_t* __restrict__ keep, int32_t* adv, float b1, float b2,
+    int ntx, int nty, float S, int span, int NB, int Tpad, int* __restrict__ mat,
+    int2* __restrict__ cell_slot) {
+  constexpr int PER = CountBig::kWaveSpan / 64;
+  static_assert(CountBig::kWaves * 64 == 1024, "one wave per 64 threads");
+  extern __shared__ __attribute__((aligned(16))) float s_dyn[];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float* s_w = s_dyn + wave * 64 * 15;   // this wave's [64][15] rows (then [64][12] out)
+  const int gw = blockIdx.x * CountBig::kBlock + wave * CountBig::kWaveSpan;
+  const Camera cam = load_camera(camera);
+  float mx[PER], my[PER];
+  uint8_t kv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int g0 = gw + 64 * i;
+    const int rows = min(64, G - g0);
+    mx[i] = my[i] = 0.f;
+    kv[i] = 0;
+    if (rows <= 0) continue;  // wave-uniform
+    {  // the rows in: 64 x 14 contiguous floats, lane-strided
+      const float* base = params + (int64_t)g0 * 14;
+      const int last = rows * 14 - 1;
+      float r[14];
+#pragma unroll
+      for (int k = 0; k < 14; ++k) r[k] = base[min(lane + 64 * k, last)];
+#pragma unroll
+      for (int k = 0; k < 14; ++k) {
+        const int e = lane + 64 * k;
+        if (e <= last) s_w[(e / 14) * 15 + e % 14] = r[k];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float orow[12];
+    if (lane < rows)
+      geo_fwd_row<SH>(s_w + lane * 15, g0 + lane, G, rest, n_rest, dw, cam, near_z, blur, orow,
+                      keep, &mx[i], &my[i], &kv[i]);
+    // every lane has read its row: the rows' space takes the projection rows ([64][12])
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < rows) {
+#pragma unroll
+      for (int k = 0; k < 12; ++k) s_w[lane * 12 + k] = orow[k];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    {  // the projection rows out: 64 x 12 contiguous floats
+      float* base = proj + (int64_t)g0 * 12;
+      const int n = rows * 12;
+#pragma unroll
+      for (int k = 0; k < 12; ++k) {
+        const int e = lane + 64 * k;
+        if (e < n) base[e] = s_w[e];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  if (adv && blockIdx.x == 0 && threadIdx.x == 0) advance_step(adv, b1, b2);
+  __syncthreads();  // every staging access is done: the count pass reuses that LDS
+  count_body<1024, PER>(mx, my, kv, G, ntx, nty, S, span, NB, Tpad,
+                        reinterpret_cast<int*>(s_dyn), mat, cell_slot);
+}
+
 // gsh (SH only): dL/drest in the rest layout; rows l >= n_rest are written as zero.
 template <bool SH>
 __global__ __launch_bounds__(256) void k_geom_bwd(const float* __restrict__ params, int G,
@@ -1124,6 +1203,39 @@ int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degr
         step_adv, b1, b2, ntx, nty, S, span, NB, Tpad, mat, cell_slot);
   else
     k_geom_fwd_count<false><<<nblk, 512, lds, stream>>>(
+        params, G, nullptr, 0, depth_bt, camera, near_z, blur, proj, keep, step_adv, b1, b2, ntx,
+        nty, S, span, NB, Tpad, mat, cell_slot);
+  return launch_status();
+}
+
+size_t geom_fwd_count_large_lds(int NB, int Tpad) {
+  const size_t stage = sizeof(float) * CountBig::kWaves * 64 * 15;
+  const size_t cnt = sizeof(int) * ((size_t)Tpad + (size_t)CountBig::kWaves * NB);
+  return stage > cnt ? stage : cnt;
+}
+
+int launch_geom_fwd_count_large(const float* params, const float* sh_rest, int sh_degree,
+                                const float* depth_bt, int G, const float* camera, float near_z,
+                                float blur, float* proj, uint8_t* keep, int32_t* step_adv,
+                                float b1, float b2, int ntx, int nty, float S, int span, int NB,
+                                int Tpad, int* mat, int2* cell_slot, hipStream_t stream) {
+  const int nblk = (G + CountBig::kBlock - 1) / CountBig::kBlock;
+  const size_t lds = geom_fwd_count_large_lds(NB, Tpad);
+  if (lds > kMaxLdsBytes) return TTS_EINVAL;  // callers check first and take the two-kernel path
+  const bool sh = sh_degree > 0;
+  const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count_large<true>)
+                      : reinterpret_cast<const void*>(&k_geom_fwd_count_large<false>);
+  if (lds > 65536) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(lds));
+    if (e != hipSuccess) return static_cast<int>(e);
+  }
+  if (sh)
+    k_geom_fwd_count_large<true><<<nblk, 1024, lds, stream>>>(
+        params, G, sh_rest, sh_rest_count(sh_degree), depth_bt, camera, near_z, blur, proj, keep,
+        step_adv, b1, b2, ntx, nty, S, span, NB, Tpad, mat, cell_slot);
+  else
+    k_geom_fwd_count_large<false><<<nblk, 1024, lds, stream>>>(
         params, G, nullptr, 0, depth_bt, camera, near_z, blur, proj, keep, step_adv, b1, b2, ntx,
         nty, S, span, NB, Tpad, mat, cell_slot);
   return launch_status();
