@@ -658,19 +658,34 @@ __global__ __launch_bounds__(1024) void k_geom_fwd_count_large(
   const Camera cam = load_camera(camera);
   float mx[PER], my[PER];
   uint8_t kv[PER];
+  // a round's rows (64 x 14 contiguous floats, lane-strided); without SH (whose rest
+  // coefficients leave no registers for it) round i + 1's are requested before round i is
+  // projected, so they arrive during it
+  float nr[14];
+  auto load_round = [&](int i) {
+    const int g0 = gw + 64 * i;
+    const int rows = min(64, G - g0);
+    if (rows <= 0) return;  // wave-uniform
+    const float* base = params + (int64_t)g0 * 14;
+    const int last = rows * 14 - 1;
+#pragma unroll
+    for (int k = 0; k < 14; ++k) nr[k] = base[min(lane + 64 * k, last)];
+  };
+  if constexpr (!SH) load_round(0);
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int g0 = gw + 64 * i;
     const int rows = min(64, G - g0);
     mx[i] = my[i] = 0.f;
     kv[i] = 0;
-    if (rows <= 0) continue;  // wave-uniform
-    {  // the rows in: 64 x 14 contiguous floats, lane-strided
-      const float* base = params + (int64_t)g0 * 14;
-      const int last = rows * 14 - 1;
+    if (rows <= 0) continue;  // wave-uniform (and so are the later rounds)
+    {
+      if constexpr (SH) load_round(i);
       float r[14];
 #pragma unroll
-      for (int k = 0; k < 14; ++k) r[k] = base[min(lane + 64 * k, last)];
+      for (int k = 0; k < 14; ++k) r[k] = nr[k];
+      if (!SH && i + 1 < PER) load_round(i + 1);
+      const int last = rows * 14 - 1;
 #pragma unroll
       for (int k = 0; k < 14; ++k) {
         const int e = lane + 64 * k;
