@@ -1,5 +1,8 @@
-"""Host-side logic (CPU): seeded workloads, camera blocks, model layout, tile maps."""
+"""Host-side logic (CPU): seeded workloads, camera blocks, model layout, tile maps, the bench's
+one-GPU contract."""
 import math
+import os
+import sys
 
 import torch
 
@@ -87,3 +90,16 @@ def test_tensor_helpers_refuse_cpu_tensors():
         forward.phi(x, x)
     with pytest.raises(ValueError):
         geometry.quat_to_rotmat(torch.zeros(2, 4))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus above 1 (or a multi-rank launch) exits with status 2
+    and says so, before touching a device."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for extra, env in ((["--gpus", "2"], {}), ([], {"WORLD_SIZE": "2"})):
+        r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), *extra],
+                           capture_output=True, text=True, timeout=120,
+                           env={**os.environ, **env})
+        assert r.returncode == 2, r.stderr
+        assert "exactly one GPU" in r.stderr
