@@ -15,7 +15,11 @@ Conversions (the device's):
   normal pair from (x0, x1): r = sqrt(-2 ln u0), (r cos 2 pi u1, r sin 2 pi u1)   (Box-Muller)
 
 Pinned by tests/test_oracle_mcmc.py: the Philox4x32-10 known-answer vectors of the Random123
-distribution and the moments of the derived normals.
+distribution, the uniform grid's symmetry about 1/2 and its ends, and the moments of the derived
+normals.  The counter word layout (index, step, tag, 0) and the Box-Muller output order are
+this library's own conventions, not the reference's (it draws from torch's host generator): no
+CPU fact fixes them, and the device parity tests (tests/test_gpu_mcmc.py) hold the device to
+this file on them.
 """
 import numpy as np
 

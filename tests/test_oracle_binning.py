@@ -9,6 +9,7 @@
   * structural invariants.
 """
 import hashlib
+import math
 import os
 
 import numpy as np
@@ -94,6 +95,30 @@ def test_stable_equals_bruteforce(S, K, seed):
     a = obin.assign_bins(mu, keep, tmap, 1, K, span=span, stable=True)
     b = obin.assign_bins_bruteforce(mu, keep, tmap, 1, K, span=span)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_candidate_pairs_stencil_order():
+    """The pair list is stencil-major (j = (dy+R)(2R+1) + dx+R ascending, dy outer, dx inner),
+    gaussians ascending within one j, each pair's tile = cell + (dx, dy) inside the grid
+    (tools/m4_train_binned.py:90-98), at R = 1 and R = 2."""
+    g = torch.Generator().manual_seed(5)
+    S, H, W, G = 16, 80, 112, 70
+    mu = torch.rand(G, 2, generator=g) * torch.tensor([W + 30.0, H + 30.0]) - 15
+    keep = torch.rand(G, generator=g) > 0.2
+    tmap = obin.TileMap(H, W, S)
+    for R in (1, 2):
+        tiles, gs, js = obin.candidate_pairs(mu, keep, tmap, R)
+        want = []
+        for j in range((2 * R + 1) ** 2):
+            dy, dx = j // (2 * R + 1) - R, j % (2 * R + 1) - R
+            for gi in range(G):
+                cx = min(max(int(math.floor(float(mu[gi, 0]) / S)), 0), tmap.ntx - 1)
+                cy = min(max(int(math.floor(float(mu[gi, 1]) / S)), 0), tmap.nty - 1)
+                tx, ty = cx + dx, cy + dy
+                if bool(keep[gi]) and 0 <= tx < tmap.ntx and 0 <= ty < tmap.nty:
+                    want.append((ty * tmap.ntx + tx, gi, j))
+        got = list(zip(tiles.tolist(), gs.tolist(), js.tolist()))
+        assert got == want
 
 
 def test_invariants(golden):

@@ -7,11 +7,16 @@
   offset leaves the render nearly unchanged, SGLD noise is gated to near-dead gaussians;
 * the regularisation gradient in closed form (d/dop = lambda_o/G o(1-o),
   d/dlog_s = lambda_s/(3G) s);
-* the inverse-CDF target pick: empirical frequencies proportional to opacity.
+* the inverse-CDF target pick: empirical frequencies proportional to opacity, and exact picks
+  at prefix-sum boundaries;
+* hand-worked cases: the near-dead gate's midpoint and width, the SGLD noise covariance of a
+  rotated anisotropic gaussian, the strict dead threshold, a relocation's split, clamp and
+  copies, and the uniform grid's symmetry about 1/2.
 """
 import math
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import geometry, mcmc, rng, splat
@@ -166,3 +171,86 @@ def test_rgba_premult_composites_over_a_background():
     out = pm[..., :3] + pm[..., 3:4] * bg
     assert torch.allclose(out, rgb * alpha + (1 - alpha) * bg, atol=1e-6)
     assert torch.equal(out[0, 0], rgb[0, 0]) and torch.allclose(out[0, 1], bg)
+
+
+def test_near_dead_gate_midpoint_and_width():
+    """op_sigmoid(1 - o) is 1/2 at opacity 0.005 (spike/mcmc.py:13-15: gate ~1 only for
+    opacity below ~0.005) and rises from 0.1 to 0.9 over 2 ln 9 / 100 of opacity."""
+    assert float(mcmc.op_sigmoid(torch.tensor(1.0 - 0.005, dtype=D))) == pytest.approx(0.5, abs=1e-12)
+    lo = 0.995 - math.log(9.0) / 100.0
+    hi = 0.995 + math.log(9.0) / 100.0
+    assert float(mcmc.op_sigmoid(torch.tensor(lo, dtype=D))) == pytest.approx(0.1, abs=1e-12)
+    assert float(mcmc.op_sigmoid(torch.tensor(hi, dtype=D))) == pytest.approx(0.9, abs=1e-12)
+
+
+def test_sgld_noise_has_the_gaussian_covariance():
+    """For the unit draws e_x, e_y, e_z the noise columns form w L with L L^T = Sigma, the
+    gaussian's own covariance R diag(s^2) R^T (oracle/geometry.py cov3d): an anisotropic,
+    rotated gaussian tells L = R diag(s) from diag(s) R."""
+    P = _scene(1, 9).repeat(3, 1)
+    P[:, 3:7] = torch.tensor([math.cos(0.6), 0.3, -0.5, math.sin(0.6)], dtype=D)
+    P[:, 7:10] = torch.log(torch.tensor([0.05, 0.2, 0.7], dtype=D))
+    P[:, 13] = _logit(1e-4)
+    lr, nlr = 5e-3, 100.0
+    N = mcmc.sgld_noise(P, lr, nlr, torch.eye(3, dtype=D)).T          # columns = w L e_j
+    o = torch.sigmoid(P[0, 13])
+    w = float(torch.sigmoid(100.0 * ((1.0 - o) - 0.995))) * nlr * lr
+    R = geometry.quat_to_rotmat(P[:1, 3:7])[0]
+    sigma = geometry.cov3d(torch.exp(P[:1, 7:10]), R[None])[0]
+    assert torch.allclose(N @ N.T, w * w * sigma, rtol=1e-12, atol=0.0)
+    assert not torch.allclose(N @ N.T, w * w * torch.diag(torch.exp(2 * P[0, 7:10])), rtol=1e-3)
+
+
+def test_classify_threshold_is_strict():
+    """dead = o < thr, alive = o >= thr (spike/mcmc.py:45-46): an opacity equal to the
+    threshold is alive."""
+    P = _scene(3, 4)
+    P[:, 13] = torch.tensor([0.0, -0.1, 0.1], dtype=D)      # o = 1/2 exactly, below, above
+    _, dead, alive = mcmc.classify(P, 0.5)
+    assert dead.tolist() == [1] and alive.tolist() == [0, 2]
+
+
+def test_pick_targets_boundaries():
+    """The first live j whose inclusive prefix sum exceeds u * total: u * total on a prefix
+    boundary goes to the next gaussian, u = 0 to the first, u -> 1 to the last."""
+    o = torch.tensor([0.25, 0.0, 0.25, 0.5], dtype=D)
+    alive = torch.tensor([0, 2, 3])
+    u = torch.tensor([0.0, 0.2499, 0.25, 0.4999, 0.5, 0.75, 0.999999], dtype=D)
+    assert mcmc.pick_targets(o, alive, u).tolist() == [0, 0, 2, 2, 3, 3, 3]
+
+
+def test_relocate_split_clamp_and_copies():
+    """Hand-worked relocation: a target at o = 0.006 with three copies splits to 0.0015 each
+    (o_t / (n_t + 1), spike/mcmc.py:51-54); one at 1.5e-6 with one copy clamps to 1e-6; a copy
+    takes the target's row with means + offset (spike/mcmc.py:57-65)."""
+    P = _scene(7, 6)
+    P[:, 13] = torch.tensor([_logit(0.006), _logit(1e-5), _logit(1e-5), _logit(1e-5),
+                             _logit(1.5e-6), _logit(1e-5), _logit(0.8)], dtype=D)
+    old = P.clone()
+    dead = torch.tensor([1, 2, 3, 5])
+    targets = torch.tensor([0, 0, 0, 4])
+    offsets = torch.tensor([[0.1, 0.0, 0.0], [0.0, -0.2, 0.0], [0.0, 0.0, 0.3],
+                            [0.01, 0.02, 0.03]], dtype=D)
+    m, v = torch.ones_like(P), torch.ones_like(P)
+    touched = mcmc.relocate(P, m, v, dead, targets, offsets)
+    o_new = torch.sigmoid(P[:, 13])
+    for i in (0, 1, 2, 3):
+        assert float(o_new[i]) == pytest.approx(0.0015, rel=1e-12)
+    for i in (4, 5):
+        assert float(o_new[i]) == pytest.approx(1e-6, rel=1e-9)
+    assert float(o_new[6]) == pytest.approx(0.8, rel=1e-12)
+    for d, t, off in zip(dead.tolist(), targets.tolist(), offsets):
+        assert torch.equal(P[d, 0:3], old[t, 0:3] + off)
+        assert torch.equal(P[d, 3:13], old[t, 3:13])
+    assert touched.tolist() == [0, 1, 2, 3, 4, 5]
+
+
+def test_uniform_conversion_is_centred():
+    """uniform(x) = ((x >> 8) + 1/2) 2^-24: the 2^24 cell midpoints, symmetric about 1/2
+    (uniform(x) + uniform(~x) = 1 exactly), from 2^-25 to 1 - 2^-25."""
+    x = np.concatenate([np.array([0, 255, 256, 0xFFFFFFFF], dtype=np.uint64),
+                        rng.draws(np.arange(1000), 1, 2, 3).reshape(-1)])
+    u = rng.uniform(x)
+    assert np.array_equal(u + rng.uniform(x ^ np.uint64(0xFFFFFFFF)), np.ones_like(u))
+    assert u[0] == 2.0 ** -25 and u[1] == 2.0 ** -25 and u[2] == 3 * 2.0 ** -25
+    assert u[3] == 1.0 - 2.0 ** -25

@@ -16,8 +16,10 @@ import math
 import pytest
 import torch
 
+from oracle import adam as oadam
 from oracle import geometry as ogeo
 from oracle import loss as oloss
+from oracle import splat as osplat
 
 DT = torch.float64
 
@@ -218,3 +220,59 @@ def test_depth_weight_gradients_closed_form(beta, tau):
     gpre = c * o * rho * (1 - rho)
     assert abs(float(bt.grad[0]) - float((gpre * (tau - z)).sum())) < 1e-13
     assert abs(float(bt.grad[1]) - float((gpre * beta).sum())) < 1e-13
+
+
+def test_depth_weight_is_a_constant_of_the_geometry_gradient():
+    """The device step holds z constant in rho = sigmoid(beta (tau - z))
+    (tools/resident_traced.py:333-337): the render and the gradient of every column but the
+    opacity equal those of the same scene without a depth weight whose opacity already carries
+    rho (sigmoid(op') = sigmoid(op) rho).  A rho that let the gradient reach z would add a
+    term to the means gradient."""
+    from oracle import binning as obin
+    from oracle import pipeline as opipe
+    P, cam = _dw_scene()
+    P[:, 7:10] = -2.2
+    tmap = obin.TileMap(64, 64, 16)
+    gen = torch.Generator().manual_seed(33)
+    tgt = torch.rand(64, 64, 3, generator=gen, dtype=DT)
+    beta, tau = 3.0, 3.0
+    z = ogeo.project_params(P, cam)["depth"]
+    rho = torch.sigmoid(beta * (tau - z))
+    assert float(rho.min()) > 0.05 and float(rho.max()) < 0.95
+    P2 = P.clone()
+    o2 = torch.sigmoid(P[:, 13]) * rho
+    P2[:, 13] = torch.log(o2 / (1 - o2))
+    img1, L1, g1, _ = opipe.render_and_grad(P, cam, tmap, tgt, depth_bt=(beta, tau))
+    img2, L2, g2, _ = opipe.render_and_grad(P2, cam, tmap, tgt)
+    assert torch.allclose(img1, img2, rtol=0, atol=1e-13)
+    assert float(g1[:, 0:3].abs().max()) > 1e-6
+    assert torch.allclose(g1[:, :13], g2[:, :13], rtol=1e-9, atol=1e-15)
+
+
+def test_empty_slots_carry_zero_operands():
+    """An empty slot (valid = 0, index 0) carries theta = 0, colour 0 and opacity 0
+    (tools/m4_train_binned.py:207-211 mask all three by valid)."""
+    from oracle import binning as obin
+    P, cam = _dw_scene()
+    tmap = obin.TileMap(64, 64, 16)
+    theta, col, oc, _, (idx, valid) = osplat.operands(P, cam, tmap, K=16)
+    assert bool((~valid).any()) and bool(valid.any())
+    assert float(theta.permute(0, 2, 1)[~valid].abs().max()) == 0.0
+    assert float(col[~valid].abs().max()) == 0.0 and float(oc[~valid].abs().max()) == 0.0
+    assert float(theta.permute(0, 2, 1)[valid].abs().max()) > 0.0
+
+
+def test_train_step_number_is_one_based():
+    """train_step(..., t) applies Adam step t counting from 1: the first call (t = 1) moves P by
+    exactly what torch.optim.Adam's first step does with the same gradient."""
+    from oracle import binning as obin
+    from oracle import pipeline as opipe
+    P, cam = _dw_scene()
+    tmap = obin.TileMap(64, 64, 16)
+    tgt = torch.rand(64, 64, 3, generator=torch.Generator().manual_seed(34), dtype=DT)
+    lr = torch.full((14,), 1e-3, dtype=DT)
+    _, _, g, _ = opipe.render_and_grad(P, cam, tmap, tgt)
+    ref = oadam.torch_adam_reference(P, [g], lr)
+    Pt, m, v = P.clone(), torch.zeros_like(P), torch.zeros_like(P)
+    opipe.train_step(Pt, m, v, 1, cam, tmap, tgt, lr)
+    assert torch.allclose(Pt - P, ref - P, rtol=1e-9, atol=1e-18)
