@@ -10,6 +10,12 @@ chosen so that a plausible mistake fails it:
       entries J02 = -fx x/z^2, J12 = -fy y/z^2 fails;
   depth weight (spike/arms.py:34-37): a flipped sign of beta (tau - z), and gradients other than
       the closed forms of tools/m8_depthweight_oracle.py:7-12, fail.
+  camera and cull (spike/camera.py:51-63, spike/geometry.py:39-40, spike/synthetic.py:21): a
+      frame turned 180 degrees, a non-strict near cull, another z clamp for culled gaussians, a
+      vertical field of view and an ungated dense weight fail;
+  operands and step: theta left unmasked in empty slots, a depth weight whose gradient reaches
+      z, and an Adam step number off by one fail;
+  loss: SSIM on the unclamped target fails.
 """
 import math
 
@@ -22,6 +28,10 @@ from oracle import loss as oloss
 from oracle import splat as osplat
 
 DT = torch.float64
+
+
+def _f(x):
+    return torch.tensor(x, dtype=DT)
 
 # The 11-tap gaussian window of sigma 1.5, normalised (taps 0..5; the window is symmetric):
 # exp(-c^2 / 4.5) / sum over c = -5..5.
@@ -276,3 +286,75 @@ def test_train_step_number_is_one_based():
     Pt, m, v = P.clone(), torch.zeros_like(P), torch.zeros_like(P)
     opipe.train_step(Pt, m, v, 1, cam, tmap, tgt, lr)
     assert torch.allclose(Pt - P, ref - P, rtol=1e-9, atol=1e-18)
+
+
+# ------------------------------------------------------------- camera, cull, loss clamps
+def test_look_at_frame_orientation():
+    """look_at_opencv (spike/camera.py:51-63): z toward the target, x = normalise(up x z), and
+    y = z x x, which by the triple product is the part of `up` orthogonal to z (normalised); the
+    target lands on the principal point at depth |target - eye|."""
+    for eye, target in (((0.3, 0.9, 2.7), (0.1, -0.2, 0.05)), ((-2.0, 0.4, -1.1), (0.0, 0.0, 0.0))):
+        R_v, t_v = ogeo.look_at_opencv(eye, target, dtype=DT)
+        e, t, up = _f(eye), _f(target), _f([0.0, 1.0, 0.0])
+        z = (t - e) / (t - e).norm()
+        y = up - z * (z @ up)
+        y = y / y.norm()
+        assert torch.allclose(R_v[2], z, atol=1e-14)
+        assert torch.allclose(R_v[1], y, atol=1e-14)
+        assert torch.allclose(R_v[0], torch.linalg.cross(y, z), atol=1e-14)
+        assert abs(float(torch.det(R_v)) - 1.0) < 1e-13
+        cam_t = R_v @ t + t_v
+        assert torch.allclose(cam_t, torch.stack([_f(0.0), _f(0.0), (t - e).norm()]), atol=1e-14)
+
+
+def test_horizontal_field_of_view():
+    """make_camera's fov is horizontal (fx = fy = W / (2 tan(fov/2)), spike/synthetic.py:21):
+    on a 32 x 96 image a point fov/2 off the axis horizontally lands on the right edge x = W,
+    one fov/2 off vertically lands W/2 below the centre, not H/2."""
+    H, W, fov = 32, 96, 60.0
+    cam = ogeo.make_camera(H, W, (0.4, 0.3, 3.0), fov_deg=fov)
+    R_v, t_v = cam["R_v"].to(DT), cam["t_v"].to(DT)
+    tan = math.tan(math.radians(fov) / 2.0)
+    pts_cam = _f([[2.0 * tan, 0.0, 2.0], [0.0, 2.0 * tan, 2.0]])
+    world = (pts_cam - t_v) @ R_v                         # R_v^T (p - t_v), row-wise
+    cov = torch.eye(3, dtype=DT).expand(2, 3, 3) * 1e-4
+    mu2d, _, _, _ = ogeo.project_ewa(world, cov, R_v, t_v, cam["fx"], cam["fy"], cam["cx"],
+                                     cam["cy"])
+    assert torch.allclose(mu2d[0], _f([W, H / 2.0]), atol=1e-9)
+    assert torch.allclose(mu2d[1], _f([W / 2.0, H / 2.0 + W / 2.0]), atol=1e-9)
+
+
+def test_near_cull_is_strict_and_clamps_z():
+    """keep = depth > near (spike/geometry.py:39): a gaussian exactly at the near plane is
+    culled; a culled gaussian is projected with z clamped to near (:40), so it stays finite."""
+    R_v = _f([[-1.0, 0.0, 0.0], [0.0, 1.0, 0.0], [0.0, 0.0, -1.0]])   # eye (0, 0, 2) -> origin
+    t_v = _f([0.0, 0.0, 2.0])
+    means = _f([[0.0, 0.0, 1.75], [0.0, 0.0, 1.7], [-0.5, -0.25, 3.0]])  # depth 0.25, 0.3, -1
+    cov = torch.eye(3, dtype=DT).expand(3, 3, 3) * 0.01
+    fx, fy, cx, cy = 100.0, 90.0, 32.0, 24.0
+    mu2d, conic, depth, keep = ogeo.project_ewa(means, cov, R_v, t_v, fx, fy, cx, cy, 0.3, 0.25)
+    assert float(depth[0]) == 0.25 and keep.tolist() == [False, True, False]
+    assert torch.allclose(mu2d[2], _f([fx * 0.5 / 0.25 + cx, fy * -0.25 / 0.25 + cy]),
+                          atol=1e-12)
+    assert bool(torch.isfinite(conic).all())
+
+
+def test_ssim_clamps_both_images():
+    """SSIM sees clamp(pred, 0, 1) and clamp(gt, 0, 1) (spike/metrics.py:7), the L1 term the raw
+    values: pred = 1, gt = 3 everywhere give SSIM 1 and loss (1 - lambda) * 2."""
+    pred = torch.ones(16, 16, 3, dtype=DT)
+    gt = torch.full((16, 16, 3), 3.0, dtype=DT)
+    for a, b in ((pred, gt), (gt, pred)):
+        L = float(oloss.loss_fn(a, b, 0.2))
+        assert abs(L - 0.8 * 2.0) < 1e-14
+
+
+def test_dense_render_ignores_culled_gaussians():
+    """The poly-splat weight is gated by keep (spike/forward.py:61-66): a gaussian behind the
+    camera, which the z clamp projects onto the image centre, changes nothing."""
+    P, cam = _dw_scene()
+    base = osplat.render_dense(P, cam)
+    extra = torch.cat([P, P[:1].clone()])
+    extra[-1, 0:3] = _f([0.0, 0.0, 4.0])                  # 1 behind the eye at (0, 0, 3)
+    extra[-1, 13] = 3.0
+    assert torch.allclose(osplat.render_dense(extra, cam), base, rtol=0, atol=1e-15)
