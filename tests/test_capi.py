@@ -111,3 +111,31 @@ def test_wrappers_refuse_cpu_tensors():
     from ttsplat import kernels
     with pytest.raises(ValueError):
         kernels.geom_fwd(torch.zeros(4, 14), torch.zeros(16))
+
+
+def _null_args(argtypes, ival):
+    args = []
+    for a in argtypes:
+        if a is ctypes.c_float:
+            args.append(1.0)
+        elif a in (ctypes.c_void_p, ctypes.c_char_p) or issubclass(a, ctypes._Pointer):
+            args.append(None)
+        else:
+            args.append(ival)
+    return args
+
+
+def test_every_compute_entry_point_rejects_null_pointers(lib):
+    """Every entry point that takes device buffers, called with all of them NULL, returns a
+    negative domain code (TTS_EINVAL, or TTS_ETILE where the tile geometry is checked first)
+    before launching anything; the host-only size queries answer without touching memory."""
+    from ttsplat._lib import SIGNATURES
+    host_only = {"tts_version", "tts_strerror"}
+    for name, (res, argtypes) in SIGNATURES.items():
+        if name in host_only or res is not ctypes.c_int:
+            continue
+        if not any(a is ctypes.c_void_p for a in argtypes):
+            continue
+        for ival in (16, 1):
+            rc = getattr(lib, name)(*_null_args(argtypes, ival))
+            assert rc in (-1, -2), (name, ival, rc)
