@@ -46,6 +46,44 @@ def test_dense_arm_forward_and_grads(arm, G):
         assert float(model.w_b_raw.grad) == 0.0            # revealage has no w_b
 
 
+def test_revealage_clamps_near_opaque_splats():
+    """Revealage clamps each alpha o w_geo at 1 - 1e-4 before log1p (spike/arms.py:71-83): with
+    near-opaque, wide splats many pixels have o w_geo above 0.99, where the clamp decides the
+    transmittance; image and gradients still follow the oracle."""
+    import math
+    from oracle import geometry as ogeo
+    cfg, P, cam = config_inputs("c1_ref", G=300)
+    P = P.clone()
+    # twice as wide, still anisotropic (an isotropic covariance leaves the rotation without a
+    # gradient); opacity 0.9995, where fp32 still resolves 1 - o to 1e-4 for the opacity gradient
+    P[:, 7:10] += math.log(2.0)
+    P[:, 13] = math.log(0.9995 / 0.0005)
+    camd = cam_dict(cam)
+    pr = ogeo.project_params(P.double(), camd)
+    px, py = ogeo.pixel_grid(cam.H, cam.W, dtype=torch.float64)
+    wg = osplat.poly_splat_wgeo(osplat.quad_form(px, py, pr["mu2d"], pr["conic"]), 4.0,
+                                pr["keep"])
+    alpha = torch.sigmoid(P[:, 13].double())[None, :] * wg
+    n_hi = int((alpha > 0.99).any(dim=1).sum())
+    print(f"[RV-opaque] pixels with an alpha above 0.99: {n_hi}", flush=True)
+    assert n_hi >= 50
+    model = GaussianModel(P.cuda())
+    model.params.requires_grad_(True)
+    img = trender.render(model, cam, "RV")
+    R = torch.randn(cam.H, cam.W, 3, generator=torch.Generator().manual_seed(9))
+    (img * R.cuda()).sum().backward()
+    Pr = P.double().clone().requires_grad_(True)
+    ref = osplat.render_dense(Pr, camd, arm="RV")
+    err = max_abs(img, ref)
+    print(f"[RV-opaque] max|err| {err:.2e}", flush=True)
+    assert err <= 1e-4
+    (ref * R.double()).sum().backward()
+    for sl in (slice(0, 3), slice(3, 7), slice(7, 10), slice(10, 13), slice(13, 14)):
+        e = rel_l2(model.params.grad[:, sl], Pr.grad[:, sl])
+        print(f"[RV-opaque] grad {sl}: {e:.2e}", flush=True)
+        assert e <= 1e-3, sl
+
+
 @pytest.mark.parametrize("arm", ["SZ", "RV"])
 def test_fit_trains_the_arm(arm):
     from ttsplat import scenes

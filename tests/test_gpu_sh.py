@@ -37,6 +37,42 @@ def test_geom_fwd_sh(name, deg):
     assert max_abs(dc["color_o"], ref["color_o"]) > 1e-2
 
 
+@pytest.mark.parametrize("deg", [1, 2, 3])
+def test_sh_view_direction_gradient_alone(deg):
+    """The SH colour's gradient through its view direction (spike/render.py:23-25: the dense
+    render's direction means - centre is not detached), alone: with an upstream gradient on the
+    colour only, the means receive nothing but that term, so the geometry backward with
+    TTS_GRAD_SH_DIR must equal autograd of sum(gcol_o keo colour(means - centre)) through the
+    direction, and without the flag give zero (the device step's detached direction)."""
+    from oracle import sh as osh
+    cfg, P, cam = config_inputs("c1_ref")
+    rest = rest_for(cfg.G)
+    G = cfg.G
+    gen = torch.Generator().manual_seed(40 + deg)
+    grad9 = torch.zeros(G, 9)
+    grad9[:, 5:8] = torch.randn(G, 3, generator=gen)
+    print(f"[sh-dir] degree {deg} G={G}", flush=True)
+    Pc, camb, g9 = P.cuda(), cam.device_block("cuda"), grad9.cuda()
+    rl = kernels.sh_rest_layout(rest.cuda())
+    on = kernels.geom_bwd(Pc, camb, g9, sh_rest=rl, sh_degree=deg, sh_dirgrad=True)[0].cpu()
+    off = kernels.geom_bwd(Pc, camb, g9, sh_rest=rl, sh_degree=deg, sh_dirgrad=False)[0].cpu()
+    camd = cam_dict(cam)
+    Pd = P.double()
+    keo = ogeo.project_params(Pd, camd)["o_col"]
+    means = Pd[:, 0:3].clone().requires_grad_(True)
+    centre = osh.camera_center(camd["R_v"].double(), camd["t_v"].double())
+    coeffs = torch.cat([Pd[:, 10:13][:, None, :], rest.double()], dim=1)
+    colour = osh.eval_sh_color(deg, coeffs, means - centre[None, :])
+    (grad9[:, 5:8].double() * keo[:, None] * colour).sum().backward()
+    ref = means.grad
+    assert float(ref.norm()) > 1e-3
+    assert float(off[:, 0:3].abs().max()) == 0.0
+    e = rel_l2(on[:, 0:3], ref)
+    print(f"[sh-dir] degree {deg}: rel L2 {e:.2e}", flush=True)
+    assert e <= 1e-4
+    assert torch.equal(on[:, 3:], off[:, 3:])
+
+
 def _lib_keep(Pc, camb):
     return kernels.geom_fwd(Pc, camb)[1]
 

@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 
 GROUPS = {"means": slice(0, 3), "quats": slice(3, 7), "scales": slice(7, 10),
           "color": slice(10, 13), "opacity": slice(13, 14)}
+CB = (0.2, 0.5, 0.9)   # a background colour whose three channels differ
 
 
 def setup(name, G=None, k=None):
@@ -108,11 +109,16 @@ def test_theta_gather_matches_operands():
     assert rel_l2(th, rth) <= 1e-5
 
 
-@pytest.mark.parametrize("name,k", [("c1_ref", 4.0), ("c1", 9.0), ("c3", 4.0)])
-def test_splat_bwd_param_grads(name, k):
-    """d(sum R*img)/dparams, GPU fused backward + geometry backward vs oracle autograd."""
+@pytest.mark.parametrize("name,k,cb", [("c1_ref", 4.0, None), ("c1", 9.0, None), ("c3", 4.0, None),
+                                       ("c1_ref", 4.0, CB)])
+def test_splat_bwd_param_grads(name, k, cb):
+    """d(sum R*img)/dparams, GPU fused backward + geometry backward vs oracle autograd (cb: a
+    background colour with three different channels)."""
     cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup(name, k=k)
-    print(f"[bwd] {name} k={k}", flush=True)
+    cbt = torch.ones(3, dtype=torch.float64) if cb is None else torch.tensor(cb, dtype=torch.float64)
+    if cb is not None:
+        bg = torch.tensor([float(bg[0]), *cb], device="cuda")
+    print(f"[bwd] {name} k={k} cb={cb}", flush=True)
     g = torch.Generator().manual_seed(7)
     R = torch.randn(cfg.H, cfg.W, 3, generator=g)
     img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
@@ -126,7 +132,7 @@ def test_splat_bwd_param_grads(name, k):
     gwb = gwb.sum()
     gP = kernels.geom_bwd(P.cuda(), camera, grad9).cpu()
     Pr = P.clone().requires_grad_(True)
-    ref = osplat.render_binned(Pr, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
+    ref = osplat.render_binned(Pr, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins, c_b=cbt)
     (ref * R).sum().backward()
     for gname, sl in GROUPS.items():
         e = rel_l2(gP[:, sl], Pr.grad[:, sl])
@@ -135,7 +141,7 @@ def test_splat_bwd_param_grads(name, k):
     # dL/dw_b: autograd through the oracle with w_b as a leaf
     wb = torch.tensor(float(bg[0]), dtype=torch.float64, requires_grad=True)
     th, col, oc, _, _ = osplat.operands(P.double(), cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
-    C, _ = osplat.splat_tiles(th, col, oc, tmap.Phi.double(), wb, torch.ones(3, dtype=torch.float64))
+    C, _ = osplat.splat_tiles(th, col, oc, tmap.Phi.double(), wb, cbt)
     (osplat.tiles_to_image(C, tmap) * R.double()).sum().backward()
     assert abs(float(gwb) - float(wb.grad)) <= 1e-3 * abs(float(wb.grad)) + 1e-4
 
@@ -215,6 +221,39 @@ def test_backward_is_deterministic():
         gslot = kernels.splat_bwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k, img, den, R)
         outs.append(kernels.geom_bwd(P.cuda(), camera, kernels.slot_reduce(gslot, setup.inv)))
     assert torch.equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("name,variant", [("c1_ref", "tile"), ("c1", "tile"), ("c1_ref", "rec"),
+                                          ("c1_ref", "mx"), ("c1_ref", "mx_bf16")])
+def test_splat_fwd_coloured_background(name, variant):
+    """A background colour whose channels differ (a random-background training step's draw,
+    tools/resident_traced.py:671-674): every forward kernel -- the 16x16 walk from proj and from
+    slot records, the 32x32 kernel, the matrix-core forward in both modes -- puts w_b c_b[c]
+    into channel c's numerator."""
+    cfg, P, cam, camera, proj, idx, valid, bg, bins, tmap, k = setup(name)
+    bg = torch.tensor([float(bg[0]), *CB], device="cuda")
+    print(f"[fwd-bg] {name} {variant}", flush=True)
+    if variant == "tile":
+        img, den = kernels.splat_fwd(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k)
+    elif variant == "rec":
+        order = torch.empty(tmap.T, dtype=torch.int32, device="cuda")
+        slot_rec = torch.empty(tmap.T, cfg.K, 12, device="cuda")
+        pos = torch.empty(tmap.T, dtype=torch.int32, device="cuda")
+        inv = torch.empty(cfg.G, 9, dtype=torch.int32, device="cuda")
+        kernels.geom_fwd_assign_bins(P.cuda(), camera, cfg.H, cfg.W, cfg.S, cfg.K, cfg.span,
+                                     inv=inv, order=order, slot_rec=slot_rec, pos_count=pos)
+        img, den = kernels.splat_fwd_rec(slot_rec, pos, order, bg, cfg.H, cfg.W, cfg.S, k)
+    else:
+        img, den = kernels.splat_fwd_mx(proj, idx, valid, bg, cfg.H, cfg.W, cfg.S, k,
+                                        bf16=variant == "mx_bf16")
+    ref = osplat.render_binned(P, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins,
+                               c_b=torch.tensor(CB))
+    tol = 1e-2 if variant == "mx_bf16" else 1e-4
+    err = max_abs(img, ref)
+    print(f"[fwd-bg] {name} {variant} max|err|={err:.3e}")
+    assert err <= tol
+    white = osplat.render_binned(P, cam_dict(cam), tmap, K=cfg.K, k=k, bins=bins)
+    assert max_abs(white, ref) > 10 * tol          # the background colour shows
 
 
 @pytest.mark.parametrize("name,bf16", [("c1_ref", False), ("c3", False), ("c4", False),
