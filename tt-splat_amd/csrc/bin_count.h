@@ -5,6 +5,8 @@
 // tools/m4_train_binned.py:85-86 exactly.
 #pragma once
 
+#include <atomic>
+
 #include "tts_common.h"
 
 namespace tts {
@@ -239,6 +241,28 @@ __device__ __forceinline__ void count_body(const float (&mx)[PER], const float (
 // cell_slot as k_bin_count.  geom_fwd_count_lds: its dynamic LDS request in bytes; callers fall
 // back to the two-kernel path when that exceeds kMaxLdsBytes (one workgroup's LDS on gfx950).
 constexpr size_t kMaxLdsBytes = 160 * 1024;
+
+// A kernel's dynamic-LDS limit (per function and device) raised to kMaxLdsBytes once per device:
+// the largest any call can ask for, so that callers on several host threads or streams never
+// lower it under one another (setting each call's own size would race).  One LdsLimit per
+// kernel instance; the first call on a device should not be under graph capture.
+constexpr int kLdsDevices = 64;
+struct LdsLimit {
+  std::atomic<int> ready[kLdsDevices] = {};
+};
+inline int raise_lds_limit(const void* fn, LdsLimit& lim) {
+  int dev = 0;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return static_cast<int>(de);
+  if (dev < 0 || dev >= kLdsDevices) return TTS_EINVAL;
+  if (!lim.ready[dev].load()) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             static_cast<int>(kMaxLdsBytes));
+    if (e != hipSuccess) return static_cast<int>(e);
+    lim.ready[dev].store(1);
+  }
+  return 0;
+}
 size_t geom_fwd_count_lds(int NB, int Tpad);
 int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degree,
                           const float* depth_bt, int G, const float* camera, float near_z,

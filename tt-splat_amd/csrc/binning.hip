@@ -1293,12 +1293,12 @@ static int bin_run(const float* mu2d, int mu_stride, const uint8_t* keep, int ke
     const bool small = ws.cblock == CountSmall::kBlock;
     const size_t lds =
         sizeof(int) * (size_t)(Tpad + (small ? CountSmall::kWaves : CountLarge::kWaves) * NB);
-    const void* fn = small ? reinterpret_cast<const void*>(&k_bin_count<256, 2>)
-                           : reinterpret_cast<const void*>(&k_bin_count<1024, 4>);
+    static LdsLimit lim[2];
     if (lds > 65536) {
-      const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               static_cast<int>(lds));
-      if (e != hipSuccess) return static_cast<int>(e);
+      const void* fn = small ? reinterpret_cast<const void*>(&k_bin_count<256, 2>)
+                             : reinterpret_cast<const void*>(&k_bin_count<1024, 4>);
+      const int e = raise_lds_limit(fn, lim[small ? 0 : 1]);
+      if (e) return e;
     }
     if (small)
       k_bin_count<256, 2><<<nblk, 256, lds, stream>>>(mu2d, mu_stride, keep, keep_stride, G, ntx,

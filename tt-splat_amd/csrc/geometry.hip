@@ -1205,12 +1205,12 @@ int launch_geom_fwd_count(const float* params, const float* sh_rest, int sh_degr
   const size_t lds = geom_fwd_count_lds(NB, Tpad);
   if (lds > kMaxLdsBytes) return TTS_EINVAL;  // callers check first and take the two-kernel path
   const bool sh = sh_degree > 0;
-  const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count<true>)
-                      : reinterpret_cast<const void*>(&k_geom_fwd_count<false>);
+  static LdsLimit lim[2];
   if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(lds));
-    if (e != hipSuccess) return static_cast<int>(e);
+    const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count<true>)
+                        : reinterpret_cast<const void*>(&k_geom_fwd_count<false>);
+    const int e = raise_lds_limit(fn, lim[sh ? 1 : 0]);
+    if (e) return e;
   }
   if (sh)
     k_geom_fwd_count<true><<<nblk, 512, lds, stream>>>(
@@ -1238,12 +1238,12 @@ int launch_geom_fwd_count_large(const float* params, const float* sh_rest, int s
   const size_t lds = geom_fwd_count_large_lds(NB, Tpad);
   if (lds > kMaxLdsBytes) return TTS_EINVAL;  // callers check first and take the two-kernel path
   const bool sh = sh_degree > 0;
-  const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count_large<true>)
-                      : reinterpret_cast<const void*>(&k_geom_fwd_count_large<false>);
+  static LdsLimit lim[2];
   if (lds > 65536) {
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             static_cast<int>(lds));
-    if (e != hipSuccess) return static_cast<int>(e);
+    const void* fn = sh ? reinterpret_cast<const void*>(&k_geom_fwd_count_large<true>)
+                        : reinterpret_cast<const void*>(&k_geom_fwd_count_large<false>);
+    const int e = raise_lds_limit(fn, lim[sh ? 1 : 0]);
+    if (e) return e;
   }
   if (sh)
     k_geom_fwd_count_large<true><<<nblk, 1024, lds, stream>>>(
@@ -1270,22 +1270,10 @@ int launch_geom_seam(float* params, int G, const float* cam_b, const float* cam_
   const int nblk = (G + CountFused::kBlock - 1) / CountFused::kBlock;
   const size_t lds = geom_seam_lds(NB, Tpad);
   if (lds > kMaxLdsBytes) return TTS_EINVAL;
-  // the kernel's dynamic-LDS limit, raised once per device to the most it can ask for (the
-  // first call on a device should not be under graph capture: TrainStep makes one before it
-  // captures)
-  constexpr int kDevices = 64;
-  static std::atomic<int> lds_ready[kDevices] = {};
-  int dev = 0;
-  const hipError_t de = hipGetDevice(&dev);
-  if (de != hipSuccess) return static_cast<int>(de);
-  if (dev < 0 || dev >= kDevices) return TTS_EINVAL;
-  if (!lds_ready[dev].load()) {
-    const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_geom_bwd_adam_fwd_count),
-        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kMaxLdsBytes));
-    if (e != hipSuccess) return static_cast<int>(e);
-    lds_ready[dev].store(1);
-  }
+  // its staging always passes 64 KB (TrainStep makes one call before it captures)
+  static LdsLimit lim;
+  const int le = raise_lds_limit(reinterpret_cast<const void*>(&k_geom_bwd_adam_fwd_count), lim);
+  if (le) return le;
   k_geom_bwd_adam_fwd_count<<<nblk, 512, lds, stream>>>(
       params, G, cam_b, cam_f, near_z, blur, gslot, inv, gparams, m, v, lr, step, b1, b2, eps,
       proj, keep, ntx, nty, S, span, NB, Tpad, mat, cell_slot);
