@@ -3,7 +3,10 @@
  *
  * Every entry point takes device pointers allocated by the caller, plain sizes and a
  * hipStream_t; it only enqueues work on that stream (no allocation, no synchronisation),
- * so every call can be captured into a hipGraph.  Return value: 0 on success, a negative
+ * so every call can be captured into a hipGraph.  (A kernel that needs more than 64 KB of LDS --
+ * the step seam always, the binning's count pass on grids whose count histogram passes 64 KB --
+ * raises its limit once per device with hipFuncSetAttribute on its first call: make that first
+ * call outside stream capture.)  Return value: 0 on success, a negative
  * TTS_E* domain code for bad arguments (nothing is launched), or a positive hipError_t from
  * the launch.  tts_strerror() names a code.
  *
