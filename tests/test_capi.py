@@ -139,3 +139,10 @@ def test_every_compute_entry_point_rejects_null_pointers(lib):
         for ival in (16, 1):
             rc = getattr(lib, name)(*_null_args(argtypes, ival))
             assert rc in (-1, -2), (name, ival, rc)
+
+
+def test_slot_scatter_checks_sizes_in_64_bits(lib):
+    """T * K past 2^31 with NULL buffers: refused before launch (a 32-bit product would wrap
+    negative and skip the pointer checks)."""
+    assert lib.tts_slot_scatter(None, None, None, 70000, 40000, None, None) == -1
+    assert lib.tts_slot_scatter(None, None, None, 0, 40000, None, None) == 0

@@ -1538,8 +1538,9 @@ int tts_slot_reduce(const float* gslot, const int32_t* inv, int G, float* grad9,
 
 int tts_slot_scatter(const float* gslot, const int32_t* idx, const uint8_t* valid, int T, int K,
                      float* grad9, hipStream_t stream) {
-  if (T < 0 || K < 0 || (T * K > 0 && (!gslot || !idx || !valid || !grad9))) return TTS_EINVAL;
-  const int64_t TK = (int64_t)T * K;
+  if (T < 0 || K < 0) return TTS_EINVAL;
+  const int64_t TK = (int64_t)T * K;   // in 64 bits: a 32-bit product could wrap past the checks
+  if (TK > 0 && (!gslot || !idx || !valid || !grad9)) return TTS_EINVAL;
   if (TK == 0) return TTS_OK;
   k_slot_scatter<<<grid1d(TK, 256), 256, 0, stream>>>(gslot, idx, valid, TK, grad9);
   return launch_status();
